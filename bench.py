@@ -1,0 +1,270 @@
+"""Benchmark of SemBlend's KV-reuse path on one MI355X at the Qwen2.5-7B shape.
+
+One step is one pass of the path over synthetic inputs resident in HBM:
+
+  rope       RoPE delta correction of donor K in place: K [28, 4, 8192, 128] bf16, theta 1e6,
+             delta constant per 256-token chunk, uniform in [-2048, 2048]
+             (rope_correct_k semantics; four rotating copies so the 256 MB Infinity Cache
+             cannot hold the 235 MB tensor between visits);
+  scatter    donor-KV scatter into paged caches for 28 layers in one launch: per layer cache
+             [2048, 2, 4, 16, 128] bf16, donor [2, 4, 16384, 128]; 64 donor 256-token chunks
+             reused in shuffled order, minus 2458 recomputed positions -> 13926 pairs;
+  attention  GQA partial-prefill attention, 28 q heads / 4 KV heads, head_dim 128, bf16, over a
+             16384-token paged context; 2458 recompute rows (first 256 tokens, two random
+             256-token chunks, the rest scattered).
+
+The reported ``value`` is the attention phase's throughput in TFLOP/s (useful causal FLOPs
+4 * D * Hq * sum(p + 1)); the scatter and RoPE phases are reported in GB/s of useful bytes
+(each moved row read once and written once). Every phase is timed with HIP events on the
+stream its kernels run on; ``ms_per_step`` is the sum of the three phase times.
+The CPU baseline times the oracle (a restatement of the reference's CPU path) on a bounded
+sample of the same workload on the host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2516.6   # MI355X dense bf16 MFMA, TFLOP/s
+
+L, HKV, HQ, D, BS = 28, 4, 28, 128, 16
+CTX, N_RECOMPUTE, CHUNK = 16384, 2458, 256
+ROPE_TOKENS, ROPE_BASE = 8192, 1e6
+POOL_BLOCKS = 2048
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def recompute_positions(g: torch.Generator) -> torch.Tensor:
+    """First 256 tokens + two random whole chunks + uniform scatter, 2458 in total."""
+    n_chunks = CTX // CHUNK
+    mask = torch.zeros(CTX, dtype=torch.bool)
+    mask[:CHUNK] = True
+    for c in (torch.randperm(n_chunks - 1, generator=g)[:2] + 1).tolist():
+        mask[c * CHUNK:(c + 1) * CHUNK] = True
+    rest = (~mask).nonzero().flatten()
+    mask[rest[torch.randperm(rest.numel(), generator=g)[:N_RECOMPUTE - int(mask.sum())]]] = True
+    return mask.nonzero().flatten().to(torch.int32)
+
+
+def build_inputs(dev: torch.device):
+    g = torch.Generator("cpu").manual_seed(0)
+    gd = torch.Generator(dev).manual_seed(0)
+    inp = {}
+    # rope: four rotating copies of K
+    inp["rope_k"] = [torch.randn((L, HKV, ROPE_TOKENS, D), generator=gd, device=dev,
+                                 dtype=torch.bfloat16) for _ in range(4)]
+    deltas = torch.randint(-2048, 2049, (ROPE_TOKENS // CHUNK,), generator=g)
+    d = torch.arange(ROPE_TOKENS)
+    inp["rope_d"] = d.to(torch.int32).to(dev)
+    inp["rope_t"] = (d + deltas[d // CHUNK]).to(torch.int32).to(dev)
+    # scatter: 28 layers
+    pos_r = recompute_positions(g)
+    perm = torch.randperm(CTX // CHUNK, generator=g)
+    t = torch.arange(CTX)
+    dpos = perm[t // CHUNK] * CHUNK + t % CHUNK
+    keep = torch.ones(CTX, dtype=torch.bool)
+    keep[pos_r.long()] = False
+    inp["sc_d"] = dpos[keep].to(torch.int32).to(dev)
+    inp["sc_t"] = t[keep].to(torch.int32).to(dev)
+    inp["block_table"] = torch.randperm(POOL_BLOCKS, generator=g)[:CTX // BS].to(torch.int32).to(dev)
+    inp["caches"] = [torch.zeros((POOL_BLOCKS, 2, HKV, BS, D), dtype=torch.bfloat16, device=dev)
+                     for _ in range(L)]
+    inp["donors"] = [torch.randn((2, HKV, CTX, D), generator=gd, device=dev, dtype=torch.bfloat16)
+                     for _ in range(L)]
+    # attention over the first layer's cache, fully populated
+    kv = inp["caches"][0]
+    kv.normal_(generator=gd)
+    inp["attn_kv"] = kv
+    inp["attn_pos"] = pos_r.to(dev)
+    inp["attn_q"] = torch.randn((pos_r.shape[0], HQ, D), generator=gd, device=dev,
+                                dtype=torch.bfloat16)
+    inp["pos_cpu"] = pos_r
+    return inp
+
+
+def cpu_baseline(inp, budget_s: float = 20.0) -> dict:
+    """Oracle (reference CPU path restated) on a bounded sample, on the host's cores."""
+    from oracle import ref_cpu as ref
+
+    torch.set_num_threads(max(1, torch.get_num_threads()))
+    cores = torch.get_num_threads()
+    g = torch.Generator("cpu").manual_seed(1)
+    kv = inp["attn_kv"].cpu()
+    bt = inp["block_table"].cpu()
+    pos = inp["pos_cpu"]
+    q = inp["attn_q"].cpu()
+    n_sample = 256
+    rows = torch.randperm(pos.shape[0], generator=g)[:n_sample].sort().values
+    flops = 4.0 * D * HQ * float((pos[rows].double() + 1).sum())
+    t0 = time.perf_counter()
+    ref.partial_attention_paged(q[rows], kv, bt, pos[rows])
+    dt = time.perf_counter() - t0
+    out = {
+        "value": flops / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"partial attention, {n_sample} of {pos.shape[0]} recompute rows (random), "
+                  f"28q/4kv x 128, 16384-token paged context, bf16 in / fp32 math; "
+                  f"{dt:.2f} s",
+    }
+    # scatter and RoPE on smaller samples, reported alongside
+    n_pairs = 4096
+    sel = torch.randperm(inp["sc_d"].shape[0], generator=g)[:n_pairs]
+    cache = torch.zeros((POOL_BLOCKS, 2, HKV, BS, D), dtype=torch.bfloat16)
+    donor = inp["donors"][0].cpu()
+    t0 = time.perf_counter()
+    ref.scatter_donor_kv_paged(cache, donor, bt, inp["sc_d"].cpu()[sel], inp["sc_t"].cpu()[sel])
+    dt_s = time.perf_counter() - t0
+    out["scatter_gbps"] = n_pairs * 2 * HKV * D * 2 * 2 / dt_s / 1e9
+    n_tok = 2048
+    k = inp["rope_k"][0][:, :, :n_tok].cpu()
+    t0 = time.perf_counter()
+    ref.rope_correct_k(k, inp["rope_d"].cpu()[:n_tok], inp["rope_t"].cpu()[:n_tok], head_dim=D,
+                       rope_base=ROPE_BASE)
+    dt_r = time.perf_counter() - t0
+    out["rope_gbps"] = k.numel() * 2 * 2 / dt_r / 1e9
+    out["sample"] += (f"; scatter {n_pairs} pairs x 1 layer {dt_s:.2f} s; "
+                      f"rope {n_tok} tokens x 28 layers x 4 heads {dt_r:.2f} s")
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(each GPU would own its own layers or KV heads with no exchange). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    from semblend_amd import rope_correction as rc
+    from semblend_amd import triton_kernels as tk
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log("building inputs")
+    inp = build_inputs(dev)
+    torch.cuda.synchronize()
+
+    pos = inp["pos_cpu"].double()
+    attn_flops = 4.0 * D * HQ * float((pos + 1).sum())
+    n_pairs = inp["sc_d"].shape[0]
+    scatter_bytes = float(n_pairs) * L * 2 * HKV * D * 2 * 2
+    rope_bytes = float(L * HKV * ROPE_TOKENS * D * 2 * 2)
+
+    def phase_rope(i):
+        rc.rope_correct_k_inplace(inp["rope_k"][i % 4], inp["rope_d"], inp["rope_t"],
+                                  head_dim=D, rope_base=ROPE_BASE)
+
+    def phase_scatter(i):
+        tk.scatter_donor_kv_paged_layers(inp["caches"], inp["donors"], inp["block_table"],
+                                         inp["sc_d"], inp["sc_t"])
+
+    def phase_attn(i):
+        tk.partial_prefill_attention_paged(inp["attn_q"], inp["attn_kv"], inp["block_table"],
+                                           inp["attn_pos"], out=inp.setdefault(
+                                               "attn_out", torch.empty_like(inp["attn_q"])))
+
+    phases = [("rope", phase_rope), ("scatter", phase_scatter), ("attention", phase_attn)]
+    log(f"warmup {args.warmup}")
+    for i in range(args.warmup):
+        for _, fn in phases:
+            fn(i)
+    torch.cuda.synchronize()
+
+    log(f"timing {args.steps} steps")
+    ev = {name: [] for name, _ in phases}
+    t_wall0 = time.perf_counter()
+    for i in range(args.steps):
+        for name, fn in phases:
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn(i)
+            e1.record()
+            ev[name].append((e0, e1))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall0
+    ms = {name: [a.elapsed_time(b) for a, b in pairs] for name, pairs in ev.items()}
+    med = {name: sorted(v)[len(v) // 2] for name, v in ms.items()}
+    avg = {name: sum(v) / len(v) for name, v in ms.items()}
+    ms_per_step = sum(avg.values())
+
+    attn_tflops = attn_flops / (avg["attention"] * 1e-3) / 1e12
+    scatter_gbps = scatter_bytes / (avg["scatter"] * 1e-3) / 1e9
+    rope_gbps = rope_bytes / (avg["rope"] * 1e-3) / 1e9
+    log(f"attention {avg['attention']:.3f} ms ({attn_tflops:.1f} TFLOP/s), "
+        f"scatter {avg['scatter']:.3f} ms ({scatter_gbps:.0f} GB/s), "
+        f"rope {avg['rope']:.3f} ms ({rope_gbps:.0f} GB/s), wall {wall:.3f} s")
+
+    result = {
+        "metric": "partial-attn TFLOP/s + scatter/RoPE GB/s @7B GQA 16K ctx; % of roofline",
+        "value": round(attn_tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "Qwen2.5-7B KV reuse, 16K context: partial attention 28q/4kv x 128 "
+                        "over 16384 paged tokens, |R|=2458; scatter 28 layers x 13926 pairs; "
+                        "RoPE K[28,4,8192,128] theta 1e6",
+            "attention_rows": int(inp["pos_cpu"].shape[0]),
+            "attention_flops": attn_flops,
+            "scatter_pairs": int(n_pairs),
+            "scatter_bytes": scatter_bytes,
+            "rope_bytes": rope_bytes,
+            "block_size": BS,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(attn_tflops, 2),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+        },
+        "phases": {
+            "attention": {"ms": round(avg["attention"], 4), "ms_median": round(med["attention"], 4),
+                          "tflops": round(attn_tflops, 2),
+                          "frac_of_peak": round(attn_tflops / BF16_PEAK_TFLOPS, 4)},
+            "scatter": {"ms": round(avg["scatter"], 4), "ms_median": round(med["scatter"], 4),
+                        "gbps": round(scatter_gbps, 1),
+                        "frac_of_peak": round(scatter_gbps / HBM_PEAK_GBS, 4)},
+            "rope": {"ms": round(avg["rope"], 4), "ms_median": round(med["rope"], 4),
+                     "gbps": round(rope_gbps, 1),
+                     "frac_of_peak": round(rope_gbps / HBM_PEAK_GBS, 4)},
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle on host cores)")
+        result["cpu_baseline"] = cpu_baseline(inp)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

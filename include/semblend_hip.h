@@ -1,0 +1,211 @@
+/*
+ * semblend_hip.h — C ABI of libsemblend_hip.so, the MI355X (gfx950) kernel library
+ * behind SemBlend's KV-reuse path: donor-KV scatter into a paged cache, RoPE delta
+ * correction of donor K, and partial-prefill attention.
+ *
+ * Conventions shared by every entry point
+ *   - All tensor arguments are device pointers owned by the caller. The library never
+ *     allocates: any workspace is passed in by the caller, sized as documented.
+ *   - Strides are in ELEMENTS (not bytes) and are passed as host arrays of int64_t, so the
+ *     standard [num_blocks, 2, heads, block_size, head_dim] cache, vLLM's flash-attn
+ *     [2, num_blocks, block_size, heads, head_dim] cache and TRT-LLM's
+ *     [num_blocks, 2, block_size, heads, head_dim] cache are all addressed without copies.
+ *   - Index arrays (positions, block tables) are int32 device arrays.
+ *   - dtype is one of SB_DTYPE_*; RoPE and attention arithmetic is fp32.
+ *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream); work is
+ *     enqueued asynchronously and the call never synchronises the device.
+ *   - Return value: SB_OK (0), SB_ERR_INVALID_ARGUMENT, or a hipError_t value from the
+ *     launch. sb_last_error_string() describes the last failure on the calling thread.
+ *   - Out-of-range pairs (donor position >= donor length, logical block beyond the block
+ *     table, physical block >= pool size, negative positions) are skipped silently, as the
+ *     reference's GPU kernels skip them.
+ */
+#ifndef SEMBLEND_HIP_H
+#define SEMBLEND_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SB_OK 0
+#define SB_ERR_INVALID_ARGUMENT 100001
+
+#define SB_DTYPE_F32 0
+#define SB_DTYPE_F16 1
+#define SB_DTYPE_BF16 2
+
+/* Library version string, e.g. "semblend_hip 0.1.0 gfx950". */
+const char* sb_version(void);
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char* sb_last_error_string(void);
+
+/* ------------------------------------------------------------------------------------------
+ * Donor-KV scatter
+ * ---------------------------------------------------------------------------------------- */
+
+/* Flat scatter over all layers:
+ *   target[l, kv, h, t, :] = donor[l, kv, h, d, :] for every pair (d, t).
+ * target [L, 2, H, St, D] with strides t_strides[5]; donor [L, 2, H, Sd, D] with d_strides[5].
+ * Replaces semblend_core/triton_kernels.py:132-191 (scatter_donor_kv, kernel :59-129). */
+int sb_scatter_donor_kv(void* target, const void* donor, const int32_t* donor_pos,
+                        const int32_t* target_pos, int64_t num_pairs, int64_t num_layers,
+                        int64_t num_heads, int64_t head_dim, int64_t target_seq_len,
+                        int64_t donor_seq_len, const int64_t* t_strides,
+                        const int64_t* d_strides, int32_t dtype, void* stream);
+
+/* Paged scatter, one layer:
+ *   kv_cache[bt[t / bs], kv, h, t % bs, :] = donor_kv[kv, h, d, :].
+ * kv_cache [NB, 2, H, bs, D] addressed by kv_strides[5] = (block, kv, head, pos, dim);
+ * donor_kv [2, H, Sd, D] addressed by d_strides[4].
+ * Replaces semblend_core/triton_kernels.py:279-356 (scatter_donor_kv_paged, kernel :200-276). */
+int sb_scatter_donor_kv_paged(void* kv_cache, const void* donor_kv, const int32_t* block_table,
+                              const int32_t* donor_pos, const int32_t* target_pos,
+                              int64_t num_pairs, int64_t num_heads, int64_t block_size,
+                              int64_t head_dim, int64_t donor_seq_len, int64_t num_blocks_total,
+                              int64_t num_blocks_per_seq, const int64_t* kv_strides,
+                              const int64_t* d_strides, int32_t dtype, void* stream);
+
+/* Paged scatter over several layers in one launch. kv_layer_ptrs / donor_layer_ptrs are
+ * DEVICE arrays of num_layers base addresses (uint64); every layer shares the strides.
+ * No reference counterpart: it replaces the per-layer loop of callers such as
+ * synapse_kv_connector/model_runner_hook.py:215-276. */
+int sb_scatter_donor_kv_paged_layers(const uint64_t* kv_layer_ptrs,
+                                     const uint64_t* donor_layer_ptrs, int64_t num_layers,
+                                     const int32_t* block_table, const int32_t* donor_pos,
+                                     const int32_t* target_pos, int64_t num_pairs,
+                                     int64_t num_heads, int64_t block_size, int64_t head_dim,
+                                     int64_t donor_seq_len, int64_t num_blocks_total,
+                                     int64_t num_blocks_per_seq, const int64_t* kv_strides,
+                                     const int64_t* d_strides, int32_t dtype, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * RoPE delta correction (interleaved pairs (2i, 2i+1); inv_freq is a device fp32 array of
+ * head_dim/2 entries, 1 / base^(2i/head_dim))
+ * ---------------------------------------------------------------------------------------- */
+
+/* Fused scatter + RoPE: V copied; K rotated by (t - d) and rounded once to the cache dtype.
+ * Same arguments as sb_scatter_donor_kv_paged plus inv_freq.
+ * Replaces semblend_core/rope_correction.py:193-282 (kernel :66-190, CPU path :285-328). */
+int sb_rope_correct_scatter_paged(void* kv_cache, const void* donor_kv,
+                                  const int32_t* block_table, const int32_t* donor_pos,
+                                  const int32_t* target_pos, const float* inv_freq,
+                                  int64_t num_pairs, int64_t num_heads, int64_t block_size,
+                                  int64_t head_dim, int64_t donor_seq_len,
+                                  int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                                  const int64_t* kv_strides, const int64_t* d_strides,
+                                  int32_t dtype, void* stream);
+
+/* Multi-layer form of sb_rope_correct_scatter_paged (device arrays of layer base addresses,
+ * as in sb_scatter_donor_kv_paged_layers). cos/sin are computed once per pair and shared by
+ * every layer and head. No reference counterpart (replaces a per-layer caller loop, e.g.
+ * semblend/integration/trtllm/pytorch_backend.py:106-154). */
+int sb_rope_correct_scatter_paged_layers(const uint64_t* kv_layer_ptrs,
+                                         const uint64_t* donor_layer_ptrs, int64_t num_layers,
+                                         const int32_t* block_table, const int32_t* donor_pos,
+                                         const int32_t* target_pos, const float* inv_freq,
+                                         int64_t num_pairs, int64_t num_heads,
+                                         int64_t block_size, int64_t head_dim,
+                                         int64_t donor_seq_len, int64_t num_blocks_total,
+                                         int64_t num_blocks_per_seq, const int64_t* kv_strides,
+                                         const int64_t* d_strides, int32_t dtype, void* stream);
+
+/* Flat RoPE correction over k [L, H, S, D] (k_strides[4]; pass L = 1 for [H, S, D]):
+ * for each pair i in order, the row at donor position d_i is rotated by (t_i - d_i) and
+ * rounded to dtype; rows hit by several pairs are rotated once per pair, in pair order.
+ * out may equal k (in place); when out != k, rows no pair touches are copied unchanged.
+ * workspace: device int32 array of 2 * S entries (scratch for the per-row pair index).
+ * Replaces semblend_core/rope_correction.py:336-399 (rope_correct_k). */
+int sb_rope_correct_k(void* out, const void* k, const int32_t* donor_pos,
+                      const int32_t* target_pos, const float* inv_freq, int32_t* workspace,
+                      int64_t num_pairs, int64_t num_layers, int64_t num_heads, int64_t seq_len,
+                      int64_t head_dim, const int64_t* out_strides, const int64_t* k_strides,
+                      int32_t dtype, void* stream);
+
+/* In-place rotation of K rows in a paged cache by one delta:
+ *   K[bt[p / bs], h, p % bs, :] = R(delta) K[...], applied repeat[i] times (rounded to dtype
+ *   after each application) for positions[i]. repeat may be NULL (once each).
+ * k_plane points at the K plane; k_strides[4] = (block, head, pos, dim), so both the
+ * [NB, 2, H, bs, D] and the vLLM [2, NB, bs, H, D] layouts are addressed.
+ * Replaces semblend_core/rope_correction.py:699-783 (apply_rope_delta_inplace). */
+int sb_apply_rope_delta_inplace(void* k_plane, const int32_t* block_table,
+                                const int32_t* positions, const int32_t* repeat,
+                                int64_t num_positions, int64_t delta, const float* inv_freq,
+                                int64_t num_heads, int64_t block_size, int64_t head_dim,
+                                int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                                const int64_t* k_strides, int32_t dtype, void* stream);
+
+/* Permutation inside a paged cache with snapshot semantics: every source row (K and V) is
+ * read before any target row is written; V is copied, K rotated by (tgt - src).
+ * workspace: device buffer of num_pairs * 2 * H * D elements of dtype.
+ * Replaces semblend_core/rope_correction.py:407-476 (permute_paged_kv_with_rope). */
+int sb_permute_paged_kv_with_rope(void* kv_cache, const int32_t* block_table,
+                                  const int32_t* src_pos, const int32_t* tgt_pos,
+                                  const float* inv_freq, void* workspace, int64_t num_pairs,
+                                  int64_t num_heads, int64_t block_size, int64_t head_dim,
+                                  int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                                  const int64_t* kv_strides, int32_t dtype, void* stream);
+
+/* NoPE two-step permutation: K at each target = R(tgt) R(-src) K_snapshot(src) (two fp32
+ * rotations, one rounding); V rows copied from v_src_pos to v_tgt_pos after a snapshot.
+ * The host resolves the reference's sequential V copies into (v_src, v_tgt) pairs.
+ * workspace: device buffer of (num_pairs + num_v_pairs) * H * D elements of dtype.
+ * Replaces semblend_core/rope_correction.py:599-697 (kernel :496-596, CPU path :786-823). */
+int sb_nope_permute_paged_kv(void* kv_cache, const int32_t* block_table,
+                             const int32_t* src_pos, const int32_t* tgt_pos, int64_t num_pairs,
+                             const int32_t* v_src_pos, const int32_t* v_tgt_pos,
+                             int64_t num_v_pairs, const float* inv_freq, void* workspace,
+                             int64_t num_heads, int64_t block_size, int64_t head_dim,
+                             int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                             const int64_t* kv_strides, int32_t dtype, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Partial-prefill attention (causal; row at position p attends to keys 0..p)
+ * ---------------------------------------------------------------------------------------- */
+
+/* Dense drop-in: out[h, i, :] = softmax(scale * q[h, i] . k[h, :i+1]) v[h, :i+1] for every i
+ * with compute_mask[i] != 0, and 0 elsewhere. q, k, v, out are [H, S, D] with strides
+ * (head, seq, dim) given in q_strides[3], k_strides[3], v_strides[3] and o_strides[3].
+ * compute_mask: device uint8 array of S entries. The rows are compacted on the device, so the
+ * call never synchronises with the host. Rows whose mask is 0 are written as zeros.
+ * workspace: device buffer of sb_partial_prefill_attention_workspace_size(...) bytes.
+ * Replaces semblend_core/triton_kernels.py:655-734 (kernel :531-652, CPU path :717-732). */
+int64_t sb_partial_prefill_attention_workspace_size(int64_t num_heads, int64_t seq_len,
+                                                    int64_t head_dim, int32_t dtype);
+int sb_partial_prefill_attention(void* out, const void* q, const void* k, const void* v,
+                                 const uint8_t* compute_mask, void* workspace,
+                                 int64_t workspace_bytes, int64_t num_heads, int64_t seq_len,
+                                 int64_t head_dim, float scale, const int64_t* q_strides,
+                                 const int64_t* k_strides, const int64_t* v_strides,
+                                 const int64_t* o_strides, int32_t dtype, void* stream);
+
+/* GQA attention over a paged cache for a compact set of query rows:
+ *   out[r, hq, :] = softmax(scale * q[r, hq] . K[hkv, 0..p_r]) V[hkv, 0..p_r],
+ *   hkv = hq / (num_q_heads / num_kv_heads), p_r = positions[r].
+ * q and out are [R, Hq, D] (q_strides[3], o_strides[3] = (row, head, dim));
+ * kv_cache [NB, 2, Hkv, bs, D] with kv_strides[5] = (block, kv, head, pos, dim).
+ * positions should be ascending (any order is correct; ascending is fastest).
+ * workspace: device buffer of sb_partial_attention_paged_workspace_size(...) bytes (fp32
+ * partials of the split key range; the size may be 0, then workspace may be NULL).
+ * No reference counterpart: the reference attention is MHA over contiguous K/V
+ * (semblend_core/triton_kernels.py:655-734); this is the GQA + paged form its callers need. */
+int64_t sb_partial_attention_paged_workspace_size(int64_t num_rows, int64_t num_q_heads,
+                                                  int64_t num_kv_heads, int64_t head_dim,
+                                                  int64_t block_size,
+                                                  int64_t num_blocks_per_seq, int32_t dtype);
+int sb_partial_attention_paged(void* out, const void* q, const void* kv_cache,
+                               const int32_t* block_table, const int32_t* positions,
+                               void* workspace, int64_t workspace_bytes, int64_t num_rows,
+                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                               int64_t block_size, int64_t num_blocks_total,
+                               int64_t num_blocks_per_seq, float scale,
+                               const int64_t* q_strides, const int64_t* o_strides,
+                               const int64_t* kv_strides, int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SEMBLEND_HIP_H */

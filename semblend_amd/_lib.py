@@ -1,0 +1,191 @@
+"""ctypes binding of libsemblend_hip.so (the C ABI declared in include/semblend_hip.h).
+
+The library is loaded after ``import torch`` so that it binds to the HIP runtime torch already
+loaded (both carry the ``libamdhip64.so.7`` soname); device pointers and hipStream_t handles
+from torch are then valid in the library. There is no fallback: if the library is missing or
+fails to load, every kernel entry point raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libsemblend_hip.so"
+
+SB_OK = 0
+SB_ERR_INVALID_ARGUMENT = 100001
+SB_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# Argument signatures of every exported function (order as in include/semblend_hip.h).
+SIGNATURES: dict[str, list] = {
+    "sb_scatter_donor_kv": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p,
+                            _i64p, _i32, _vp],
+    "sb_scatter_donor_kv_paged": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                                  _i64, _i64p, _i64p, _i32, _vp],
+    "sb_scatter_donor_kv_paged_layers": [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                         _i64, _i64, _i64, _i64p, _i64p, _i32, _vp],
+    "sb_rope_correct_scatter_paged": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                      _i64, _i64, _i64, _i64p, _i64p, _i32, _vp],
+    "sb_rope_correct_scatter_paged_layers": [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
+                                             _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i32,
+                                             _vp],
+    "sb_rope_correct_k": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p,
+                          _i64p, _i32, _vp],
+    "sb_apply_rope_delta_inplace": [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
+                                    _i64, _i64, _i64p, _i32, _vp],
+    "sb_permute_paged_kv_with_rope": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                      _i64, _i64, _i64p, _i32, _vp],
+    "sb_nope_permute_paged_kv": [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64,
+                                 _i64, _i64, _i64, _i64, _i64p, _i32, _vp],
+    "sb_partial_prefill_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                     _f32, _i64p, _i64p, _i64p, _i64p, _i32, _vp],
+    "sb_partial_attention_paged": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                   _i64, _i64, _i64, _f32, _i64p, _i64p, _i64p, _i32, _vp],
+}
+
+# Size queries (return int64_t, not a status code).
+SIZE_QUERIES: dict[str, list] = {
+    "sb_partial_prefill_attention_workspace_size": [_i64, _i64, _i64, _i32],
+    "sb_partial_attention_paged_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i64, _i32],
+}
+
+_lib: ctypes.CDLL | None = None
+_load_error: str | None = None
+
+
+def _load() -> ctypes.CDLL:
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        _load_error = (
+            f"{LIB_PATH} is missing; build it with `python -m semblend_amd._build` "
+            "(hipcc, gfx950)"
+        )
+        raise RuntimeError(_load_error)
+    try:
+        lib = ctypes.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+    except OSError as exc:  # pragma: no cover - depends on the runtime image
+        _load_error = f"failed to load {LIB_PATH}: {exc}"
+        raise RuntimeError(_load_error) from exc
+    try:
+        lib.sb_version.restype = ctypes.c_char_p
+        lib.sb_version.argtypes = []
+        lib.sb_last_error_string.restype = ctypes.c_char_p
+        lib.sb_last_error_string.argtypes = []
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = argtypes
+        for name, argtypes in SIZE_QUERIES.items():
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int64
+            fn.argtypes = argtypes
+    except AttributeError as exc:
+        _load_error = (f"{LIB_PATH} does not export the expected C ABI ({exc}); rebuild it "
+                       "with `python -m semblend_amd._build`")
+        raise RuntimeError(_load_error) from exc
+    _lib = lib
+    return lib
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises RuntimeError if it cannot be loaded."""
+    return _load()
+
+
+def available() -> bool:
+    try:
+        _load()
+        return True
+    except RuntimeError:
+        return False
+
+
+def version() -> str:
+    return lib().sb_version().decode()
+
+
+def size_query(name: str, *args) -> int:
+    return int(getattr(lib(), name)(*args))
+
+
+def call(name: str, *args) -> None:
+    """Invoke an entry point and turn a nonzero status into RuntimeError."""
+    rc = getattr(lib(), name)(*args)
+    if rc != SB_OK:
+        msg = lib().sb_last_error_string().decode()
+        kind = "invalid argument" if rc == SB_ERR_INVALID_ARGUMENT else f"hip error {rc}"
+        raise RuntimeError(f"{name} failed ({kind}): {msg}")
+
+
+# ------------------------------------------------------------------------------------------
+# Argument helpers
+# ------------------------------------------------------------------------------------------
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def strides(t: torch.Tensor, dims: tuple[int, ...] | None = None):
+    s = t.stride() if dims is None else tuple(t.stride(d) for d in dims)
+    return (ctypes.c_int64 * len(s))(*s)
+
+
+def i64_array(values) -> ctypes.Array:
+    vals = list(values)
+    return (ctypes.c_int64 * len(vals))(*vals)
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return SB_DTYPE[t.dtype]
+    except KeyError:
+        raise TypeError(
+            f"unsupported dtype {t.dtype}; the HIP kernels take float32, float16 or bfloat16"
+        ) from None
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors must live on one HIP device; CPU tensors are rejected (no CPU path)."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                "semblend_amd runs on MI355X (HIP) device tensors only; got a tensor on "
+                f"{t.device}. Move the KV cache and inputs to the GPU."
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise RuntimeError("no device tensor given")
+    return dev
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def as_index(t, device: torch.device) -> torch.Tensor:
+    """int32 contiguous device copy of an index tensor or sequence (no copy if already so)."""
+    if not isinstance(t, torch.Tensor):
+        t = torch.as_tensor(list(t), dtype=torch.int32)
+    if t.device != device:
+        t = t.to(device)
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    return t.contiguous().reshape(-1)

@@ -1,0 +1,890 @@
+// Partial-prefill attention for gfx950.
+//
+// Semantics (semblend_core/triton_kernels.py:558-652, CPU path :717-732): a query row at
+// position p attends causally to keys 0..p of its KV head:
+//     out = softmax(scale * q . K[0..p]^T) V[0..p]
+// computed with fp32 accumulation and an online (running max / running sum) softmax.
+//
+// MFMA path (bf16 / fp16, head_dim 64 or 128). The query rows of one KV head are flattened
+// as (row, q-head-in-group), so the whole GQA group shares every K/V tile. A workgroup owns
+// 128 flattened rows (4 waves x 32) and one chunk of the key range, walked in tiles of 64
+// keys staged in LDS:
+//   * S^T = K Q^T with v_mfma_f32_32x32x16: K tile rows are the A operand (one ds_read_b128
+//     per lane per 16-wide k-step), Q stays in registers as the B operand. In the S^T
+//     accumulator each lane owns ONE query row and 16 keys, so row max / row sum need only
+//     in-lane work plus one exchange with lane ^ 32.
+//   * O^T += V^T P^T with the same MFMA: P^T comes straight from the S^T accumulators
+//     (after exp2 and conversion) as the B operand; the key order inside each 16-key step is
+//     permuted consistently in both operands, so no cross-lane shuffles are needed. V is
+//     stored transposed in LDS (Vt[d][key]) so each lane reads its 8 keys as two 8-byte words.
+//   * K/V tiles are double-buffered: the global loads of tile i+1 are issued into registers
+//     before tile i is computed and written to the other LDS buffer afterwards, so one
+//     barrier per tile separates the stages. The block-table slice of the chunk is staged in
+//     LDS once, so tile addresses need no dependent global load.
+//   * Online softmax in the log2 domain with a lazily updated reference max: the running
+//     reference only moves (and O is only rescaled) when a row's max grows by more than
+//     2^8, which keeps every p <= 256 and removes almost all rescaling work. O / l is
+//     unchanged by the choice of reference.
+// Load balance: the key range of each row tile is split into chunks of `ksplit` keys. Work
+// items are ordered (chunk ascending, tile descending), so with ascending positions the
+// largest items start first. Tiles that need more than one chunk write unnormalised fp32
+// partials (O, m, l) and a merge kernel combines them (log-sum-exp weights).
+//
+// VALU path (fp32 and any other head_dim): one wave per (row, q-head), a 64-key chunk per
+// step, one key per lane for the scores and the PV sum over the chunk per output dimension.
+
+#include "sb_common.h"
+
+namespace sb {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kTileRows = 128;  // flattened query rows per workgroup
+constexpr int kTileKeys = 64;   // keys per LDS tile
+constexpr int kBtLds = 1024;    // block-table entries staged per chunk
+constexpr float kLazyMax = 8.f; // log2 growth of a row max that forces a rescale
+
+struct AttnArgs {
+  const char* q;        // query rows
+  char* o;              // output rows
+  int64_t q_s_row, q_s_head;  // byte strides; row = position (q_by_position) or compact index
+  int64_t o_s_row, o_s_head;
+  int q_by_position;
+  const int32_t* positions;
+  const int32_t* count_ptr;   // device row count (dense drop-in), or nullptr
+  int64_t num_rows;           // host row count (upper bound when count_ptr != nullptr)
+  const char* k;              // K base (paged: cache + kv stride 0)
+  const char* v;              // V base
+  int64_t k_s_head, v_s_head; // byte strides
+  int64_t k_s_seq, v_s_seq;   // flat only
+  int paged;
+  const int32_t* block_table;
+  int64_t block_size, nb_total, nb_per_seq;
+  int bs_log2;                // log2(block_size) when a power of two, else -1
+  int64_t s_block, s_pos;     // paged byte strides (shared by K and V)
+  int64_t kv_len;             // addressable keys
+  int num_kv_heads;
+  int group;                  // q heads per kv head
+  int head_dim;
+  float scale;
+  float scale_log2;           // scale * log2(e)
+  int ksplit;                 // keys per work item (multiple of kTileKeys)
+  int max_chunks;             // ceil(kv_len / ksplit)
+  int64_t n_tiles;            // row tiles per kv head used for the partial layout
+  float* part_o;              // [Hkv][n_tiles][max_chunks][128][D] fp32, or nullptr
+  float* part_ml;             // [Hkv][n_tiles][max_chunks][128][2] fp32 (m, l)
+};
+
+__device__ __forceinline__ int64_t attn_num_rows(const AttnArgs& a) {
+  return a.count_ptr ? static_cast<int64_t>(*a.count_ptr) : a.num_rows;
+}
+
+__device__ __forceinline__ int clamp_block(const AttnArgs& a, int64_t pb) {
+  return static_cast<int>(pb < 0 ? 0 : (pb >= a.nb_total ? a.nb_total - 1 : pb));
+}
+
+__device__ __forceinline__ const char* key_row(const AttnArgs& a, const char* base,
+                                               int64_t s_head, int64_t s_seq, int64_t key,
+                                               int kvh) {
+  if (a.paged) {
+    const int64_t lb = key / a.block_size;
+    const int pb = clamp_block(a, a.block_table[lb]);
+    return base + pb * a.s_block + kvh * s_head + (key - lb * a.block_size) * a.s_pos;
+  }
+  return base + kvh * s_head + key * s_seq;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+template <int DT> struct Mma;
+template <> struct Mma<SB_DTYPE_BF16> {
+  using vec8 = bf16x8_t;
+  __device__ __forceinline__ static f32x16_t mma(vec8 a, vec8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static vec8 cvt8(const float* f) {
+    vec8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = static_cast<__bf16>(f[e]);
+    return r;
+  }
+  __device__ __forceinline__ static uint16_t cvt1(float f) { return f32_to_bf16(f); }
+};
+template <> struct Mma<SB_DTYPE_F16> {
+  using vec8 = f16x8_t;
+  __device__ __forceinline__ static f32x16_t mma(vec8 a, vec8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static vec8 cvt8(const float* f) {
+    vec8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = static_cast<_Float16>(f[e]);
+    return r;
+  }
+  __device__ __forceinline__ static uint16_t cvt1(float f) { return f32_to_f16(f); }
+};
+
+// Work-item decode shared by the attention and merge kernels.
+struct Item {
+  int kvh;
+  int64_t tile;
+  int chunk;
+};
+
+__device__ __forceinline__ Item decode_item(const AttnArgs& a, int64_t n_tiles_live) {
+  // blockIdx.x = (chunk * n_tiles + tile_rev) * Hkv + kvh; tiles taken in descending order.
+  Item it;
+  const int64_t b = blockIdx.x;
+  it.kvh = static_cast<int>(b % a.num_kv_heads);
+  const int64_t rest = b / a.num_kv_heads;
+  const int64_t tile_rev = rest % a.n_tiles;
+  it.chunk = static_cast<int>(rest / a.n_tiles);
+  it.tile = n_tiles_live - 1 - tile_rev;
+  return it;
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnArgs a) {
+  using M = Mma<DT>;
+  using vec8 = typename M::vec8;
+  constexpr int KSTR = D + 8;          // K tile row stride (elements)
+  constexpr int VSTR = kTileKeys + 4;  // transposed V row stride (elements)
+  constexpr int NKS = D / 16;          // QK^T k-steps
+  constexpr int NDT = D / 32;          // PV output d-tiles
+  constexpr int CH = D / 8;            // 16-byte chunks per row
+  constexpr int KLD = kTileKeys * CH / 256;  // K vectors loaded per thread per tile
+  constexpr int VLD = CH / 8;                // V key-pair passes per thread per tile
+  __shared__ __align__(16) uint16_t Ks[2][kTileKeys * KSTR];
+  __shared__ __align__(16) uint16_t Vt[2][D * VSTR];
+  __shared__ int bt_s[kBtLds];
+  __shared__ int red_max[4];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int lq = lane & 31;
+  const int lg = lane >> 5;
+
+  const int64_t n_rows = attn_num_rows(a);
+  const int64_t rows_kv = n_rows * a.group;
+  const int64_t n_tiles_live = (rows_kv + kTileRows - 1) / kTileRows;
+  const Item item = decode_item(a, n_tiles_live);
+  if (item.tile < 0 || item.chunk >= a.max_chunks) return;  // uniform, before any barrier
+  const int kvh = item.kvh;
+
+  // This lane's query row.
+  const int row_in_tile = wave * 32 + lq;
+  const int64_t r = item.tile * kTileRows + row_in_tile;
+  int p = -1;
+  int64_t qrow = 0;
+  int qh = 0;
+  if (r < rows_kv) {
+    const int64_t pi = r / a.group;
+    qh = kvh * a.group + static_cast<int>(r - pi * a.group);
+    p = a.positions[pi];
+    if (p >= a.kv_len) p = static_cast<int>(a.kv_len - 1);
+    qrow = a.q_by_position ? p : pi;
+    if (p < 0) p = -1;
+  }
+  const int pmax_w = wave_max_i(p);
+  if (lane == 0) red_max[wave] = pmax_w;
+  __syncthreads();
+  const int kend = max(max(red_max[0], red_max[1]), max(red_max[2], red_max[3])) + 1;
+  const int k0 = item.chunk * a.ksplit;
+  if (k0 >= kend) return;  // uniform: kend comes from shared memory
+  const int k1 = min(k0 + a.ksplit, kend);
+  const int nchunks = (kend + a.ksplit - 1) / a.ksplit;
+  const int plim = min(p, k1 - 1);                 // keys beyond the chunk are masked
+  const int pmin_w = wave_min_i(p >= 0 ? plim : 0x7fffffff);
+  const int pmax_c = min(pmax_w, k1 - 1);
+
+  vec8 qf[NKS];
+  {
+    const char* qp = a.q + qrow * a.q_s_row + qh * a.q_s_head;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      uint4 w = make_uint4(0, 0, 0, 0);
+      if (p >= 0) w = *reinterpret_cast<const uint4*>(qp + (16 * s + 8 * lg) * 2);
+      qf[s] = __builtin_bit_cast(vec8, w);
+    }
+  }
+
+  // Stage the chunk's block-table slice.
+  int lb0 = 0;
+  const bool bt_in_lds = a.paged && a.bs_log2 >= 0;
+  if (bt_in_lds) {
+    lb0 = k0 >> a.bs_log2;
+    const int nb = ((k1 - 1) >> a.bs_log2) - lb0 + 1;
+    for (int i = tid; i < nb; i += 256) bt_s[i] = clamp_block(a, a.block_table[lb0 + i]);
+    __syncthreads();
+  }
+  auto row_addr = [&](const char* base, int64_t s_head, int64_t s_seq, int key) -> const char* {
+    if (bt_in_lds) {
+      const int pb = bt_s[(key >> a.bs_log2) - lb0];
+      return base + pb * a.s_block + kvh * s_head +
+             static_cast<int64_t>(key & ((1 << a.bs_log2) - 1)) * a.s_pos;
+    }
+    return key_row(a, base, s_head, s_seq, key, kvh);
+  };
+
+  // Register staging of one tile.
+  uint4 kreg[KLD];
+  uint4 vreg[VLD][2];
+  auto load_tile = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) {
+      const int key = i * (256 / CH) + tid / CH;
+      const int kk = t0 + key;
+      kreg[i] = make_uint4(0, 0, 0, 0);
+      if (kk < k1)
+        kreg[i] = *reinterpret_cast<const uint4*>(row_addr(a.k, a.k_s_head, a.k_s_seq, kk) +
+                                                  (tid % CH) * 16);
+    }
+#pragma unroll
+    for (int ps = 0; ps < VLD; ++ps) {
+      const int m = tid & 31;
+      const int ch = (tid >> 5) + 8 * ps;
+      const int kk = t0 + 2 * m;
+      vreg[ps][0] = make_uint4(0, 0, 0, 0);
+      vreg[ps][1] = make_uint4(0, 0, 0, 0);
+      if (kk < k1)
+        vreg[ps][0] = *reinterpret_cast<const uint4*>(
+            row_addr(a.v, a.v_s_head, a.v_s_seq, kk) + ch * 16);
+      if (kk + 1 < k1)
+        vreg[ps][1] = *reinterpret_cast<const uint4*>(
+            row_addr(a.v, a.v_s_head, a.v_s_seq, kk + 1) + ch * 16);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) {
+      const int key = i * (256 / CH) + tid / CH;
+      *reinterpret_cast<uint4*>(&Ks[buf][key * KSTR + (tid % CH) * 8]) = kreg[i];
+    }
+#pragma unroll
+    for (int ps = 0; ps < VLD; ++ps) {
+      const int m = tid & 31;
+      const int ch = (tid >> 5) + 8 * ps;
+      const uint32_t x0[4] = {vreg[ps][0].x, vreg[ps][0].y, vreg[ps][0].z, vreg[ps][0].w};
+      const uint32_t x1[4] = {vreg[ps][1].x, vreg[ps][1].y, vreg[ps][1].z, vreg[ps][1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t lo = (x0[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+        const uint32_t hi = (x1[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+        *reinterpret_cast<uint32_t*>(&Vt[buf][(ch * 8 + e) * VSTR + 2 * m]) = lo | (hi << 16);
+      }
+    }
+  };
+
+  const float c = a.scale_log2;
+  float m_ref = -INFINITY;  // reference max (log2 domain) O and l are relative to
+  float l_run = 0.f;
+  f32x16_t o[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[t][i] = 0.f;
+
+  load_tile(k0);
+  store_tile(0);
+  __syncthreads();
+
+  int buf = 0;
+  for (int t0 = k0; t0 < k1; t0 += kTileKeys) {
+    const bool more = t0 + kTileKeys < k1;
+    if (more) load_tile(t0 + kTileKeys);
+
+    if (t0 <= pmax_c) {
+      // ---- S^T = K Q^T for two 32-key subtiles ----
+      f32x16_t s[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[j][i] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const vec8 kf = *reinterpret_cast<const vec8*>(
+              &Ks[buf][(32 * j + lq) * KSTR + 16 * ks + 8 * lg]);
+          s[j] = M::mma(kf, qf[ks], s[j]);
+        }
+      }
+      // ---- online softmax (log2 domain, lazy reference) ----
+      const bool need_mask = t0 + kTileKeys - 1 > pmin_w;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float v = s[j][i] * c;
+          if (need_mask) {
+            const int kk = t0 + 32 * j + 8 * (i >> 2) + 4 * lg + (i & 3);
+            if (kk > plim) v = -INFINITY;
+          }
+          s[j][i] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // Move the reference only when the max grows by more than 2^kLazyMax.
+      const bool bump = mx > m_ref + kLazyMax;
+      if (__any(bump)) {
+        const float m_new = bump ? mx : m_ref;
+        // 1 when this row keeps its reference, 0 when it had none (O and l are still 0).
+        const float alpha = bump ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.f;
+        l_run *= alpha;
+#pragma unroll
+        for (int t = 0; t < NDT; ++t)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[t][i] *= alpha;
+        m_ref = m_new;
+      }
+      const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
+      float lsum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float pv = __builtin_amdgcn_exp2f(s[j][i] - m_use);
+          s[j][i] = pv;
+          lsum += pv;
+        }
+      l_run += lsum;
+
+      // ---- O^T += V^T P^T ----
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          float pf[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) pf[e] = s[j][8 * st + e];
+          const vec8 pb = M::cvt8(pf);
+          const int kb = 32 * j + 16 * st + 4 * lg;
+#pragma unroll
+          for (int t = 0; t < NDT; ++t) {
+            const uint16_t* vrow = &Vt[buf][(32 * t + lq) * VSTR + kb];
+            const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+            const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+            const vec8 va = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            o[t] = M::mma(va, pb, o[t]);
+          }
+        }
+      }
+    }
+    if (more) store_tile(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // ---- finish: lane holds d = 32t + 8*(i/4) + 4*lg + (i%4) of its row ----
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (p < 0) return;
+  if (nchunks == 1) {
+    const float inv = 1.f / l_tot;
+    char* op = a.o + qrow * a.o_s_row + qh * a.o_s_head;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = 32 * t + 8 * qd + 4 * lg;
+        const uint32_t w0 = static_cast<uint32_t>(M::cvt1(o[t][4 * qd] * inv)) |
+                            (static_cast<uint32_t>(M::cvt1(o[t][4 * qd + 1] * inv)) << 16);
+        const uint32_t w1 = static_cast<uint32_t>(M::cvt1(o[t][4 * qd + 2] * inv)) |
+                            (static_cast<uint32_t>(M::cvt1(o[t][4 * qd + 3] * inv)) << 16);
+        *reinterpret_cast<uint2*>(op + d0 * 2) = make_uint2(w0, w1);
+      }
+  } else {
+    const int64_t slot =
+        ((static_cast<int64_t>(kvh) * a.n_tiles + item.tile) * a.max_chunks + item.chunk) *
+            kTileRows + row_in_tile;
+    float* po = a.part_o + slot * D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = 32 * t + 8 * qd + 4 * lg;
+        *reinterpret_cast<float4*>(po + d0) =
+            make_float4(o[t][4 * qd], o[t][4 * qd + 1], o[t][4 * qd + 2], o[t][4 * qd + 3]);
+      }
+    if (lg == 0)
+      *reinterpret_cast<float2*>(a.part_ml + slot * 2) =
+          make_float2(l_tot > 0.f ? m_ref : -INFINITY, l_tot);
+  }
+}
+
+// Combines the per-chunk partials of every row tile that needed more than one chunk:
+//   M = max_c m_c,  O = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.
+template <int DT>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
+  __shared__ int red[4];
+  const int tid = threadIdx.x;
+  const int64_t n_rows = attn_num_rows(a);
+  const int64_t rows_kv = n_rows * a.group;
+  const int64_t n_tiles_live = (rows_kv + kTileRows - 1) / kTileRows;
+  const int kvh = static_cast<int>(blockIdx.x % a.num_kv_heads);
+  const int64_t tile = static_cast<int64_t>(blockIdx.x / a.num_kv_heads);
+  if (tile >= n_tiles_live) return;
+  // Two threads per row, each owning half of head_dim.
+  const int row_in_tile = tid >> 1;
+  const int half = tid & 1;
+  const int64_t r = tile * kTileRows + row_in_tile;
+  int p = -1;
+  int64_t qrow = 0;
+  int qh = 0;
+  if (r < rows_kv) {
+    const int64_t pi = r / a.group;
+    qh = kvh * a.group + static_cast<int>(r - pi * a.group);
+    p = a.positions[pi];
+    if (p >= a.kv_len) p = static_cast<int>(a.kv_len - 1);
+    qrow = a.q_by_position ? p : pi;
+  }
+  const int pm = wave_max_i(p);
+  if ((tid & 63) == 0) red[tid >> 6] = pm;
+  __syncthreads();
+  const int kend = max(max(red[0], red[1]), max(red[2], red[3])) + 1;
+  const int nchunks = (kend + a.ksplit - 1) / a.ksplit;
+  if (nchunks <= 1 || p < 0) return;
+  const int D = a.head_dim;
+  const int64_t base = (static_cast<int64_t>(kvh) * a.n_tiles + tile) * a.max_chunks;
+  float mmax = -INFINITY;
+  for (int ch = 0; ch < nchunks; ++ch)
+    mmax = fmaxf(mmax, a.part_ml[((base + ch) * kTileRows + row_in_tile) * 2]);
+  float lsum = 0.f;
+  for (int ch = 0; ch < nchunks; ++ch) {
+    const float2 ml =
+        *reinterpret_cast<const float2*>(a.part_ml + ((base + ch) * kTileRows + row_in_tile) * 2);
+    if (ml.x != -INFINITY) lsum += __builtin_amdgcn_exp2f(ml.x - mmax) * ml.y;
+  }
+  const float inv = 1.f / lsum;
+  char* op = a.o + qrow * a.o_s_row + qh * a.o_s_head;
+  const int d_begin = half * (D / 2);
+  for (int d = d_begin; d < d_begin + D / 2; d += 4) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int ch = 0; ch < nchunks; ++ch) {
+      const int64_t slot = (base + ch) * kTileRows + row_in_tile;
+      const float m = a.part_ml[slot * 2];
+      if (m == -INFINITY) continue;
+      const float w = __builtin_amdgcn_exp2f(m - mmax);
+      const float4 v = *reinterpret_cast<const float4*>(a.part_o + slot * D + d);
+      acc.x += w * v.x; acc.y += w * v.y; acc.z += w * v.z; acc.w += w * v.w;
+    }
+    const uint32_t w0 = static_cast<uint32_t>(Mma<DT>::cvt1(acc.x * inv)) |
+                        (static_cast<uint32_t>(Mma<DT>::cvt1(acc.y * inv)) << 16);
+    const uint32_t w1 = static_cast<uint32_t>(Mma<DT>::cvt1(acc.z * inv)) |
+                        (static_cast<uint32_t>(Mma<DT>::cvt1(acc.w * inv)) << 16);
+    *reinterpret_cast<uint2*>(op + d * 2) = make_uint2(w0, w1);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// VALU path: any dtype, any head_dim. One wave per (row, q-head).
+// ---------------------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ float load_elem(const char* p, int64_t idx) {
+  if (DT == SB_DTYPE_F32) return reinterpret_cast<const float*>(p)[idx];
+  const uint16_t h = reinterpret_cast<const uint16_t*>(p)[idx];
+  return DT == SB_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+template <int DT>
+__device__ __forceinline__ void store_elem(char* p, int64_t idx, float f) {
+  if (DT == SB_DTYPE_F32) {
+    reinterpret_cast<float*>(p)[idx] = f;
+  } else {
+    reinterpret_cast<uint16_t*>(p)[idx] = DT == SB_DTYPE_BF16 ? f32_to_bf16(f) : f32_to_f16(f);
+  }
+}
+
+constexpr int kValuMaxDim = 512;
+
+template <int DT>
+__global__ __launch_bounds__(64) void attn_valu_kernel(AttnArgs a) {
+  __shared__ float qs[kValuMaxDim];
+  __shared__ float ps[64];
+  const int lane = threadIdx.x;
+  const int64_t pi = blockIdx.x;
+  const int qh = static_cast<int>(blockIdx.y);
+  if (pi >= attn_num_rows(a)) return;
+  int p = a.positions[pi];
+  if (p < 0) return;
+  if (p >= a.kv_len) p = static_cast<int>(a.kv_len - 1);
+  const int kvh = qh / a.group;
+  const int D = a.head_dim;
+  const int64_t qrow = a.q_by_position ? p : pi;
+  const char* qp = a.q + qrow * a.q_s_row + qh * a.q_s_head;
+  for (int d = lane; d < D; d += 64) qs[d] = load_elem<DT>(qp, d);
+  __syncthreads();
+
+  constexpr int kU = kValuMaxDim / 64;
+  float acc[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) acc[u] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  for (int t0 = 0; t0 <= p; t0 += 64) {
+    const int key = t0 + lane;
+    float sc = -INFINITY;
+    if (key <= p) {
+      const char* kp = key_row(a, a.k, a.k_s_head, a.k_s_seq, key, kvh);
+      float dot = 0.f;
+      for (int d = 0; d < D; ++d) dot += qs[d] * load_elem<DT>(kp, d);
+      sc = dot * a.scale;
+    }
+    const float m_new = fmaxf(m_run, wave_max(sc));
+    const float alpha = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
+    const float pk = key <= p ? expf(sc - m_new) : 0.f;
+    l_run = l_run * alpha + wave_sum(pk);
+    m_run = m_new;
+    ps[lane] = pk;
+    __syncthreads();
+    const int nk = min(64, p - t0 + 1);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int d = lane + 64 * u;
+      if (d < D) {
+        float sum = 0.f;
+        for (int kk = 0; kk < nk; ++kk)
+          sum += ps[kk] * load_elem<DT>(key_row(a, a.v, a.v_s_head, a.v_s_seq, t0 + kk, kvh), d);
+        acc[u] = acc[u] * alpha + sum;
+      }
+    }
+    __syncthreads();
+  }
+  char* op = a.o + qrow * a.o_s_row + qh * a.o_s_head;
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const int d = lane + 64 * u;
+    if (d < D) store_elem<DT>(op, d, acc[u] / l_run);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Dense drop-in helpers: compact a bool mask into ascending positions (+ count), and write
+// zeros into the output rows whose mask entry is 0.
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void mask_compact_kernel(const uint8_t* mask, int64_t n,
+                                                            int32_t* pos_out,
+                                                            int32_t* count_out) {
+  __shared__ int wsum[16];
+  __shared__ int base;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) base = 0;
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < n; c0 += 1024) {
+    const int64_t i = c0 + tid;
+    const bool f = i < n && mask[i] != 0;
+    const uint64_t b = __ballot(f);
+    const int pre = __popcll(b & ((uint64_t{1} << lane) - 1));
+    if (lane == 0) wsum[wave] = __popcll(b);
+    __syncthreads();
+    int off = base;
+    for (int w = 0; w < wave; ++w) off += wsum[w];
+    if (f) pos_out[off + pre] = static_cast<int32_t>(i);
+    __syncthreads();
+    if (tid == 0) {
+      int t = 0;
+      for (int w = 0; w < 16; ++w) t += wsum[w];
+      base += t;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) *count_out = base;
+}
+
+template <int VB>
+__global__ void zero_rows_kernel(char* out, const uint8_t* mask, int64_t num_heads,
+                                 int64_t seq_len, int64_t s_head, int64_t s_seq, int vpr) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = num_heads * seq_len * vpr;
+  if (idx >= total) return;
+  const int64_t j = idx % vpr;
+  const int64_t row = idx / vpr;
+  const int64_t s = row % seq_len;
+  const int64_t h = row / seq_len;
+  if (mask[s]) return;
+  char* p = out + h * s_head + s * s_seq + j * VB;
+  if (VB == 16) *reinterpret_cast<uint4*>(p) = make_uint4(0, 0, 0, 0);
+  else if (VB == 8) *reinterpret_cast<uint2*>(p) = make_uint2(0, 0);
+  else if (VB == 4) *reinterpret_cast<uint32_t*>(p) = 0u;
+  else *reinterpret_cast<uint16_t*>(p) = 0;
+}
+
+namespace {
+
+constexpr int kAssumedSlots = 512;  // resident workgroups of the MFMA kernel on 256 CUs
+
+bool mfma_path(int32_t dtype, int64_t head_dim) {
+  return (dtype == SB_DTYPE_BF16 || dtype == SB_DTYPE_F16) &&
+         (head_dim == 64 || head_dim == 128);
+}
+
+// Chunking of the key range for one call. rows_upper bounds the query rows.
+struct Plan {
+  int ksplit;
+  int max_chunks;
+  int64_t n_tiles;
+  int64_t part_bytes;  // bytes of partials (O then m/l), 0 when no tile splits
+};
+
+Plan make_plan(int64_t rows_upper, int64_t group, int64_t num_kv_heads, int64_t kv_len,
+               int64_t head_dim, int64_t block_size, bool paged) {
+  Plan pl{};
+  pl.n_tiles = (rows_upper * group + kTileRows - 1) / kTileRows;
+  const int64_t kv_pad = (kv_len + kTileKeys - 1) / kTileKeys * kTileKeys;
+  // Aim for items no longer than the average work per resident workgroup, assuming the
+  // rows' key ranges average half the context.
+  int64_t ks = pl.n_tiles * num_kv_heads * (kv_len / 2) / kAssumedSlots;
+  ks = ks / kTileKeys * kTileKeys;
+  if (ks < 512) ks = 512;
+  if (paged) {
+    int64_t cap = static_cast<int64_t>(kBtLds) * block_size / kTileKeys * kTileKeys;
+    if (ks > cap) ks = cap;
+  }
+  if (ks > kv_pad) ks = kv_pad;
+  if (ks < kTileKeys) ks = kTileKeys;
+  int64_t chunks = (kv_len + ks - 1) / ks;
+  pl.ksplit = static_cast<int>(ks);
+  pl.max_chunks = static_cast<int>(chunks < 1 ? 1 : chunks);
+  if (pl.max_chunks > 1)
+    pl.part_bytes = num_kv_heads * pl.n_tiles * pl.max_chunks * kTileRows * (head_dim + 2) * 4;
+  return pl;
+}
+
+int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upper,
+                     bool aligned16, void* workspace, int64_t workspace_bytes,
+                     hipStream_t st) {
+  if (rows_upper <= 0) return SB_OK;
+  if (mfma_path(dtype, a.head_dim) && aligned16) {
+    const Plan pl = make_plan(rows_upper, a.group, a.num_kv_heads, a.kv_len, a.head_dim,
+                              a.block_size, a.paged != 0);
+    a.ksplit = pl.ksplit;
+    a.max_chunks = pl.max_chunks;
+    a.n_tiles = pl.n_tiles;
+    if (pl.part_bytes > 0) {
+      if (!workspace || workspace_bytes < pl.part_bytes)
+        return fail(fn, "workspace too small for the split-key partials");
+      a.part_o = static_cast<float*>(workspace);
+      a.part_ml = a.part_o + a.num_kv_heads * pl.n_tiles * pl.max_chunks * kTileRows *
+                                 static_cast<int64_t>(a.head_dim);
+    }
+    const int64_t gx = pl.n_tiles * a.num_kv_heads * pl.max_chunks;
+    if (gx > 0x7fffffff) return fail(fn, "grid too large");
+    dim3 grid(static_cast<unsigned>(gx));
+    dim3 mgrid(static_cast<unsigned>(pl.n_tiles * a.num_kv_heads));
+#define SB_ATT_CASE(DT, D)                                                              \
+  if (dtype == DT && a.head_dim == D) {                                                 \
+    hipLaunchKernelGGL((attn_mfma_kernel<DT, D>), grid, dim3(256), 0, st, a);           \
+    if (pl.max_chunks > 1)                                                              \
+      hipLaunchKernelGGL((attn_merge_kernel<DT>), mgrid, dim3(256), 0, st, a);          \
+    return check_launch(fn);                                                            \
+  }
+    SB_ATT_CASE(SB_DTYPE_BF16, 128)
+    SB_ATT_CASE(SB_DTYPE_BF16, 64)
+    SB_ATT_CASE(SB_DTYPE_F16, 128)
+    SB_ATT_CASE(SB_DTYPE_F16, 64)
+#undef SB_ATT_CASE
+  }
+  if (a.head_dim > kValuMaxDim) return fail(fn, "head_dim above 512 is not supported");
+  if (rows_upper > 0x7fffffff) return fail(fn, "too many rows");
+  dim3 grid(static_cast<unsigned>(rows_upper), static_cast<unsigned>(a.num_kv_heads * a.group));
+  if (dtype == SB_DTYPE_F32) hipLaunchKernelGGL(attn_valu_kernel<SB_DTYPE_F32>, grid, dim3(64), 0, st, a);
+  else if (dtype == SB_DTYPE_BF16) hipLaunchKernelGGL(attn_valu_kernel<SB_DTYPE_BF16>, grid, dim3(64), 0, st, a);
+  else hipLaunchKernelGGL(attn_valu_kernel<SB_DTYPE_F16>, grid, dim3(64), 0, st, a);
+  return check_launch(fn);
+}
+
+int log2_exact(int64_t v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int l = 0;
+  while ((int64_t{1} << l) < v) ++l;
+  return l;
+}
+
+int64_t part_bytes_for(int32_t dtype, int64_t rows_upper, int64_t group, int64_t num_kv_heads,
+                       int64_t kv_len, int64_t head_dim, int64_t block_size, bool paged) {
+  if (!mfma_path(dtype, head_dim)) return 0;
+  return make_plan(rows_upper, group, num_kv_heads, kv_len, head_dim, block_size, paged)
+      .part_bytes;
+}
+
+}  // namespace
+}  // namespace sb
+
+using namespace sb;
+
+extern "C" int64_t sb_partial_prefill_attention_workspace_size(int64_t num_heads,
+                                                               int64_t seq_len,
+                                                               int64_t head_dim,
+                                                               int32_t dtype) {
+  // positions (S) + count, rounded to 256 bytes, then the split-key partials.
+  const int64_t idx = ((seq_len + 1) * 4 + 255) / 256 * 256;
+  return idx + part_bytes_for(dtype, seq_len, 1, num_heads, seq_len, head_dim, 1, false);
+}
+
+extern "C" int sb_partial_prefill_attention(void* out, const void* q, const void* k,
+                                            const void* v, const uint8_t* compute_mask,
+                                            void* workspace, int64_t workspace_bytes,
+                                            int64_t num_heads, int64_t seq_len,
+                                            int64_t head_dim, float scale, const int64_t* qs,
+                                            const int64_t* ks, const int64_t* vs,
+                                            const int64_t* os, int32_t dtype, void* stream) {
+  const char* fn = "sb_partial_prefill_attention";
+  clear_error();
+  if (num_heads == 0 || seq_len == 0 || head_dim == 0) return SB_OK;
+  if (elem_size(dtype) == 0) return fail(fn, "invalid dtype");
+  if (!out || !q || !k || !v || !compute_mask || !workspace || !qs || !ks || !vs || !os)
+    return fail(fn, "null pointer argument");
+  if (qs[2] != 1 || ks[2] != 1 || vs[2] != 1 || os[2] != 1)
+    return fail(fn, "head_dim must be contiguous (stride 1)");
+  if (seq_len > 0x7ffffffe) return fail(fn, "sequence too long");
+  if (workspace_bytes < sb_partial_prefill_attention_workspace_size(num_heads, seq_len,
+                                                                    head_dim, dtype))
+    return fail(fn, "workspace too small");
+  const int64_t es = elem_size(dtype);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int32_t* pos = static_cast<int32_t*>(workspace);
+  const int64_t idx_bytes = ((seq_len + 1) * 4 + 255) / 256 * 256;
+
+  // Zero the rows that are not computed (output semantics of torch.zeros_like + row writes).
+  {
+    const int vb = vec_bytes({reinterpret_cast<int64_t>(out), os[0] * es, os[1] * es,
+                              head_dim * es});
+    const int vpr = static_cast<int>(head_dim * es / vb);
+    const int64_t total = num_heads * seq_len * vpr;
+    const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+    char* o = static_cast<char*>(out);
+    if (vb >= 16) hipLaunchKernelGGL(zero_rows_kernel<16>, grid, dim3(256), 0, st, o, compute_mask, num_heads, seq_len, os[0] * es, os[1] * es, vpr);
+    else if (vb == 8) hipLaunchKernelGGL(zero_rows_kernel<8>, grid, dim3(256), 0, st, o, compute_mask, num_heads, seq_len, os[0] * es, os[1] * es, vpr);
+    else if (vb == 4) hipLaunchKernelGGL(zero_rows_kernel<4>, grid, dim3(256), 0, st, o, compute_mask, num_heads, seq_len, os[0] * es, os[1] * es, vpr);
+    else hipLaunchKernelGGL(zero_rows_kernel<2>, grid, dim3(256), 0, st, o, compute_mask, num_heads, seq_len, os[0] * es, os[1] * es, vpr);
+  }
+  hipLaunchKernelGGL(mask_compact_kernel, dim3(1), dim3(1024), 0, st, compute_mask, seq_len,
+                     pos, pos + seq_len);
+  int rc = check_launch(fn);
+  if (rc) return rc;
+
+  AttnArgs a{};
+  a.q = static_cast<const char*>(q);
+  a.o = static_cast<char*>(out);
+  a.q_s_row = qs[1] * es;
+  a.q_s_head = qs[0] * es;
+  a.o_s_row = os[1] * es;
+  a.o_s_head = os[0] * es;
+  a.q_by_position = 1;
+  a.positions = pos;
+  a.count_ptr = pos + seq_len;
+  a.num_rows = seq_len;
+  a.k = static_cast<const char*>(k);
+  a.v = static_cast<const char*>(v);
+  a.k_s_head = ks[0] * es;
+  a.v_s_head = vs[0] * es;
+  a.k_s_seq = ks[1] * es;
+  a.v_s_seq = vs[1] * es;
+  a.paged = 0;
+  a.block_size = 1;
+  a.bs_log2 = -1;
+  a.kv_len = seq_len;
+  a.num_kv_heads = static_cast<int>(num_heads);
+  a.group = 1;
+  a.head_dim = static_cast<int>(head_dim);
+  a.scale = scale;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const bool aligned16 =
+      vec_bytes({reinterpret_cast<int64_t>(q), reinterpret_cast<int64_t>(k),
+                 reinterpret_cast<int64_t>(v), reinterpret_cast<int64_t>(out), qs[0] * es,
+                 qs[1] * es, ks[0] * es, ks[1] * es, vs[0] * es, vs[1] * es, os[0] * es,
+                 os[1] * es}) >= 16;
+  return launch_attention(fn, a, dtype, seq_len, aligned16,
+                          static_cast<char*>(workspace) + idx_bytes,
+                          workspace_bytes - idx_bytes, st);
+}
+
+extern "C" int64_t sb_partial_attention_paged_workspace_size(int64_t num_rows,
+                                                             int64_t num_q_heads,
+                                                             int64_t num_kv_heads,
+                                                             int64_t head_dim,
+                                                             int64_t block_size,
+                                                             int64_t num_blocks_per_seq,
+                                                             int32_t dtype) {
+  if (num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0) return 0;
+  return part_bytes_for(dtype, num_rows, num_q_heads / num_kv_heads, num_kv_heads,
+                        num_blocks_per_seq * block_size, head_dim, block_size, true);
+}
+
+extern "C" int sb_partial_attention_paged(void* out, const void* q, const void* kv_cache,
+                                          const int32_t* block_table, const int32_t* positions,
+                                          void* workspace, int64_t workspace_bytes,
+                                          int64_t num_rows, int64_t num_q_heads,
+                                          int64_t num_kv_heads, int64_t head_dim,
+                                          int64_t block_size, int64_t num_blocks_total,
+                                          int64_t num_blocks_per_seq, float scale,
+                                          const int64_t* qs, const int64_t* os,
+                                          const int64_t* kvs, int32_t dtype, void* stream) {
+  const char* fn = "sb_partial_attention_paged";
+  clear_error();
+  if (num_rows == 0 || num_q_heads == 0 || head_dim == 0) return SB_OK;
+  if (elem_size(dtype) == 0) return fail(fn, "invalid dtype");
+  if (!out || !q || !kv_cache || !block_table || !positions || !qs || !os || !kvs)
+    return fail(fn, "null pointer argument");
+  if (num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
+    return fail(fn, "num_q_heads must be a multiple of num_kv_heads");
+  if (block_size <= 0 || num_blocks_per_seq <= 0 || num_blocks_total <= 0)
+    return fail(fn, "empty block table or pool");
+  if (qs[2] != 1 || os[2] != 1 || kvs[4] != 1)
+    return fail(fn, "head_dim must be contiguous (stride 1)");
+  const int64_t es = elem_size(dtype);
+  AttnArgs a{};
+  a.q = static_cast<const char*>(q);
+  a.o = static_cast<char*>(out);
+  a.q_s_row = qs[0] * es;
+  a.q_s_head = qs[1] * es;
+  a.o_s_row = os[0] * es;
+  a.o_s_head = os[1] * es;
+  a.q_by_position = 0;
+  a.positions = positions;
+  a.count_ptr = nullptr;
+  a.num_rows = num_rows;
+  a.k = static_cast<const char*>(kv_cache);
+  a.v = static_cast<const char*>(kv_cache) + kvs[1] * es;
+  a.k_s_head = kvs[2] * es;
+  a.v_s_head = kvs[2] * es;
+  a.paged = 1;
+  a.block_table = block_table;
+  a.block_size = block_size;
+  a.bs_log2 = log2_exact(block_size);
+  a.nb_total = num_blocks_total;
+  a.nb_per_seq = num_blocks_per_seq;
+  a.s_block = kvs[0] * es;
+  a.s_pos = kvs[3] * es;
+  a.kv_len = num_blocks_per_seq * block_size;
+  a.num_kv_heads = static_cast<int>(num_kv_heads);
+  a.group = static_cast<int>(num_q_heads / num_kv_heads);
+  a.head_dim = static_cast<int>(head_dim);
+  a.scale = scale;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const bool aligned16 =
+      vec_bytes({reinterpret_cast<int64_t>(q), reinterpret_cast<int64_t>(kv_cache),
+                 reinterpret_cast<int64_t>(out), qs[0] * es, qs[1] * es, os[0] * es,
+                 os[1] * es, kvs[0] * es, kvs[1] * es, kvs[2] * es, kvs[3] * es}) >= 16;
+  return launch_attention(fn, a, dtype, num_rows, aligned16, workspace, workspace_bytes,
+                          static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,951 @@
+// Row movers for the KV-reuse path: donor-KV scatter (flat and paged), fused scatter + RoPE,
+// in-place paged RoPE, snapshot permutations (delta and NoPE forms) and the flat
+// rope_correct_k. Every operation moves head_dim-long rows between two row addressings:
+//
+//   ROW_FLAT_POS   row of a [.., S, D] tensor selected by a position value   (donor buffers)
+//   ROW_PAGED_POS  slot of a paged cache selected by a logical position
+//                  through a block table                                     (KV caches)
+//   ROW_INDEX      row i of a dense [P, .., D] staging buffer                (snapshots)
+//
+// One thread owns one VB-byte vector of one pair's row and walks every (layer, head) plane
+// in its group, so a rotation's cos/sin are evaluated once per (pair, frequency) and reused
+// for all layers and heads. Rows are head_dim * elem bytes long; a 128-dim bf16 row is
+// 16 lanes x 16 bytes, so a wave moves four 256-byte rows per instruction.
+//
+// RoPE arithmetic follows the interleaved (GPT-J) convention of
+// semblend_core/rope_correction.py:163-178 and :317-326, in fp32:
+//   e' = e*c - o*s,  o' = e*s + o*c,  theta = delta * inv_freq[i]
+// with one rounding to the cache dtype (the CPU path of the reference, :328). This file is
+// compiled with -ffp-contract=off so each product and sum rounds exactly like torch's CPU
+// elementwise ops.
+
+#include "sb_common.h"
+
+namespace sb {
+
+enum RowMode : int { ROW_FLAT_POS = 0, ROW_PAGED_POS = 1, ROW_INDEX = 2 };
+enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3 };
+
+constexpr int kThreads = 256;
+constexpr int kBatch = 4;  // rows loaded before the first store, for memory-level parallelism
+
+struct RowSide {
+  char* base;              // layer-0 base address (used when layers == nullptr)
+  const uint64_t* layers;  // device table of per-layer base addresses, or nullptr
+  int64_t s_layer;         // byte strides
+  int64_t s_kv;
+  int64_t s_head;
+  int64_t s_row;           // FLAT_POS: sequence stride; PAGED_POS: block stride; INDEX: pair stride
+  int64_t s_pos;           // PAGED_POS: position-in-block stride
+  int64_t bound;           // FLAT_POS: sequence length
+};
+
+struct MoveArgs {
+  RowSide src, dst;
+  const int32_t* src_pos;  // per-pair source positions (FLAT_POS / PAGED_POS sources)
+  const int32_t* dst_pos;  // per-pair destination positions
+  const int32_t* repeat;   // ROT_CONST: rotations to apply per pair (nullptr = 1)
+  const int32_t* block_table;
+  int64_t block_size;
+  int64_t nb_total;
+  int64_t nb_per_seq;
+  const float* inv_freq;
+  int64_t const_delta;     // ROT_CONST
+  int64_t num_pairs;
+  int num_heads;
+  int num_layers;
+  int layers_per_group;
+  int kv_first;            // first kv plane (0 = K, 1 = V)
+  int num_kv;              // 1 or 2 planes
+  int src_index_check;     // ROW_INDEX source: also require src_pos to be a valid paged slot
+  int vpr;                 // vectors per row
+  int tpr_log2;            // log2(threads per row)
+};
+
+// Resolves a logical position to the byte offset of its slot (without layer/kv/head terms).
+__device__ __forceinline__ bool paged_slot(const MoveArgs& a, int64_t pos, int64_t s_blk,
+                                           int64_t s_pos, int64_t* off) {
+  if (pos < 0) return false;
+  const int64_t lb = pos / a.block_size;
+  if (lb >= a.nb_per_seq) return false;
+  const int64_t pb = a.block_table[lb];
+  if (pb < 0 || pb >= a.nb_total) return false;
+  *off = pb * s_blk + (pos - lb * a.block_size) * s_pos;
+  return true;
+}
+
+template <int MODE>
+__device__ __forceinline__ bool resolve_row(const MoveArgs& a, const RowSide& s,
+                                            const int32_t* pos, int64_t i, int64_t* off) {
+  if (MODE == ROW_INDEX) {
+    *off = i * s.s_row;
+    return true;
+  } else if (MODE == ROW_FLAT_POS) {
+    const int64_t p = pos[i];
+    if (p < 0 || p >= s.bound) return false;
+    *off = p * s.s_row;
+    return true;
+  } else {
+    return paged_slot(a, pos[i], s.s_row, s.s_pos, off);
+  }
+}
+
+__device__ __forceinline__ char* layer_base(const RowSide& s, int l) {
+  return s.layers ? reinterpret_cast<char*>(s.layers[l]) : s.base + l * s.s_layer;
+}
+
+// Unpacks VB bytes held as W 32-bit words into E fp32 values (and back).
+template <int DT, int W>
+__device__ __forceinline__ void unpack_words(const uint32_t* w, float* f) {
+  if (DT == SB_DTYPE_F32) {
+#pragma unroll
+    for (int k = 0; k < W; ++k) f[k] = __uint_as_float(w[k]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const uint16_t lo = static_cast<uint16_t>(w[k] & 0xffffu);
+      const uint16_t hi = static_cast<uint16_t>(w[k] >> 16);
+      f[2 * k] = DT == SB_DTYPE_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+      f[2 * k + 1] = DT == SB_DTYPE_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+    }
+  }
+}
+
+template <int DT, int W>
+__device__ __forceinline__ void pack_words(const float* f, uint32_t* w) {
+  if (DT == SB_DTYPE_F32) {
+#pragma unroll
+    for (int k = 0; k < W; ++k) w[k] = __float_as_uint(f[k]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const uint32_t lo = DT == SB_DTYPE_BF16 ? f32_to_bf16(f[2 * k]) : f32_to_f16(f[2 * k]);
+      const uint32_t hi =
+          DT == SB_DTYPE_BF16 ? f32_to_bf16(f[2 * k + 1]) : f32_to_f16(f[2 * k + 1]);
+      w[k] = lo | (hi << 16);
+    }
+  }
+}
+
+template <int VB>
+__device__ __forceinline__ void load_vec(const char* p, uint32_t* w) {
+  if (VB == 16) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else if (VB == 8) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    w[0] = v.x; w[1] = v.y;
+  } else {
+    w[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+}
+
+template <int VB>
+__device__ __forceinline__ void store_vec(char* p, const uint32_t* w) {
+  if (VB == 16) {
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else if (VB == 8) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+  } else {
+    *reinterpret_cast<uint32_t*>(p) = w[0];
+  }
+}
+
+// fp32 sin/cos rounded correctly: evaluated in fp64 and rounded once to fp32. These are the
+// values a correctly rounded libm returns, which torch's CPU kernels also produce for all but
+// rare arguments. Matching them matters where e*c - o*s cancels: for an output of ~1e-6 from
+// O(1) inputs, a one-ulp difference in cos or sin is several bf16 ulps of the result.
+__device__ __forceinline__ void sincos_rn(float x, float* s, float* c) {
+  double sd, cd;
+  sincos(static_cast<double>(x), &sd, &cd);
+  *s = static_cast<float>(sd);
+  *c = static_cast<float>(cd);
+}
+
+// In-register rotation of E/2 interleaved pairs: e' = e*c - o*s, o' = e*s + o*c.
+template <int NP>
+__device__ __forceinline__ void rotate_pairs(float* f, const float* c, const float* s) {
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    const float e = f[2 * k], o = f[2 * k + 1];
+    const float ec = e * c[k], os = o * s[k], es = e * s[k], oc = o * c[k];
+    f[2 * k] = ec - os;
+    f[2 * k + 1] = es + oc;
+  }
+}
+
+// NoPE two-step: strip R(-src) then apply R(tgt) (rope_correction.py:564-578, :806-821).
+template <int NP>
+__device__ __forceinline__ void nope_pairs(float* f, const float* cs, const float* ss,
+                                           const float* ct, const float* st) {
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    const float e = f[2 * k], o = f[2 * k + 1];
+    const float re = e * cs[k] + o * ss[k];
+    const float ro = -(e * ss[k]) + o * cs[k];
+    f[2 * k] = re * ct[k] - ro * st[k];
+    f[2 * k + 1] = re * st[k] + ro * ct[k];
+  }
+}
+
+template <int DT, int VB, int ROT, int SRCM, int DSTM>
+__global__ __launch_bounds__(kThreads) void move_rows_kernel(MoveArgs a) {
+  constexpr int W = VB / 4;
+  constexpr int E = (DT == SB_DTYPE_F32) ? W : 2 * W;
+  constexpr int NP = E / 2;
+  constexpr int NPA = NP > 0 ? NP : 1;  // plain copies of 4-byte fp32 words have no pairs
+  const int tpr = 1 << a.tpr_log2;
+  const int lane = threadIdx.x & (tpr - 1);
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * (kThreads >> a.tpr_log2) +
+                    (threadIdx.x >> a.tpr_log2);
+  if (i >= a.num_pairs) return;
+
+  const int kv = a.kv_first + static_cast<int>(blockIdx.y % a.num_kv);
+  const int l0 = static_cast<int>(blockIdx.y / a.num_kv) * a.layers_per_group;
+  const int l1 = min(l0 + a.layers_per_group, a.num_layers);
+
+  int64_t src_off, dst_off;
+  if (!resolve_row<SRCM>(a, a.src, a.src_pos, i, &src_off)) return;
+  if (!resolve_row<DSTM>(a, a.dst, a.dst_pos, i, &dst_off)) return;
+  if (SRCM == ROW_INDEX && a.src_index_check) {
+    int64_t unused;
+    if (!paged_slot(a, a.src_pos[i], 0, 0, &unused)) return;
+  }
+  const bool rotate = (ROT != ROT_NONE) && kv == 0;
+  int reps = 1;
+  if (ROT == ROT_CONST && a.repeat) reps = a.repeat[i];
+
+  float ang_a = 0.f, ang_b = 0.f;  // angle multipliers (fp32, as torch computes them)
+  if (ROT == ROT_DELTA) ang_a = static_cast<float>(a.dst_pos[i] - a.src_pos[i]);
+  if (ROT == ROT_CONST) ang_a = static_cast<float>(a.const_delta);
+  if (ROT == ROT_NOPE) {
+    ang_a = static_cast<float>(a.src_pos[i]);
+    ang_b = static_cast<float>(a.dst_pos[i]);
+  }
+
+  const int nrows = (l1 - l0) * a.num_heads;
+  for (int j = lane; j < a.vpr; j += tpr) {
+    float c0[NPA], s0[NPA], c1[NPA], s1[NPA];
+    if (ROT != ROT_NONE && rotate) {
+#pragma unroll
+      for (int k = 0; k < NP; ++k) {
+        const float f = a.inv_freq[j * NP + k];
+        sincos_rn(ang_a * f, &s0[k], &c0[k]);
+        if (ROT == ROT_NOPE) sincos_rn(ang_b * f, &s1[k], &c1[k]);
+      }
+    }
+    const int64_t vofs = static_cast<int64_t>(j) * VB;
+    for (int r0 = 0; r0 < nrows; r0 += kBatch) {
+      uint32_t w[kBatch][W];
+      char* dptr[kBatch];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const int r = r0 + b;
+        dptr[b] = nullptr;
+        if (r < nrows) {
+          const int l = l0 + r / a.num_heads;
+          const int h = r - (r / a.num_heads) * a.num_heads;
+          const char* sp = layer_base(a.src, l) + kv * a.src.s_kv + h * a.src.s_head +
+                           src_off + vofs;
+          dptr[b] = layer_base(a.dst, l) + kv * a.dst.s_kv + h * a.dst.s_head + dst_off + vofs;
+          load_vec<VB>(sp, w[b]);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        if (!dptr[b]) continue;
+        if (ROT != ROT_NONE && rotate) {
+          float f[E];
+          unpack_words<DT, W>(w[b], f);
+          if (ROT == ROT_NOPE) {
+            nope_pairs<NP>(f, c0, s0, c1, s1);
+          } else {
+            for (int rep = 0; rep < reps; ++rep) {
+              if (rep > 0) {
+#pragma unroll
+                for (int k = 0; k < E; ++k) f[k] = Codec<DT>::round_trip(f[k]);
+              }
+              rotate_pairs<NP>(f, c0, s0);
+            }
+          }
+          pack_words<DT, W>(f, w[b]);
+        }
+        store_vec<VB>(dptr[b], w[b]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Row-centric flat RoPE (rope_correct_k): one thread per (position s, vector j), walking all
+// (layer, head) rows of that position. A prepass records, for every position, how many
+// pairs name it as donor position and the first such pair (ws[0:S] counts,
+// ws[S:2S] = P - first_index, via atomicMax so the smallest index wins).
+// ---------------------------------------------------------------------------------------
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__global__ void rope_index_kernel(const int32_t* dpos, int64_t num_pairs, int64_t seq_len,
+                                  int32_t* ws) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= num_pairs) return;
+  const int64_t d = dpos[i];
+  if (d < 0 || d >= seq_len) return;
+  atomicAdd(&ws[d], 1);
+  atomicMax(&ws[seq_len + d], static_cast<int32_t>(num_pairs - i));
+}
+
+struct RopeRowsArgs {
+  char* out;
+  const char* k;
+  int64_t o_s_layer, o_s_head, o_s_seq;  // byte strides
+  int64_t k_s_layer, k_s_head, k_s_seq;
+  const int32_t* dpos;
+  const int32_t* tpos;
+  const int32_t* ws;
+  const float* inv_freq;
+  int64_t num_pairs;
+  int64_t seq_len;
+  int num_layers;
+  int num_heads;
+  int rows_per_group;  // (layer, head) rows handled per grid.y slice
+  int in_place;
+  int vpr;
+  int tpr_log2;
+};
+
+template <int DT, int VB>
+__global__ __launch_bounds__(kThreads) void rope_rows_kernel(RopeRowsArgs a) {
+  constexpr int W = VB / 4;
+  constexpr int E = (DT == SB_DTYPE_F32) ? W : 2 * W;
+  constexpr int NP = E / 2;
+  const int tpr = 1 << a.tpr_log2;
+  const int lane = threadIdx.x & (tpr - 1);
+  const int64_t s = static_cast<int64_t>(blockIdx.x) * (kThreads >> a.tpr_log2) +
+                    (threadIdx.x >> a.tpr_log2);
+  if (s >= a.seq_len) return;
+  const int cnt = a.ws[s];
+  if (cnt == 0 && a.in_place) return;
+  const int64_t first = a.num_pairs - a.ws[a.seq_len + s];
+
+  const int total_rows = a.num_layers * a.num_heads;
+  const int r_begin = static_cast<int>(blockIdx.y) * a.rows_per_group;
+  const int r_end = min(r_begin + a.rows_per_group, total_rows);
+
+  for (int j = lane; j < a.vpr; j += tpr) {
+    float c[NP], sn[NP];
+    if (cnt == 1) {
+      const float delta = static_cast<float>(a.tpos[first] - a.dpos[first]);
+#pragma unroll
+      for (int k = 0; k < NP; ++k) sincos_rn(delta * a.inv_freq[j * NP + k], &sn[k], &c[k]);
+    }
+    const int64_t vofs = static_cast<int64_t>(j) * VB;
+    for (int r0 = r_begin; r0 < r_end; r0 += kBatch) {
+      uint32_t w[kBatch][W];
+      char* dptr[kBatch];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const int r = r0 + b;
+        dptr[b] = nullptr;
+        if (r < r_end) {
+          const int l = r / a.num_heads;
+          const int h = r - l * a.num_heads;
+          load_vec<VB>(a.k + l * a.k_s_layer + h * a.k_s_head + s * a.k_s_seq + vofs, w[b]);
+          dptr[b] = a.out + l * a.o_s_layer + h * a.o_s_head + s * a.o_s_seq + vofs;
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        if (!dptr[b]) continue;
+        if (cnt >= 1) {
+          float f[E];
+          unpack_words<DT, W>(w[b], f);
+          if (cnt == 1) {
+            rotate_pairs<NP>(f, c, sn);
+          } else {
+            // Several pairs rotate this row: apply them in pair order, rounding to the
+            // tensor dtype after each one, as the reference's sequential loop does.
+            int seen = 0;
+            for (int64_t p = first; p < a.num_pairs && seen < cnt; ++p) {
+              if (a.dpos[p] != s) continue;
+              if (seen > 0) {
+#pragma unroll
+                for (int k = 0; k < E; ++k) f[k] = Codec<DT>::round_trip(f[k]);
+              }
+              const float delta = static_cast<float>(a.tpos[p] - a.dpos[p]);
+              float cc[NP], ss[NP];
+#pragma unroll
+              for (int k = 0; k < NP; ++k)
+                sincos_rn(delta * a.inv_freq[j * NP + k], &ss[k], &cc[k]);
+              rotate_pairs<NP>(f, cc, ss);
+              ++seen;
+            }
+          }
+          pack_words<DT, W>(f, w[b]);
+        }
+        store_vec<VB>(dptr[b], w[b]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------------------
+namespace {
+
+struct Geometry {
+  int vb;        // vector bytes
+  int vpr;       // vectors per row
+  int tpr_log2;  // log2 threads per row
+};
+
+bool make_geometry(int64_t head_dim, int64_t esize, std::initializer_list<int64_t> byte_terms,
+                   bool rotate, Geometry* g) {
+  const int64_t row_bytes = head_dim * esize;
+  int vb = vec_bytes(byte_terms);
+  int row_vb = vec_bytes({row_bytes});
+  vb = vb < row_vb ? vb : row_vb;
+  if (vb < 4) return false;
+  if (rotate && vb < 2 * esize) return false;
+  g->vb = vb;
+  g->vpr = static_cast<int>(row_bytes / vb);
+  int64_t tpr = next_pow2(g->vpr);
+  if (tpr > kThreads) tpr = kThreads;
+  int lg = 0;
+  while ((int64_t{1} << lg) < tpr) ++lg;
+  g->tpr_log2 = lg;
+  return true;
+}
+
+template <int ROT, int SRCM, int DSTM>
+int launch_move(const char* fn, const MoveArgs& a0, int32_t dtype, const Geometry& g,
+                int grid_y, hipStream_t stream) {
+  MoveArgs a = a0;
+  a.vpr = g.vpr;
+  a.tpr_log2 = g.tpr_log2;
+  const int64_t rows_per_block = kThreads >> g.tpr_log2;
+  const int64_t gx = (a.num_pairs + rows_per_block - 1) / rows_per_block;
+  if (gx > 0x7fffffff || grid_y > 65535) return fail(fn, "grid too large");
+  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(grid_y));
+#define SB_MOVE_CASE(DT, VB)                                                              \
+  if (dtype == DT && g.vb == VB) {                                                        \
+    hipLaunchKernelGGL((move_rows_kernel<DT, VB, ROT, SRCM, DSTM>), grid, dim3(kThreads), \
+                       0, stream, a);                                                     \
+    return check_launch(fn);                                                              \
+  }
+  if (ROT == ROT_NONE) {
+    // Plain copies do not depend on the element type: move raw 32-bit words.
+    dtype = SB_DTYPE_F32;
+    SB_MOVE_CASE(SB_DTYPE_F32, 16)
+    SB_MOVE_CASE(SB_DTYPE_F32, 8)
+    SB_MOVE_CASE(SB_DTYPE_F32, 4)
+  } else {
+    SB_MOVE_CASE(SB_DTYPE_F32, 16)
+    SB_MOVE_CASE(SB_DTYPE_F32, 8)
+    SB_MOVE_CASE(SB_DTYPE_BF16, 16)
+    SB_MOVE_CASE(SB_DTYPE_BF16, 8)
+    SB_MOVE_CASE(SB_DTYPE_BF16, 4)
+    SB_MOVE_CASE(SB_DTYPE_F16, 16)
+    SB_MOVE_CASE(SB_DTYPE_F16, 8)
+    SB_MOVE_CASE(SB_DTYPE_F16, 4)
+  }
+#undef SB_MOVE_CASE
+  return fail(fn, "unsupported dtype / vector width combination");
+}
+
+bool valid_dtype(int32_t dtype) { return elem_size(dtype) != 0; }
+
+// Flat-position side: [.., S, D] indexed by position; strides in elements -> bytes.
+RowSide side_flat(void* base, const uint64_t* layers, int64_t s_layer, int64_t s_kv,
+                  int64_t s_head, int64_t s_seq, int64_t bound, int64_t es) {
+  RowSide s{};
+  s.base = static_cast<char*>(base);
+  s.layers = layers;
+  s.s_layer = s_layer * es;
+  s.s_kv = s_kv * es;
+  s.s_head = s_head * es;
+  s.s_row = s_seq * es;
+  s.s_pos = 0;
+  s.bound = bound;
+  return s;
+}
+
+// Paged side: kv_strides = (block, kv, head, pos, dim) in elements.
+RowSide side_paged(void* base, const uint64_t* layers, const int64_t* st, int64_t es) {
+  RowSide s{};
+  s.base = static_cast<char*>(base);
+  s.layers = layers;
+  s.s_layer = 0;
+  s.s_kv = st[1] * es;
+  s.s_head = st[2] * es;
+  s.s_row = st[0] * es;
+  s.s_pos = st[3] * es;
+  s.bound = 0;
+  return s;
+}
+
+// Dense staging side [P, planes, H, D] (contiguous), indexed by pair. With planes == 1 the
+// kv stride is 0, so whichever kv plane is moved lands at the start of each row.
+RowSide side_index(void* base, int64_t num_heads, int64_t head_dim, int64_t es, int planes) {
+  RowSide s{};
+  s.base = static_cast<char*>(base);
+  s.layers = nullptr;
+  s.s_layer = 0;
+  s.s_head = head_dim * es;
+  s.s_kv = planes == 2 ? num_heads * head_dim * es : 0;
+  s.s_row = planes * num_heads * head_dim * es;
+  s.s_pos = 0;
+  s.bound = 0;
+  return s;
+}
+
+int layers_per_group_for(int64_t num_layers, int64_t num_pairs) {
+  // Enough grid.y slices to fill the chip when there are few pairs; otherwise walk several
+  // layers per thread so cos/sin and index work are amortised.
+  if (num_pairs >= 8192) return static_cast<int>(num_layers < 4 ? num_layers : 4);
+  return 1;
+}
+
+}  // namespace
+}  // namespace sb
+
+using namespace sb;
+
+extern "C" int sb_scatter_donor_kv(void* target, const void* donor, const int32_t* donor_pos,
+                                   const int32_t* target_pos, int64_t num_pairs,
+                                   int64_t num_layers, int64_t num_heads, int64_t head_dim,
+                                   int64_t target_seq_len, int64_t donor_seq_len,
+                                   const int64_t* ts, const int64_t* ds, int32_t dtype,
+                                   void* stream) {
+  const char* fn = "sb_scatter_donor_kv";
+  clear_error();
+  if (num_pairs == 0 || num_layers == 0 || num_heads == 0 || head_dim == 0) return SB_OK;
+  if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
+  if (!target || !donor || !donor_pos || !target_pos || !ts || !ds)
+    return fail(fn, "null pointer argument");
+  if (ts[4] != 1 || ds[4] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
+  const int64_t es = elem_size(dtype);
+  Geometry g;
+  if (!make_geometry(head_dim, es,
+                     {reinterpret_cast<int64_t>(target), reinterpret_cast<int64_t>(donor),
+                      ts[0] * es, ts[1] * es, ts[2] * es, ts[3] * es, ds[0] * es, ds[1] * es,
+                      ds[2] * es, ds[3] * es},
+                     false, &g))
+    return fail(fn, "rows are not 4-byte aligned");
+  MoveArgs a{};
+  a.src = side_flat(const_cast<void*>(donor), nullptr, ds[0], ds[1], ds[2], ds[3],
+                    donor_seq_len, es);
+  a.dst = side_flat(target, nullptr, ts[0], ts[1], ts[2], ts[3], target_seq_len, es);
+  a.src_pos = donor_pos;
+  a.dst_pos = target_pos;
+  a.num_pairs = num_pairs;
+  a.num_heads = static_cast<int>(num_heads);
+  a.num_layers = static_cast<int>(num_layers);
+  a.layers_per_group = layers_per_group_for(num_layers, num_pairs);
+  a.kv_first = 0;
+  a.num_kv = 2;
+  const int groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
+  return launch_move<ROT_NONE, ROW_FLAT_POS, ROW_FLAT_POS>(fn, a, dtype, g, 2 * groups,
+                                                           static_cast<hipStream_t>(stream));
+}
+
+static int paged_scatter_impl(const char* fn, void* kv_base, const uint64_t* kv_layers,
+                              const void* donor_base, const uint64_t* donor_layers,
+                              int64_t num_layers, const int32_t* block_table,
+                              const int32_t* donor_pos, const int32_t* target_pos,
+                              const float* inv_freq, int64_t num_pairs, int64_t num_heads,
+                              int64_t block_size, int64_t head_dim, int64_t donor_seq_len,
+                              int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                              const int64_t* ks, const int64_t* ds, int32_t dtype,
+                              bool rope, void* stream) {
+  clear_error();
+  if (num_pairs == 0 || num_layers == 0 || num_heads == 0 || head_dim == 0) return SB_OK;
+  if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
+  if ((!kv_base && !kv_layers) || (!donor_base && !donor_layers) || !block_table ||
+      !donor_pos || !target_pos || !ks || !ds)
+    return fail(fn, "null pointer argument");
+  if (rope && !inv_freq) return fail(fn, "null inv_freq");
+  if (rope && (head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
+  if (block_size <= 0) return fail(fn, "block_size must be positive");
+  if (ks[4] != 1 || ds[3] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
+  const int64_t es = elem_size(dtype);
+  // Per-layer tables are checked for 16-byte alignment by the caller.
+  const int64_t kb = kv_layers ? 16 : reinterpret_cast<int64_t>(kv_base);
+  const int64_t db = donor_layers ? 16 : reinterpret_cast<int64_t>(donor_base);
+  Geometry g;
+  if (!make_geometry(head_dim, es,
+                     {kb, db, ks[0] * es, ks[1] * es, ks[2] * es, ks[3] * es, ds[0] * es,
+                      ds[1] * es, ds[2] * es},
+                     rope, &g))
+    return fail(fn, "rows are not aligned for vector access");
+  MoveArgs a{};
+  a.src = side_flat(const_cast<void*>(donor_base), donor_layers, 0, ds[0], ds[1], ds[2],
+                    donor_seq_len, es);
+  a.dst = side_paged(kv_base, kv_layers, ks, es);
+  a.src_pos = donor_pos;
+  a.dst_pos = target_pos;
+  a.block_table = block_table;
+  a.block_size = block_size;
+  a.nb_total = num_blocks_total;
+  a.nb_per_seq = num_blocks_per_seq;
+  a.inv_freq = inv_freq;
+  a.num_pairs = num_pairs;
+  a.num_heads = static_cast<int>(num_heads);
+  a.num_layers = static_cast<int>(num_layers);
+  a.layers_per_group = layers_per_group_for(num_layers, num_pairs);
+  a.kv_first = 0;
+  a.num_kv = 2;
+  const int groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rope)
+    return launch_move<ROT_DELTA, ROW_FLAT_POS, ROW_PAGED_POS>(fn, a, dtype, g, 2 * groups, st);
+  return launch_move<ROT_NONE, ROW_FLAT_POS, ROW_PAGED_POS>(fn, a, dtype, g, 2 * groups, st);
+}
+
+extern "C" int sb_scatter_donor_kv_paged(void* kv_cache, const void* donor_kv,
+                                         const int32_t* block_table, const int32_t* donor_pos,
+                                         const int32_t* target_pos, int64_t num_pairs,
+                                         int64_t num_heads, int64_t block_size,
+                                         int64_t head_dim, int64_t donor_seq_len,
+                                         int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                                         const int64_t* kv_strides, const int64_t* d_strides,
+                                         int32_t dtype, void* stream) {
+  return paged_scatter_impl("sb_scatter_donor_kv_paged", kv_cache, nullptr, donor_kv, nullptr,
+                            1, block_table, donor_pos, target_pos, nullptr, num_pairs,
+                            num_heads, block_size, head_dim, donor_seq_len, num_blocks_total,
+                            num_blocks_per_seq, kv_strides, d_strides, dtype, false, stream);
+}
+
+extern "C" int sb_scatter_donor_kv_paged_layers(
+    const uint64_t* kv_layer_ptrs, const uint64_t* donor_layer_ptrs, int64_t num_layers,
+    const int32_t* block_table, const int32_t* donor_pos, const int32_t* target_pos,
+    int64_t num_pairs, int64_t num_heads, int64_t block_size, int64_t head_dim,
+    int64_t donor_seq_len, int64_t num_blocks_total, int64_t num_blocks_per_seq,
+    const int64_t* kv_strides, const int64_t* d_strides, int32_t dtype, void* stream) {
+  if (!kv_layer_ptrs || !donor_layer_ptrs) {
+    clear_error();
+    if (num_pairs == 0 || num_layers == 0) return SB_OK;
+    return fail("sb_scatter_donor_kv_paged_layers", "null layer table");
+  }
+  return paged_scatter_impl("sb_scatter_donor_kv_paged_layers", nullptr, kv_layer_ptrs,
+                            nullptr, donor_layer_ptrs, num_layers, block_table, donor_pos,
+                            target_pos, nullptr, num_pairs, num_heads, block_size, head_dim,
+                            donor_seq_len, num_blocks_total, num_blocks_per_seq, kv_strides,
+                            d_strides, dtype, false, stream);
+}
+
+extern "C" int sb_rope_correct_scatter_paged(void* kv_cache, const void* donor_kv,
+                                             const int32_t* block_table,
+                                             const int32_t* donor_pos,
+                                             const int32_t* target_pos, const float* inv_freq,
+                                             int64_t num_pairs, int64_t num_heads,
+                                             int64_t block_size, int64_t head_dim,
+                                             int64_t donor_seq_len, int64_t num_blocks_total,
+                                             int64_t num_blocks_per_seq,
+                                             const int64_t* kv_strides,
+                                             const int64_t* d_strides, int32_t dtype,
+                                             void* stream) {
+  return paged_scatter_impl("sb_rope_correct_scatter_paged", kv_cache, nullptr, donor_kv,
+                            nullptr, 1, block_table, donor_pos, target_pos, inv_freq,
+                            num_pairs, num_heads, block_size, head_dim, donor_seq_len,
+                            num_blocks_total, num_blocks_per_seq, kv_strides, d_strides, dtype,
+                            true, stream);
+}
+
+extern "C" int sb_rope_correct_scatter_paged_layers(
+    const uint64_t* kv_layer_ptrs, const uint64_t* donor_layer_ptrs, int64_t num_layers,
+    const int32_t* block_table, const int32_t* donor_pos, const int32_t* target_pos,
+    const float* inv_freq, int64_t num_pairs, int64_t num_heads, int64_t block_size,
+    int64_t head_dim, int64_t donor_seq_len, int64_t num_blocks_total,
+    int64_t num_blocks_per_seq, const int64_t* kv_strides, const int64_t* d_strides,
+    int32_t dtype, void* stream) {
+  if (!kv_layer_ptrs || !donor_layer_ptrs) {
+    clear_error();
+    if (num_pairs == 0 || num_layers == 0) return SB_OK;
+    return fail("sb_rope_correct_scatter_paged_layers", "null layer table");
+  }
+  return paged_scatter_impl("sb_rope_correct_scatter_paged_layers", nullptr, kv_layer_ptrs,
+                            nullptr, donor_layer_ptrs, num_layers, block_table, donor_pos,
+                            target_pos, inv_freq, num_pairs, num_heads, block_size, head_dim,
+                            donor_seq_len, num_blocks_total, num_blocks_per_seq, kv_strides,
+                            d_strides, dtype, true, stream);
+}
+
+extern "C" int sb_rope_correct_k(void* out, const void* k, const int32_t* donor_pos,
+                                 const int32_t* target_pos, const float* inv_freq,
+                                 int32_t* workspace, int64_t num_pairs, int64_t num_layers,
+                                 int64_t num_heads, int64_t seq_len, int64_t head_dim,
+                                 const int64_t* os, const int64_t* ks, int32_t dtype,
+                                 void* stream) {
+  const char* fn = "sb_rope_correct_k";
+  clear_error();
+  if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
+  if (!out || !k || !os || !ks) return fail(fn, "null pointer argument");
+  if (num_layers == 0 || num_heads == 0 || seq_len == 0 || head_dim == 0) return SB_OK;
+  if (num_pairs > 0 && (!donor_pos || !target_pos || !inv_freq))
+    return fail(fn, "null pointer argument");
+  if ((head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
+  if (os[3] != 1 || ks[3] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
+  if (num_pairs > 0x7ffffffe) return fail(fn, "too many pairs");
+  const int64_t es = elem_size(dtype);
+  Geometry g;
+  if (!make_geometry(head_dim, es,
+                     {reinterpret_cast<int64_t>(out), reinterpret_cast<int64_t>(k), os[0] * es,
+                      os[1] * es, os[2] * es, ks[0] * es, ks[1] * es, ks[2] * es},
+                     true, &g))
+    return fail(fn, "rows are not aligned for vector access");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool in_place = out == k;
+  if (num_pairs == 0 && in_place) return SB_OK;
+  if (!workspace) return fail(fn, "null workspace");
+
+  // Per-position pair index: counts in ws[0:S], (P - first pair) in ws[S:2S].
+  int32_t* ws = workspace;
+  const int64_t n = 2 * seq_len;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     st, ws, n, 0);
+  if (num_pairs > 0)
+    hipLaunchKernelGGL(rope_index_kernel, dim3(static_cast<unsigned>((num_pairs + 255) / 256)),
+                       dim3(256), 0, st, donor_pos, num_pairs, seq_len, ws);
+  {
+    int rc = check_launch(fn);
+    if (rc) return rc;
+  }
+  RopeRowsArgs a{};
+  a.out = static_cast<char*>(out);
+  a.k = static_cast<const char*>(k);
+  a.o_s_layer = os[0] * es; a.o_s_head = os[1] * es; a.o_s_seq = os[2] * es;
+  a.k_s_layer = ks[0] * es; a.k_s_head = ks[1] * es; a.k_s_seq = ks[2] * es;
+  a.dpos = donor_pos;
+  a.tpos = target_pos;
+  a.ws = ws;
+  a.inv_freq = inv_freq;
+  a.num_pairs = num_pairs;
+  a.seq_len = seq_len;
+  a.num_layers = static_cast<int>(num_layers);
+  a.num_heads = static_cast<int>(num_heads);
+  a.in_place = in_place ? 1 : 0;
+  a.vpr = g.vpr;
+  a.tpr_log2 = g.tpr_log2;
+  const int total_rows = static_cast<int>(num_layers * num_heads);
+  // Split the (layer, head) rows over grid.y so that short sequences still fill 256 CUs.
+  const int64_t rows_per_block = kThreads >> g.tpr_log2;
+  const int64_t gx = (seq_len + rows_per_block - 1) / rows_per_block;
+  int splits = 1;
+  while (splits < total_rows && gx * splits < 2048) splits *= 2;
+  if (splits > total_rows) splits = total_rows;
+  a.rows_per_group = (total_rows + splits - 1) / splits;
+  const int gy = (total_rows + a.rows_per_group - 1) / a.rows_per_group;
+  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+#define SB_ROWS_CASE(DT, VB)                                                              \
+  if (dtype == DT && g.vb == VB) {                                                        \
+    hipLaunchKernelGGL((rope_rows_kernel<DT, VB>), grid, dim3(kThreads), 0, st, a);       \
+    return check_launch(fn);                                                              \
+  }
+  SB_ROWS_CASE(SB_DTYPE_F32, 16)
+  SB_ROWS_CASE(SB_DTYPE_F32, 8)
+  SB_ROWS_CASE(SB_DTYPE_BF16, 16)
+  SB_ROWS_CASE(SB_DTYPE_BF16, 8)
+  SB_ROWS_CASE(SB_DTYPE_BF16, 4)
+  SB_ROWS_CASE(SB_DTYPE_F16, 16)
+  SB_ROWS_CASE(SB_DTYPE_F16, 8)
+  SB_ROWS_CASE(SB_DTYPE_F16, 4)
+#undef SB_ROWS_CASE
+  return fail(fn, "unsupported dtype / vector width combination");
+}
+
+extern "C" int sb_apply_rope_delta_inplace(void* k_plane, const int32_t* block_table,
+                                           const int32_t* positions, const int32_t* repeat,
+                                           int64_t num_positions, int64_t delta,
+                                           const float* inv_freq, int64_t num_heads,
+                                           int64_t block_size, int64_t head_dim,
+                                           int64_t num_blocks_total,
+                                           int64_t num_blocks_per_seq, const int64_t* ks,
+                                           int32_t dtype, void* stream) {
+  const char* fn = "sb_apply_rope_delta_inplace";
+  clear_error();
+  if (num_positions == 0 || num_heads == 0 || head_dim == 0 || delta == 0) return SB_OK;
+  if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
+  if (!k_plane || !block_table || !positions || !inv_freq || !ks)
+    return fail(fn, "null pointer argument");
+  if ((head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
+  if (block_size <= 0) return fail(fn, "block_size must be positive");
+  if (ks[3] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
+  const int64_t es = elem_size(dtype);
+  Geometry g;
+  if (!make_geometry(head_dim, es,
+                     {reinterpret_cast<int64_t>(k_plane), ks[0] * es, ks[1] * es, ks[2] * es},
+                     true, &g))
+    return fail(fn, "rows are not aligned for vector access");
+  // k_strides = (block, head, pos, dim); expressed as a paged side with a single kv plane.
+  const int64_t st5[5] = {ks[0], 0, ks[1], ks[2], ks[3]};
+  MoveArgs a{};
+  a.src = side_paged(k_plane, nullptr, st5, es);
+  a.dst = a.src;
+  a.src_pos = positions;
+  a.dst_pos = positions;
+  a.repeat = repeat;
+  a.block_table = block_table;
+  a.block_size = block_size;
+  a.nb_total = num_blocks_total;
+  a.nb_per_seq = num_blocks_per_seq;
+  a.inv_freq = inv_freq;
+  a.const_delta = delta;
+  a.num_pairs = num_positions;
+  a.num_heads = static_cast<int>(num_heads);
+  a.num_layers = 1;
+  a.layers_per_group = 1;
+  a.kv_first = 0;
+  a.num_kv = 1;
+  return launch_move<ROT_CONST, ROW_PAGED_POS, ROW_PAGED_POS>(fn, a, dtype, g, 1,
+                                                              static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sb_permute_paged_kv_with_rope(void* kv_cache, const int32_t* block_table,
+                                             const int32_t* src_pos, const int32_t* tgt_pos,
+                                             const float* inv_freq, void* workspace,
+                                             int64_t num_pairs, int64_t num_heads,
+                                             int64_t block_size, int64_t head_dim,
+                                             int64_t num_blocks_total,
+                                             int64_t num_blocks_per_seq, const int64_t* ks,
+                                             int32_t dtype, void* stream) {
+  const char* fn = "sb_permute_paged_kv_with_rope";
+  clear_error();
+  if (num_pairs == 0 || num_heads == 0 || head_dim == 0) return SB_OK;
+  if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
+  if (!kv_cache || !block_table || !src_pos || !tgt_pos || !inv_freq || !workspace || !ks)
+    return fail(fn, "null pointer argument");
+  if ((head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
+  if (block_size <= 0) return fail(fn, "block_size must be positive");
+  if (ks[4] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
+  const int64_t es = elem_size(dtype);
+  Geometry g;
+  if (!make_geometry(head_dim, es,
+                     {reinterpret_cast<int64_t>(kv_cache), reinterpret_cast<int64_t>(workspace),
+                      ks[0] * es, ks[1] * es, ks[2] * es, ks[3] * es},
+                     true, &g))
+    return fail(fn, "rows are not aligned for vector access");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // Phase 1: snapshot every source row (K and V) into workspace[P, 2, H, D].
+  MoveArgs a{};
+  a.src = side_paged(kv_cache, nullptr, ks, es);
+  a.dst = side_index(workspace, num_heads, head_dim, es, 2);
+  a.src_pos = src_pos;
+  a.dst_pos = tgt_pos;
+  a.block_table = block_table;
+  a.block_size = block_size;
+  a.nb_total = num_blocks_total;
+  a.nb_per_seq = num_blocks_per_seq;
+  a.inv_freq = inv_freq;
+  a.num_pairs = num_pairs;
+  a.num_heads = static_cast<int>(num_heads);
+  a.num_layers = 1;
+  a.layers_per_group = 1;
+  a.kv_first = 0;
+  a.num_kv = 2;
+  int rc = launch_move<ROT_NONE, ROW_PAGED_POS, ROW_INDEX>(fn, a, dtype, g, 2, st);
+  if (rc) return rc;
+  // Phase 2: write every target: V copied, K rotated by (tgt - src).
+  MoveArgs b = a;
+  b.src = a.dst;
+  b.dst = a.src;
+  b.src_index_check = 1;
+  return launch_move<ROT_DELTA, ROW_INDEX, ROW_PAGED_POS>(fn, b, dtype, g, 2, st);
+}
+
+extern "C" int sb_nope_permute_paged_kv(void* kv_cache, const int32_t* block_table,
+                                        const int32_t* src_pos, const int32_t* tgt_pos,
+                                        int64_t num_pairs, const int32_t* v_src_pos,
+                                        const int32_t* v_tgt_pos, int64_t num_v_pairs,
+                                        const float* inv_freq, void* workspace,
+                                        int64_t num_heads, int64_t block_size,
+                                        int64_t head_dim, int64_t num_blocks_total,
+                                        int64_t num_blocks_per_seq, const int64_t* ks,
+                                        int32_t dtype, void* stream) {
+  const char* fn = "sb_nope_permute_paged_kv";
+  clear_error();
+  if ((num_pairs == 0 && num_v_pairs == 0) || num_heads == 0 || head_dim == 0) return SB_OK;
+  if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
+  if (!kv_cache || !block_table || !inv_freq || !workspace || !ks)
+    return fail(fn, "null pointer argument");
+  if (num_pairs > 0 && (!src_pos || !tgt_pos)) return fail(fn, "null pointer argument");
+  if (num_v_pairs > 0 && (!v_src_pos || !v_tgt_pos)) return fail(fn, "null pointer argument");
+  if ((head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
+  if (block_size <= 0) return fail(fn, "block_size must be positive");
+  if (ks[4] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
+  const int64_t es = elem_size(dtype);
+  Geometry g;
+  if (!make_geometry(head_dim, es,
+                     {reinterpret_cast<int64_t>(kv_cache), reinterpret_cast<int64_t>(workspace),
+                      ks[0] * es, ks[1] * es, ks[2] * es, ks[3] * es},
+                     true, &g))
+    return fail(fn, "rows are not aligned for vector access");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws_k = static_cast<char*>(workspace);
+  char* ws_v = ws_k + num_pairs * num_heads * head_dim * es;
+
+  MoveArgs base{};
+  base.block_table = block_table;
+  base.block_size = block_size;
+  base.nb_total = num_blocks_total;
+  base.nb_per_seq = num_blocks_per_seq;
+  base.inv_freq = inv_freq;
+  base.num_heads = static_cast<int>(num_heads);
+  base.num_layers = 1;
+  base.layers_per_group = 1;
+  base.num_kv = 1;
+  const RowSide cache = side_paged(kv_cache, nullptr, ks, es);
+  int rc;
+  // Snapshot K at every source (kv plane 0) and V at every resolved V source (plane 1)
+  // before anything is written.
+  if (num_pairs > 0) {
+    MoveArgs a = base;
+    a.src = cache;
+    a.dst = side_index(ws_k, num_heads, head_dim, es, 1);
+    a.src_pos = src_pos;
+    a.dst_pos = tgt_pos;
+    a.num_pairs = num_pairs;
+    a.kv_first = 0;
+    rc = launch_move<ROT_NONE, ROW_PAGED_POS, ROW_INDEX>(fn, a, dtype, g, 1, st);
+    if (rc) return rc;
+  }
+  if (num_v_pairs > 0) {
+    MoveArgs a = base;
+    a.src = cache;
+    a.dst = side_index(ws_v, num_heads, head_dim, es, 1);
+    a.src_pos = v_src_pos;
+    a.dst_pos = v_tgt_pos;
+    a.num_pairs = num_v_pairs;
+    a.kv_first = 1;
+    rc = launch_move<ROT_NONE, ROW_PAGED_POS, ROW_INDEX>(fn, a, dtype, g, 1, st);
+    if (rc) return rc;
+  }
+  if (num_v_pairs > 0) {
+    MoveArgs a = base;
+    a.src = side_index(ws_v, num_heads, head_dim, es, 1);
+    a.dst = cache;
+    a.src_pos = v_src_pos;
+    a.dst_pos = v_tgt_pos;
+    a.num_pairs = num_v_pairs;
+    a.kv_first = 1;
+    a.src_index_check = 1;
+    rc = launch_move<ROT_NONE, ROW_INDEX, ROW_PAGED_POS>(fn, a, dtype, g, 1, st);
+    if (rc) return rc;
+  }
+  if (num_pairs > 0) {
+    MoveArgs a = base;
+    a.src = side_index(ws_k, num_heads, head_dim, es, 1);
+    a.dst = cache;
+    a.src_pos = src_pos;
+    a.dst_pos = tgt_pos;
+    a.num_pairs = num_pairs;
+    a.kv_first = 0;
+    a.src_index_check = 1;
+    rc = launch_move<ROT_NOPE, ROW_INDEX, ROW_PAGED_POS>(fn, a, dtype, g, 1, st);
+    if (rc) return rc;
+  }
+  return SB_OK;
+}

@@ -1,0 +1,401 @@
+"""RoPE delta correction of reused donor K on MI355X — drop-in for
+``semblend_core.rope_correction`` (semblend_core/rope_correction.py).
+
+Same function names, parameters, defaults, return values and in-place conventions as the
+reference module. Every function runs hand-written HIP kernels from ``libsemblend_hip.so``
+through its C ABI on torch's current stream; CPU tensors are rejected.
+
+Convention (semblend_core/rope_correction.py:163-178, :317-326): interleaved (GPT-J) pairs
+``(2i, 2i+1)`` rotated by ``theta = delta * inv_freq[i]`` with
+``inv_freq[i] = 1 / base ** (2i / head_dim)``:
+
+    e' = e * cos(theta) - o * sin(theta)
+    o' = e * sin(theta) + o * cos(theta)
+
+computed in fp32 and rounded once to the cache dtype (the reference's CPU path, :328; its
+Triton kernels store fp16 regardless of the cache dtype, :183-190, which is not reproduced).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+# Kept for import compatibility with callers that re-export it
+# (synapse_kv_connector/rope_correction.py:8-21). There is no Triton here; the kernels are
+# HIP and their availability is HAS_HIP.
+HAS_TRITON = False
+HAS_HIP = _lib.available()
+
+__all__ = [
+    "HAS_TRITON",
+    "HAS_HIP",
+    "apply_rope_delta_inplace",
+    "inv_freq_table",
+    "nope_permute_paged_kv",
+    "permute_paged_kv_with_rope",
+    "rope_correct_k",
+    "rope_correct_k_inplace",
+    "rope_correct_scatter_paged",
+    "rope_correct_scatter_paged_layers",
+]
+
+_INV_FREQ_CACHE: dict[tuple[float, int, torch.device], torch.Tensor] = {}
+
+
+def inv_freq_table(rope_base: float, head_dim: int, device: torch.device) -> torch.Tensor:
+    """fp32 ``1 / base ** (arange(0, D, 2) / D)`` on ``device``, cached.
+
+    The table is evaluated with the reference's exact torch expression
+    (semblend_core/rope_correction.py:234-238) on the host and copied once to the device, so
+    the angles ``delta * inv_freq`` are bit-identical to the reference's: at |delta| ~ 4096 a
+    one-ulp difference in inv_freq would move the angle by ~5e-4 rad.
+    """
+    key = (float(rope_base), int(head_dim), torch.device(device))
+    tab = _INV_FREQ_CACHE.get(key)
+    if tab is None:
+        host = 1.0 / (rope_base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+        tab = host.to(device)
+        _INV_FREQ_CACHE[key] = tab
+    return tab
+
+
+def _check_head_dim(head_dim: int, actual: int, fn: str) -> None:
+    if head_dim != actual:
+        raise ValueError(
+            f"{fn}: head_dim={head_dim} does not match the tensor's last dimension {actual}"
+        )
+    if head_dim % 2:
+        raise ValueError(f"{fn}: head_dim must be even for RoPE, got {head_dim}")
+
+
+def rope_correct_scatter_paged(
+    kv_cache: torch.Tensor,
+    donor_kv: torch.Tensor,
+    block_table: torch.Tensor,
+    donor_positions: torch.Tensor,
+    target_positions: torch.Tensor,
+    rope_base: float = 10000.0,
+    head_dim: int | None = None,
+) -> torch.Tensor:
+    """Scatter donor KV into a paged cache, rotating K by ``target - donor``; V is copied.
+
+    kv_cache: [num_blocks, 2, num_heads, block_size, head_dim] (any strides);
+    donor_kv: [2, num_heads, donor_seq_len, head_dim]; block_table: [num_blocks_per_seq].
+    Returns kv_cache (modified in place). Pairs whose donor position, logical block or
+    physical block is out of range are skipped.
+    Reference: semblend_core/rope_correction.py:193-282.
+    """
+    num_pairs = donor_positions.shape[0]
+    if num_pairs == 0:
+        return kv_cache
+    nb_total, _, num_heads, block_size, hd = kv_cache.shape
+    head_dim = hd if head_dim is None else head_dim
+    _check_head_dim(head_dim, hd, "rope_correct_scatter_paged")
+    dev = _lib.require_device(kv_cache, donor_kv)
+    if donor_kv.dtype != kv_cache.dtype:
+        raise TypeError("donor_kv and kv_cache must share a dtype")
+    bt = _lib.as_index(block_table, dev)
+    dpos = _lib.as_index(donor_positions, dev)
+    tpos = _lib.as_index(target_positions, dev)
+    inv_freq = inv_freq_table(rope_base, head_dim, dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_rope_correct_scatter_paged",
+            kv_cache.data_ptr(), donor_kv.data_ptr(), bt.data_ptr(), dpos.data_ptr(),
+            tpos.data_ptr(), inv_freq.data_ptr(), num_pairs, num_heads, block_size, head_dim,
+            donor_kv.shape[2], nb_total, bt.shape[0], _lib.strides(kv_cache),
+            _lib.strides(donor_kv), _lib.dtype_code(kv_cache), _lib.stream_handle(dev),
+        )
+    return kv_cache
+
+
+def rope_correct_scatter_paged_layers(
+    kv_caches: list[torch.Tensor],
+    donor_kvs: list[torch.Tensor],
+    block_table: torch.Tensor,
+    donor_positions: torch.Tensor,
+    target_positions: torch.Tensor,
+    rope_base: float = 10000.0,
+) -> list[torch.Tensor]:
+    """``rope_correct_scatter_paged`` over many layers in one launch.
+
+    kv_caches / donor_kvs: one tensor per layer, all with the same shape, strides and dtype.
+    cos/sin of each pair are evaluated once and reused for every layer and head. Extension
+    with no reference counterpart; it replaces a per-layer loop around
+    ``rope_correct_scatter_paged`` (semblend/integration/trtllm/pytorch_backend.py:106-154).
+    """
+    if len(kv_caches) != len(donor_kvs):
+        raise ValueError("kv_caches and donor_kvs must have the same length")
+    num_pairs = donor_positions.shape[0]
+    if num_pairs == 0 or not kv_caches:
+        return kv_caches
+    ref, dref = kv_caches[0], donor_kvs[0]
+    nb_total, _, num_heads, block_size, head_dim = ref.shape
+    _check_head_dim(head_dim, head_dim, "rope_correct_scatter_paged_layers")
+    dev = _lib.require_device(*kv_caches, *donor_kvs)
+    _check_uniform(kv_caches, "kv_caches")
+    _check_uniform(donor_kvs, "donor_kvs")
+    if dref.dtype != ref.dtype:
+        raise TypeError("donor_kvs and kv_caches must share a dtype")
+    kv_tab = _layer_table(kv_caches, dev)
+    d_tab = _layer_table(donor_kvs, dev)
+    bt = _lib.as_index(block_table, dev)
+    dpos = _lib.as_index(donor_positions, dev)
+    tpos = _lib.as_index(target_positions, dev)
+    inv_freq = inv_freq_table(rope_base, head_dim, dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_rope_correct_scatter_paged_layers",
+            kv_tab.data_ptr(), d_tab.data_ptr(), len(kv_caches), bt.data_ptr(),
+            dpos.data_ptr(), tpos.data_ptr(), inv_freq.data_ptr(), num_pairs, num_heads,
+            block_size, head_dim, dref.shape[2], nb_total, bt.shape[0], _lib.strides(ref),
+            _lib.strides(dref), _lib.dtype_code(ref), _lib.stream_handle(dev),
+        )
+    return kv_caches
+
+
+def _check_uniform(ts: list[torch.Tensor], name: str) -> None:
+    t0 = ts[0]
+    for t in ts[1:]:
+        if t.shape != t0.shape or t.stride() != t0.stride() or t.dtype != t0.dtype:
+            raise ValueError(f"all {name} must share shape, strides and dtype")
+    for t in ts:
+        if t.data_ptr() % 16:
+            raise ValueError(f"{name} base addresses must be 16-byte aligned")
+
+
+def _layer_table(ts: list[torch.Tensor], dev: torch.device) -> torch.Tensor:
+    return torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64).to(dev)
+
+
+def _rope_k(out: torch.Tensor, k: torch.Tensor, dpos, tpos, head_dim, rope_base) -> None:
+    dev = _lib.require_device(k, out)
+    if k.dim() == 3:
+        k4, o4 = k.unsqueeze(0), out.unsqueeze(0)
+    elif k.dim() == 4:
+        k4, o4 = k, out
+    else:
+        raise ValueError("k_tensor must be [H, S, D] or [L, H, S, D]")
+    num_layers, num_heads, seq_len, hd = k4.shape
+    _check_head_dim(head_dim, hd, "rope_correct_k")
+    d = _lib.as_index(dpos, dev)
+    t = _lib.as_index(tpos, dev)
+    if d.shape[0] != t.shape[0]:
+        raise ValueError("donor_positions and target_positions differ in length")
+    inv_freq = inv_freq_table(rope_base, head_dim, dev)
+    ws = torch.empty(2 * seq_len, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_rope_correct_k",
+            o4.data_ptr(), k4.data_ptr(), d.data_ptr(), t.data_ptr(), inv_freq.data_ptr(),
+            ws.data_ptr(), d.shape[0], num_layers, num_heads, seq_len, head_dim,
+            _lib.strides(o4), _lib.strides(k4), _lib.dtype_code(k4), _lib.stream_handle(dev),
+        )
+
+
+def rope_correct_k(
+    k_tensor: torch.Tensor,
+    donor_positions: torch.Tensor,
+    target_positions: torch.Tensor,
+    head_dim: int = 128,
+    rope_base: float = 10000.0,
+) -> torch.Tensor:
+    """Return a copy of ``k_tensor`` whose rows at the donor positions are rotated.
+
+    k_tensor: [num_heads, seq_len, head_dim] or [num_layers, num_heads, seq_len, head_dim].
+    For each pair i (in order) the row at ``donor_positions[i]`` is rotated by
+    ``target_positions[i] - donor_positions[i]`` and rounded to the tensor dtype; a row named
+    by several pairs is rotated once per pair. The input is not modified.
+    Reference: semblend_core/rope_correction.py:336-399.
+    """
+    _lib.require_device(k_tensor)
+    out = torch.empty_like(k_tensor)
+    if k_tensor.stride(-1) != 1:
+        k_tensor = k_tensor.contiguous()
+    if out.stride(-1) != 1:
+        out = torch.empty_like(k_tensor, memory_format=torch.contiguous_format)
+    _rope_k(out, k_tensor, donor_positions, target_positions, head_dim, rope_base)
+    return out
+
+
+def rope_correct_k_inplace(
+    k_tensor: torch.Tensor,
+    donor_positions: torch.Tensor,
+    target_positions: torch.Tensor,
+    head_dim: int = 128,
+    rope_base: float = 10000.0,
+) -> torch.Tensor:
+    """In-place form of :func:`rope_correct_k` (same result, written back into k_tensor).
+
+    Only rows named by a pair are read and written. Extension with no reference counterpart.
+    """
+    _lib.require_device(k_tensor)
+    if k_tensor.stride(-1) != 1:
+        work = k_tensor.contiguous()
+        _rope_k(work, work, donor_positions, target_positions, head_dim, rope_base)
+        k_tensor.copy_(work)
+        return k_tensor
+    _rope_k(k_tensor, k_tensor, donor_positions, target_positions, head_dim, rope_base)
+    return k_tensor
+
+
+def permute_paged_kv_with_rope(
+    kv_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    permutation: list[tuple[int, int]],
+    rope_base: float = 10000.0,
+) -> None:
+    """Move (source, target) logical positions inside a paged cache, rotating K by
+    ``target - source``; V is copied.
+
+    Every source row is read before any target row is written (the reference snapshots all
+    sources first, semblend_core/rope_correction.py:437-448), so overlapping permutations
+    such as swaps are exact. kv_cache layout: [num_blocks, 2, num_heads, block_size, head_dim].
+    Reference: semblend_core/rope_correction.py:407-476.
+    """
+    if not permutation:
+        return
+    dev = _lib.require_device(kv_cache)
+    nb_total, _, num_heads, block_size, head_dim = kv_cache.shape
+    _check_head_dim(head_dim, head_dim, "permute_paged_kv_with_rope")
+    src = torch.tensor([p[0] for p in permutation], dtype=torch.int32).to(dev)
+    tgt = torch.tensor([p[1] for p in permutation], dtype=torch.int32).to(dev)
+    bt = _lib.as_index(block_table, dev)
+    inv_freq = inv_freq_table(rope_base, head_dim, dev)
+    ws = torch.empty((len(permutation), 2, num_heads, head_dim), dtype=kv_cache.dtype,
+                     device=dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_permute_paged_kv_with_rope",
+            kv_cache.data_ptr(), bt.data_ptr(), src.data_ptr(), tgt.data_ptr(),
+            inv_freq.data_ptr(), ws.data_ptr(), len(permutation), num_heads, block_size,
+            head_dim, nb_total, bt.shape[0], _lib.strides(kv_cache), _lib.dtype_code(kv_cache),
+            _lib.stream_handle(dev),
+        )
+
+
+def _sequential_v_moves(permutation: list[tuple[int, int]]) -> list[tuple[int, int]]:
+    """Resolve a sequence of in-place copies ``V[t] = V[s]`` (done in list order) into
+    (original source, target) pairs, one per distinct target, with the same final contents.
+
+    The reference copies V rows one pair at a time (semblend_core/rope_correction.py:650-653),
+    so a later pair reads what an earlier pair wrote. Tracking, for every written position,
+    which original row it now holds reproduces that outcome with a single snapshot-and-write
+    pass. Positions are logical; distinct logical blocks are assumed to map to distinct
+    physical blocks, as in engine block tables.
+    """
+    holds: dict[int, int] = {}
+    for s, t in permutation:
+        holds[t] = holds.get(s, s)
+    return list(holds.items())
+
+
+def nope_permute_paged_kv(
+    kv_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    permutation: list[tuple[int, int]],
+    rope_base: float = 10000.0,
+) -> None:
+    """NoPE two-step correction: ``K[tgt] = R(tgt) R(-src) K[src]``; V copied.
+
+    K rows are read before any K row is written; V rows follow the reference's sequential
+    copy semantics (see ``_sequential_v_moves``). Both rotations run in fp32 with one
+    rounding to the cache dtype.
+    Reference: semblend_core/rope_correction.py:599-697 (CPU path :786-823).
+    """
+    if not permutation:
+        return
+    dev = _lib.require_device(kv_cache)
+    nb_total, _, num_heads, block_size, head_dim = kv_cache.shape
+    _check_head_dim(head_dim, head_dim, "nope_permute_paged_kv")
+    src = torch.tensor([p[0] for p in permutation], dtype=torch.int32).to(dev)
+    tgt = torch.tensor([p[1] for p in permutation], dtype=torch.int32).to(dev)
+    vmoves = _sequential_v_moves(permutation)
+    # holds maps target -> original source; emit (source, target) pairs.
+    vsrc = torch.tensor([s for _, s in vmoves], dtype=torch.int32).to(dev)
+    vtgt = torch.tensor([t for t, _ in vmoves], dtype=torch.int32).to(dev)
+    bt = _lib.as_index(block_table, dev)
+    inv_freq = inv_freq_table(rope_base, head_dim, dev)
+    ws = torch.empty((len(permutation) + len(vmoves), num_heads, head_dim),
+                     dtype=kv_cache.dtype, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_nope_permute_paged_kv",
+            kv_cache.data_ptr(), bt.data_ptr(), src.data_ptr(), tgt.data_ptr(),
+            len(permutation), vsrc.data_ptr(), vtgt.data_ptr(), len(vmoves),
+            inv_freq.data_ptr(), ws.data_ptr(), num_heads, block_size, head_dim, nb_total,
+            bt.shape[0], _lib.strides(kv_cache), _lib.dtype_code(kv_cache),
+            _lib.stream_handle(dev),
+        )
+
+
+def apply_rope_delta_inplace(
+    kv_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    positions: list[int],
+    delta: int,
+    rope_base: float = 10000.0,
+) -> int:
+    """Rotate K at the given logical positions by ``delta`` in place; V untouched.
+
+    Accepts the vLLM flash-attn layout [2, num_blocks, block_size, num_kv_heads, head_dim]
+    and the standard [num_blocks, 2, num_heads, block_size, head_dim], detected exactly as
+    the reference does (semblend_core/rope_correction.py:740). Positions whose logical block
+    lies beyond the block table are skipped; a position listed k times is rotated k times.
+    Returns the number of positions processed (duplicates counted), or 0 for delta == 0 or
+    an empty list. Reference: semblend_core/rope_correction.py:699-783.
+    """
+    if delta == 0 or not positions:
+        return 0
+    dev = _lib.require_device(kv_cache)
+    is_vllm_layout = kv_cache.shape[0] == 2 and (kv_cache.ndim == 5 and kv_cache.shape[1] != 2)
+    if is_vllm_layout:
+        head_dim = kv_cache.shape[4]
+        block_size = kv_cache.shape[2]
+        num_heads = kv_cache.shape[3]
+        nb_total = kv_cache.shape[1]
+        k_plane = kv_cache[0]                     # [NB, bs, H, D]
+        kst = (k_plane.stride(0), k_plane.stride(2), k_plane.stride(1), k_plane.stride(3))
+    else:
+        head_dim = kv_cache.shape[4]
+        block_size = kv_cache.shape[3]
+        num_heads = kv_cache.shape[2]
+        nb_total = kv_cache.shape[0]
+        k_plane = kv_cache[:, 0]                  # [NB, H, bs, D]
+        kst = (k_plane.stride(0), k_plane.stride(1), k_plane.stride(2), k_plane.stride(3))
+    _check_head_dim(head_dim, head_dim, "apply_rope_delta_inplace")
+    nbs = block_table.shape[0]
+    # Host-side normalisation with Python index semantics (negative positions index blocks
+    # from the end of the table, as block_table[pos // block_size] does in the reference).
+    counts: dict[int, int] = {}
+    modified = 0
+    for pos in positions:
+        blk_idx = pos // block_size
+        if blk_idx >= nbs:
+            continue
+        if blk_idx < -nbs:
+            raise IndexError(f"position {pos} indexes block {blk_idx} of a {nbs}-entry table")
+        if blk_idx < 0:
+            blk_idx += nbs
+        logical = blk_idx * block_size + pos % block_size
+        counts[logical] = counts.get(logical, 0) + 1
+        modified += 1
+    if not counts:
+        return 0
+    pos_t = torch.tensor(list(counts.keys()), dtype=torch.int32).to(dev)
+    rep_t = None
+    if any(c != 1 for c in counts.values()):
+        rep_t = torch.tensor(list(counts.values()), dtype=torch.int32).to(dev)
+    bt = _lib.as_index(block_table, dev)
+    inv_freq = inv_freq_table(rope_base, head_dim, dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_apply_rope_delta_inplace",
+            k_plane.data_ptr(), bt.data_ptr(), pos_t.data_ptr(),
+            None if rep_t is None else rep_t.data_ptr(), len(counts), int(delta),
+            inv_freq.data_ptr(), num_heads, block_size, head_dim, nb_total, nbs,
+            _lib.i64_array(kst), _lib.dtype_code(kv_cache), _lib.stream_handle(dev),
+        )
+    return modified

@@ -1,0 +1,426 @@
+"""SemBlend partial-prefill kernels on MI355X — drop-in for ``semblend_core.triton_kernels``
+(semblend_core/triton_kernels.py).
+
+The module keeps the reference's names, signatures, defaults and return conventions:
+
+* ``scatter_donor_kv`` / ``scatter_donor_kv_paged`` — donor KV copied into the target cache,
+  in place, bit-exact (HIP row mover, 16-byte vector loads);
+* ``masked_qkv_projection`` — projection for compute rows only, reuse rows zero;
+* ``partial_prefill_attention`` — causal attention for compute rows only, zero elsewhere
+  (bf16/fp16 MFMA kernel with an fp32 online softmax; fp32 inputs take an fp32 kernel);
+* ``partial_prefill`` / ``PartialPrefillResult`` — the single-layer orchestrator.
+
+Extensions with no reference counterpart: ``scatter_donor_kv_paged_layers`` (many layers in
+one launch) and ``partial_prefill_attention_paged`` (GQA over a paged cache for a compact
+set of query rows). CPU tensors are rejected: the kernels exist only for HIP devices.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+# Import-compatibility flag (the reference exports it, semblend_core/triton_kernels.py:42-50).
+# There is no Triton here; HAS_HIP reports whether the HIP kernel library loaded.
+HAS_TRITON = False
+HAS_HIP = _lib.available()
+
+__all__ = [
+    "HAS_TRITON",
+    "HAS_HIP",
+    "PartialPrefillResult",
+    "masked_qkv_projection",
+    "partial_prefill",
+    "partial_prefill_attention",
+    "partial_prefill_attention_paged",
+    "scatter_donor_kv",
+    "scatter_donor_kv_paged",
+    "scatter_donor_kv_paged_layers",
+]
+
+
+# ------------------------------------------------------------------------------------------
+# Donor-KV scatter
+# ------------------------------------------------------------------------------------------
+
+def _contig_last(t: torch.Tensor) -> tuple[torch.Tensor, bool]:
+    """(tensor with unit stride in the last dim, whether it is a temporary copy)."""
+    if t.stride(-1) == 1:
+        return t, False
+    return t.contiguous(), True
+
+
+def scatter_donor_kv(
+    target: torch.Tensor,
+    donor: torch.Tensor,
+    donor_positions: torch.Tensor,
+    target_positions: torch.Tensor,
+) -> torch.Tensor:
+    """``target[:, :, :, t, :] = donor[:, :, :, d, :]`` for every (d, t) pair, all layers.
+
+    target: [num_layers, 2, num_heads, target_seq_len, head_dim];
+    donor:  [num_layers, 2, num_heads, donor_seq_len, head_dim].
+    Pairs with d >= donor_seq_len or t >= target_seq_len (or negative) are skipped.
+    Returns target (modified in place). Reference: semblend_core/triton_kernels.py:132-191.
+    """
+    num_pairs = donor_positions.shape[0]
+    if num_pairs == 0:
+        return target
+    dev = _lib.require_device(target, donor)
+    if target.dtype != donor.dtype:
+        raise TypeError("target and donor must share a dtype")
+    num_layers, _, num_heads, target_seq_len, head_dim = target.shape
+    donor_seq_len = donor.shape[3]
+    dpos = _lib.as_index(donor_positions, dev)
+    tpos = _lib.as_index(target_positions, dev)
+    tw, t_tmp = _contig_last(target)
+    dw, _ = _contig_last(donor)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_scatter_donor_kv",
+            tw.data_ptr(), dw.data_ptr(), dpos.data_ptr(), tpos.data_ptr(), num_pairs,
+            num_layers, num_heads, head_dim, target_seq_len, donor_seq_len, _lib.strides(tw),
+            _lib.strides(dw), _lib.dtype_code(tw), _lib.stream_handle(dev),
+        )
+    if t_tmp:
+        target.copy_(tw)
+    return target
+
+
+def scatter_donor_kv_paged(
+    kv_cache: torch.Tensor,
+    donor_kv: torch.Tensor,
+    block_table: torch.Tensor,
+    donor_positions: torch.Tensor,
+    target_positions: torch.Tensor,
+) -> torch.Tensor:
+    """``kv_cache[bt[t // bs], :, :, t % bs, :] = donor_kv[:, :, d, :]`` for every pair.
+
+    kv_cache: [num_blocks, 2, num_heads, block_size, head_dim] (any strides);
+    donor_kv: [2, num_heads, donor_seq_len, head_dim]; block_table: [num_blocks_per_seq].
+    Pairs whose donor position, logical block or physical block is out of range are skipped
+    (the reference GPU kernel's rule, semblend_core/triton_kernels.py:246-260).
+    Returns kv_cache (modified in place). Reference: semblend_core/triton_kernels.py:279-356.
+    """
+    num_pairs = donor_positions.shape[0]
+    if num_pairs == 0:
+        return kv_cache
+    dev = _lib.require_device(kv_cache, donor_kv)
+    if kv_cache.dtype != donor_kv.dtype:
+        raise TypeError("kv_cache and donor_kv must share a dtype")
+    nb_total, _, num_heads, block_size, head_dim = kv_cache.shape
+    bt = _lib.as_index(block_table, dev)
+    dpos = _lib.as_index(donor_positions, dev)
+    tpos = _lib.as_index(target_positions, dev)
+    kw, k_tmp = _contig_last(kv_cache)
+    dw, _ = _contig_last(donor_kv)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_scatter_donor_kv_paged",
+            kw.data_ptr(), dw.data_ptr(), bt.data_ptr(), dpos.data_ptr(), tpos.data_ptr(),
+            num_pairs, num_heads, block_size, head_dim, dw.shape[2], nb_total, bt.shape[0],
+            _lib.strides(kw), _lib.strides(dw), _lib.dtype_code(kw), _lib.stream_handle(dev),
+        )
+    if k_tmp:
+        kv_cache.copy_(kw)
+    return kv_cache
+
+
+def scatter_donor_kv_paged_layers(
+    kv_caches: list[torch.Tensor],
+    donor_kvs: list[torch.Tensor],
+    block_table: torch.Tensor,
+    donor_positions: torch.Tensor,
+    target_positions: torch.Tensor,
+) -> list[torch.Tensor]:
+    """``scatter_donor_kv_paged`` for every layer in a single launch.
+
+    kv_caches / donor_kvs: one tensor per layer (same shape, strides and dtype across
+    layers, 16-byte aligned bases). Extension with no reference counterpart; it replaces the
+    per-layer Python loop of callers such as synapse_kv_connector/model_runner_hook.py:215-276.
+    """
+    if len(kv_caches) != len(donor_kvs):
+        raise ValueError("kv_caches and donor_kvs must have the same length")
+    num_pairs = donor_positions.shape[0]
+    if num_pairs == 0 or not kv_caches:
+        return kv_caches
+    dev = _lib.require_device(*kv_caches, *donor_kvs)
+    ref, dref = kv_caches[0], donor_kvs[0]
+    for group, name in ((kv_caches, "kv_caches"), (donor_kvs, "donor_kvs")):
+        for t in group:
+            if t.shape != group[0].shape or t.stride() != group[0].stride() or \
+                    t.dtype != group[0].dtype:
+                raise ValueError(f"all {name} must share shape, strides and dtype")
+            if t.data_ptr() % 16 or t.stride(-1) != 1:
+                raise ValueError(f"{name} need 16-byte aligned bases and unit last stride")
+    if ref.dtype != dref.dtype:
+        raise TypeError("kv_caches and donor_kvs must share a dtype")
+    nb_total, _, num_heads, block_size, head_dim = ref.shape
+    kv_tab = torch.tensor([t.data_ptr() for t in kv_caches], dtype=torch.int64).to(dev)
+    d_tab = torch.tensor([t.data_ptr() for t in donor_kvs], dtype=torch.int64).to(dev)
+    bt = _lib.as_index(block_table, dev)
+    dpos = _lib.as_index(donor_positions, dev)
+    tpos = _lib.as_index(target_positions, dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_scatter_donor_kv_paged_layers",
+            kv_tab.data_ptr(), d_tab.data_ptr(), len(kv_caches), bt.data_ptr(),
+            dpos.data_ptr(), tpos.data_ptr(), num_pairs, num_heads, block_size, head_dim,
+            dref.shape[2], nb_total, bt.shape[0], _lib.strides(ref), _lib.strides(dref),
+            _lib.dtype_code(ref), _lib.stream_handle(dev),
+        )
+    return kv_caches
+
+
+# ------------------------------------------------------------------------------------------
+# Masked QKV projection
+# ------------------------------------------------------------------------------------------
+
+def masked_qkv_projection(
+    hidden_states: torch.Tensor,
+    qkv_weight: torch.Tensor,
+    compute_mask: torch.Tensor,
+    qkv_bias: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """QKV projection whose reuse rows (compute_mask == False) are zero.
+
+    hidden_states [seq_len, hidden]; qkv_weight [3 * H * D, hidden]; output
+    [seq_len, 3 * H * D] in the input dtype. The product is a plain GEMM, so it runs on
+    hipBLASLt through torch in fp32 (the reference's rounding, which projects in fp32 and casts
+    back, semblend_core/triton_kernels.py:511-520). Reference: :451-522.
+    """
+    _lib.require_device(hidden_states, qkv_weight)
+    projected = torch.nn.functional.linear(
+        hidden_states.float(),
+        qkv_weight.float(),
+        qkv_bias.float() if qkv_bias is not None else None,
+    )
+    mask = compute_mask.to(device=hidden_states.device).unsqueeze(1).float()
+    return (projected * mask).to(hidden_states.dtype)
+
+
+# ------------------------------------------------------------------------------------------
+# Partial prefill attention
+# ------------------------------------------------------------------------------------------
+
+def partial_prefill_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    compute_mask: torch.Tensor,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """Causal attention for the rows where ``compute_mask`` is True; other rows are 0.
+
+    query, key, value: [num_heads, seq_len, head_dim]. Row i attends to keys 0..i:
+    ``out[:, i] = softmax(scale * q[:, i] k[:, :i+1]^T) v[:, :i+1]`` with
+    ``scale = 1/sqrt(head_dim)`` by default. fp32 accumulation for every dtype.
+    The mask is compacted on the device, so the call does not synchronise with the host.
+    Reference: semblend_core/triton_kernels.py:655-734.
+    """
+    dev = _lib.require_device(query, key, value)
+    num_heads, seq_len, head_dim = query.shape
+    if key.shape != query.shape or value.shape != query.shape:
+        raise ValueError("query, key and value must have the same shape [H, S, D]")
+    if key.dtype != query.dtype or value.dtype != query.dtype:
+        raise TypeError("query, key and value must share a dtype")
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    output = torch.empty_like(query)
+    if output.stride(-1) != 1:
+        output = torch.empty(query.shape, dtype=query.dtype, device=dev)
+    if seq_len == 0 or num_heads == 0:
+        return output
+    q = query if query.stride(-1) == 1 else query.contiguous()
+    k = key if key.stride(-1) == 1 else key.contiguous()
+    v = value if value.stride(-1) == 1 else value.contiguous()
+    mask = compute_mask.to(device=dev)
+    if mask.dtype != torch.bool:
+        mask = mask != 0
+    mask = mask.contiguous().view(torch.uint8)
+    dt = _lib.dtype_code(q)
+    ws_bytes = _lib.size_query("sb_partial_prefill_attention_workspace_size", num_heads,
+                               seq_len, head_dim, dt)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_partial_prefill_attention",
+            output.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), mask.data_ptr(),
+            ws.data_ptr(), ws_bytes, num_heads, seq_len, head_dim, float(scale), _lib.strides(q),
+            _lib.strides(k), _lib.strides(v), _lib.strides(output), _lib.dtype_code(q),
+            _lib.stream_handle(dev),
+        )
+    return output
+
+
+def partial_prefill_attention_paged(
+    query: torch.Tensor,
+    kv_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    compute_positions: torch.Tensor,
+    scale: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """GQA causal attention over a paged cache for a compact set of query rows.
+
+    query: [R, num_q_heads, head_dim] — row r is the token at ``compute_positions[r]``;
+    kv_cache: [num_blocks, 2, num_kv_heads, block_size, head_dim] (any strides);
+    block_table: [num_blocks_per_seq]. Query head h reads KV head
+    ``h // (num_q_heads // num_kv_heads)``. Returns [R, num_q_heads, head_dim]:
+    ``out[r, h] = softmax(scale * q[r, h] K[0..p_r]^T) V[0..p_r]``.
+    Ascending positions give the best schedule; any order is correct.
+    Extension with no reference counterpart: the reference attention is MHA over contiguous
+    K/V (semblend_core/triton_kernels.py:655-734), gathered from the cache by its callers.
+    """
+    dev = _lib.require_device(query, kv_cache)
+    num_rows, num_q_heads, head_dim = query.shape
+    nb_total, _, num_kv_heads, block_size, hd = kv_cache.shape
+    if hd != head_dim:
+        raise ValueError("query and kv_cache head_dim differ")
+    if num_q_heads % num_kv_heads:
+        raise ValueError("num_q_heads must be a multiple of num_kv_heads")
+    if query.dtype != kv_cache.dtype:
+        raise TypeError("query and kv_cache must share a dtype")
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    if out is None:
+        out = torch.empty((num_rows, num_q_heads, head_dim), dtype=query.dtype, device=dev)
+    if num_rows == 0:
+        return out
+    q = query if query.stride(-1) == 1 else query.contiguous()
+    kv = kv_cache if kv_cache.stride(-1) == 1 else kv_cache.contiguous()
+    pos = _lib.as_index(compute_positions, dev)
+    if pos.shape[0] != num_rows:
+        raise ValueError("compute_positions must have one entry per query row")
+    bt = _lib.as_index(block_table, dev)
+    dt = _lib.dtype_code(q)
+    ws_bytes = _lib.size_query("sb_partial_attention_paged_workspace_size", num_rows,
+                               num_q_heads, num_kv_heads, head_dim, block_size, bt.shape[0], dt)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_partial_attention_paged",
+            out.data_ptr(), q.data_ptr(), kv.data_ptr(), bt.data_ptr(), pos.data_ptr(),
+            _lib.ptr(ws), ws_bytes, num_rows, num_q_heads, num_kv_heads, head_dim, block_size,
+            nb_total, bt.shape[0],
+            float(scale), _lib.strides(q), _lib.strides(out), _lib.strides(kv),
+            _lib.dtype_code(q), _lib.stream_handle(dev),
+        )
+    return out
+
+
+# ------------------------------------------------------------------------------------------
+# Orchestrator
+# ------------------------------------------------------------------------------------------
+
+@dataclass
+class PartialPrefillResult:
+    """Result of :func:`partial_prefill` (fields as semblend_core/triton_kernels.py:742-766).
+
+    output: [seq_len, hidden] projected attention output (reuse rows zero);
+    kv_cache: [num_layers, 2, num_heads, seq_len, head_dim] assembled target cache;
+    positions_computed / positions_reused: compute-mask counts;
+    computation_ratio: positions_computed / seq_len;
+    *_time_ms: HIP-event timings of the scatter, projection and attention stages and of the
+    whole call.
+    """
+
+    output: torch.Tensor
+    kv_cache: torch.Tensor
+    positions_computed: int
+    positions_reused: int
+    computation_ratio: float
+    scatter_time_ms: float
+    projection_time_ms: float
+    attention_time_ms: float
+    total_time_ms: float
+
+
+def partial_prefill(
+    hidden_states: torch.Tensor,
+    donor_kv: torch.Tensor,
+    qkv_weight: torch.Tensor,
+    output_projection: torch.Tensor,
+    donor_positions: torch.Tensor,
+    target_positions: torch.Tensor,
+    compute_mask: torch.Tensor,
+    num_heads: int,
+    head_dim: int,
+    qkv_bias: torch.Tensor | None = None,
+    output_bias: torch.Tensor | None = None,
+    scale: float | None = None,
+) -> PartialPrefillResult:
+    """Single-layer partial prefill with donor KV reuse.
+
+    Stages, with the reference's semantics (semblend_core/triton_kernels.py:769-923):
+    (1) scatter donor K/V into a zeroed target cache [L, 2, H, S, D];
+    (2) masked QKV projection (fp32, reuse rows zero);
+    (3) merge: compute rows take the new K/V, reuse rows keep layer 0's scattered donor K/V;
+    (4) partial attention over the merged layer-0 K/V in fp32, then the output projection,
+        cast to the input dtype, with reuse rows zeroed;
+    (5) the new K/V are written into the compute rows of EVERY layer of the target cache.
+    Attention uses layer 0 only, as in the reference.
+    """
+    dev = _lib.require_device(hidden_states, donor_kv, qkv_weight, output_projection)
+    seq_len = hidden_states.shape[0]
+    num_layers = donor_kv.shape[0]
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    compute_mask = compute_mask.to(device=dev)
+    if compute_mask.dtype != torch.bool:
+        compute_mask = compute_mask != 0
+
+    target_kv = torch.zeros((num_layers, 2, num_heads, seq_len, head_dim),
+                            dtype=hidden_states.dtype, device=dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+    ev[0].record()
+    scatter_donor_kv(target_kv, donor_kv, donor_positions, target_positions)
+    ev[1].record()
+    qkv_output = masked_qkv_projection(hidden_states, qkv_weight, compute_mask, qkv_bias)
+    qkv = qkv_output.float().view(seq_len, 3, num_heads, head_dim)
+    q_new = qkv[:, 0].permute(1, 0, 2)
+    k_new = qkv[:, 1].permute(1, 0, 2)
+    v_new = qkv[:, 2].permute(1, 0, 2)
+    ev[2].record()
+
+    cm = compute_mask.view(1, seq_len, 1)
+    merged_k = torch.where(cm, k_new, target_kv[0, 0].float()).contiguous()
+    merged_v = torch.where(cm, v_new, target_kv[0, 1].float()).contiguous()
+    attn_output = partial_prefill_attention(q_new.contiguous(), merged_k, merged_v,
+                                            compute_mask, scale)
+    ev[3].record()
+
+    attn_flat = attn_output.permute(1, 0, 2).reshape(seq_len, num_heads * head_dim)
+    final_output = torch.nn.functional.linear(
+        attn_flat,
+        output_projection.float(),
+        output_bias.float() if output_bias is not None else None,
+    ).to(hidden_states.dtype)
+    final_output = torch.where(compute_mask.view(seq_len, 1), final_output,
+                               torch.zeros((), dtype=final_output.dtype, device=dev))
+
+    # New K/V into the compute rows of every layer.
+    sel = cm.unsqueeze(0)  # [1, 1, S, 1] against [L, H, S, D]
+    new_k = k_new.to(target_kv.dtype).unsqueeze(0)
+    new_v = v_new.to(target_kv.dtype).unsqueeze(0)
+    target_kv[:, 0] = torch.where(sel, new_k, target_kv[:, 0])
+    target_kv[:, 1] = torch.where(sel, new_v, target_kv[:, 1])
+    ev[4].record()
+    ev[4].synchronize()
+
+    num_computed = int(compute_mask.sum().item())
+    return PartialPrefillResult(
+        output=final_output,
+        kv_cache=target_kv,
+        positions_computed=num_computed,
+        positions_reused=seq_len - num_computed,
+        computation_ratio=num_computed / seq_len if seq_len > 0 else 1.0,
+        scatter_time_ms=ev[0].elapsed_time(ev[1]),
+        projection_time_ms=ev[1].elapsed_time(ev[2]),
+        attention_time_ms=ev[2].elapsed_time(ev[3]),
+        total_time_ms=ev[0].elapsed_time(ev[4]),
+    )

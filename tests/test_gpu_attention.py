@@ -1,0 +1,128 @@
+"""GPU parity: partial-prefill attention against the fp32 oracle.
+
+bf16 / fp16 outputs must be within 2e-2 absolute of the fp32 reference; fp32 inputs within
+the reference suite's own 1e-4 absolute / 1e-3 relative. Cases restate
+synapse_kv_connector/tests/test_triton_kernels.py:396-493 and add GQA + paged cases up to the
+Qwen2.5-7B shape (28 q heads / 4 KV heads, head_dim 128, 16384-token context).
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import ref_cpu as ref
+from semblend_amd import triton_kernels as tk
+from tests.helpers import assert_attn_close, gen, randn, recompute_set
+
+pytestmark = pytest.mark.gpu
+
+
+# ---- dense drop-in (triton_kernels.py:655-734) ----
+
+def test_dense_all_compute_fp32(dev):
+    q, k, v = (randn((2, 8, 16), torch.float32, s) for s in (1, 2, 3))
+    mask = torch.ones(8, dtype=torch.bool)
+    got = tk.partial_prefill_attention(q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
+                                       1.0 / math.sqrt(16))
+    assert_attn_close(got, ref.partial_prefill_attention(q, k, v, mask, 1.0 / math.sqrt(16)))
+
+
+def test_dense_reuse_rows_zero_and_full_context(dev):
+    q, k, v = (randn((2, 8, 16), torch.float32, s) for s in (4, 5, 6))
+    mask = torch.tensor([True, False, True, False, True, False, True, False])
+    got = tk.partial_prefill_attention(q.to(dev), k.to(dev), v.to(dev), mask.to(dev)).cpu()
+    for p in (1, 3, 5, 7):
+        assert torch.all(got[:, p] == 0)
+    assert_attn_close(got, ref.partial_prefill_attention(q, k, v, mask))
+    q1, k1, v1 = (randn((1, 4, 8), torch.float32, s) for s in (7, 8, 9))
+    m1 = torch.tensor([False, False, False, True])
+    got1 = tk.partial_prefill_attention(q1.to(dev), k1.to(dev), v1.to(dev), m1.to(dev))
+    assert_attn_close(got1, ref.partial_prefill_attention(q1, k1, v1, m1))
+
+
+def test_dense_empty_mask(dev):
+    q = randn((2, 4, 8), torch.float32, 10).to(dev)
+    got = tk.partial_prefill_attention(q, q, q, torch.zeros(4, dtype=torch.bool, device=dev))
+    assert torch.all(got == 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("seq_len", [1, 77, 300, 1000])
+def test_dense_mfma(dev, dtype, head_dim, seq_len):
+    h = 3
+    q, k, v = (randn((h, seq_len, head_dim), dtype, 20 + s) for s in range(3))
+    mask = torch.rand(seq_len, generator=gen(seq_len)) < 0.3
+    mask[-1] = True
+    got = tk.partial_prefill_attention(q.to(dev), k.to(dev), v.to(dev), mask.to(dev))
+    want = ref.partial_prefill_attention(q, k, v, mask)
+    assert got.dtype == dtype
+    assert torch.all(got.cpu()[:, ~mask] == 0)
+    assert_attn_close(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_dense_other_head_dim(dev, dtype):
+    """head_dim 96 takes the general (non-MFMA) kernel."""
+    q, k, v = (randn((2, 130, 96), dtype, 30 + s) for s in range(3))
+    mask = torch.rand(130, generator=gen(31)) < 0.5
+    got = tk.partial_prefill_attention(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.3)
+    assert_attn_close(got, ref.partial_prefill_attention(q, k, v, mask, 0.3))
+
+
+# ---- GQA over a paged cache ----
+
+def _paged_case(hq, hkv, d, seq_len, n_rows, dtype, seed, nb=None, bs=16):
+    nblk = (seq_len + bs - 1) // bs
+    nb = nb or nblk + 7
+    kv = randn((nb, 2, hkv, bs, d), dtype, seed)
+    bt = torch.randperm(nb, generator=gen(seed + 1))[:nblk].to(torch.int32)
+    pos = recompute_set(seq_len, n_rows, seed + 2, chunk=min(256, seq_len // 4 or 1))
+    q = randn((pos.shape[0], hq, d), dtype, seed + 3)
+    return q, kv, bt, pos
+
+
+def test_paged_gqa_qwen05b_fp32(dev):
+    """Qwen2.5-0.5B attention: 14 q heads / 2 KV heads, head_dim 64, fp32, 1024 tokens,
+    154 query rows drawn without replacement."""
+    kv = randn((128, 2, 2, 16, 64), torch.float32, 40)
+    bt = torch.randperm(128, generator=gen(41))[:64].to(torch.int32)
+    pos = torch.randperm(1024, generator=gen(42))[:154].sort().values.to(torch.int32)
+    q = randn((154, 14, 64), torch.float32, 43)
+    got = tk.partial_prefill_attention_paged(q.to(dev), kv.to(dev), bt.to(dev), pos.to(dev))
+    assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv,d", [(28, 4, 128), (32, 8, 128), (14, 2, 64), (8, 8, 128)])
+def test_paged_gqa_mfma(dev, dtype, hq, hkv, d):
+    q, kv, bt, pos = _paged_case(hq, hkv, d, 2048, 300, dtype, 50)
+    got = tk.partial_prefill_attention_paged(q.to(dev), kv.to(dev), bt.to(dev), pos.to(dev))
+    assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
+
+
+def test_paged_gqa_unsorted_positions(dev):
+    q, kv, bt, pos = _paged_case(28, 4, 128, 1024, 200, torch.bfloat16, 60)
+    perm = torch.randperm(pos.shape[0], generator=gen(61))
+    q, pos = q[perm].contiguous(), pos[perm].contiguous()
+    got = tk.partial_prefill_attention_paged(q.to(dev), kv.to(dev), bt.to(dev), pos.to(dev))
+    assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
+
+
+def test_paged_gqa_full_size_7b(dev):
+    """The 7B attention workload at full size: 16384-token context, 2458 query rows
+    (first 256 tokens, two random 256-token chunks, the rest scattered), 28/4 heads, bf16.
+    A sample of 48 rows (including the first, last and chunk boundaries) is compared with
+    the oracle; every output row must be finite with |o| <= max|V|."""
+    q, kv, bt, pos = _paged_case(28, 4, 128, 16384, 2458, torch.bfloat16, 70, nb=2048)
+    assert pos.shape[0] == 2458
+    got = tk.partial_prefill_attention_paged(q.to(dev), kv.to(dev), bt.to(dev), pos.to(dev))
+    assert torch.isfinite(got).all()
+    assert float(got.abs().max()) <= float(kv[:, 1].abs().max()) + 1e-2
+    rows = torch.cat([torch.tensor([0, 255, 256, 2457]),
+                      torch.randperm(2458, generator=gen(71))[:44]]).unique()
+    want = ref.partial_attention_paged(q[rows], kv, bt, pos[rows])
+    assert_attn_close(got.cpu()[rows], want)
