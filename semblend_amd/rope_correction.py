@@ -331,6 +331,33 @@ def nope_permute_paged_kv(
         )
 
 
+def _rotation_counts(positions: list[int], block_size: int,
+                     num_blocks_per_seq: int) -> tuple[dict[int, int], int]:
+    """Host-side resolution of ``apply_rope_delta_inplace``'s position list.
+
+    Returns ({logical position: times it is rotated}, positions processed). Positions whose
+    logical block lies past the table are skipped; negative positions index blocks from the
+    end of the table, as ``block_table[pos // block_size]`` does in Python
+    (semblend_core/rope_correction.py:758-763); below -num_blocks_per_seq blocks that raises
+    IndexError there and here.
+    """
+    counts: dict[int, int] = {}
+    processed = 0
+    for pos in positions:
+        blk_idx = pos // block_size
+        if blk_idx >= num_blocks_per_seq:
+            continue
+        if blk_idx < -num_blocks_per_seq:
+            raise IndexError(
+                f"position {pos} indexes block {blk_idx} of a {num_blocks_per_seq}-entry table")
+        if blk_idx < 0:
+            blk_idx += num_blocks_per_seq
+        logical = blk_idx * block_size + pos % block_size
+        counts[logical] = counts.get(logical, 0) + 1
+        processed += 1
+    return counts, processed
+
+
 def apply_rope_delta_inplace(
     kv_cache: torch.Tensor,
     block_table: torch.Tensor,
@@ -367,21 +394,7 @@ def apply_rope_delta_inplace(
         kst = (k_plane.stride(0), k_plane.stride(1), k_plane.stride(2), k_plane.stride(3))
     _check_head_dim(head_dim, head_dim, "apply_rope_delta_inplace")
     nbs = block_table.shape[0]
-    # Host-side normalisation with Python index semantics (negative positions index blocks
-    # from the end of the table, as block_table[pos // block_size] does in the reference).
-    counts: dict[int, int] = {}
-    modified = 0
-    for pos in positions:
-        blk_idx = pos // block_size
-        if blk_idx >= nbs:
-            continue
-        if blk_idx < -nbs:
-            raise IndexError(f"position {pos} indexes block {blk_idx} of a {nbs}-entry table")
-        if blk_idx < 0:
-            blk_idx += nbs
-        logical = blk_idx * block_size + pos % block_size
-        counts[logical] = counts.get(logical, 0) + 1
-        modified += 1
+    counts, modified = _rotation_counts(positions, block_size, nbs)
     if not counts:
         return 0
     pos_t = torch.tensor(list(counts.keys()), dtype=torch.int32).to(dev)

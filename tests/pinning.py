@@ -1,0 +1,414 @@
+"""Checks that pin the oracle, written against an implementation namespace ``impl`` that
+provides the oracle's function names (see oracle/ref_cpu.py).
+
+Three kinds of check:
+  * the reference's own test cases, restated (synapse_kv_connector/tests/
+    test_triton_kernels.py, test_rope_correction.py) with the reference's tolerances;
+  * float64 golden vectors written independently by tests/golden/make_golden.py;
+  * invariants fixed by the mathematics (rotation group law, norm preservation, identity at
+    delta 0, V untouched by RoPE, zero rows outside the compute mask).
+
+tests/test_oracle_pinning.py runs every check against the oracle; tests/test_oracle_mutations.py
+plants plausible mistakes in copies of the oracle and requires that some check fails.
+"""
+
+from __future__ import annotations
+
+import math
+from pathlib import Path
+
+import numpy as np
+import torch
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _gen(seed):
+    return torch.Generator("cpu").manual_seed(seed)
+
+
+def _randn(shape, seed, dtype=torch.float32):
+    return torch.randn(shape, generator=_gen(seed)).to(dtype)
+
+
+def apply_rope_from_scratch(x, positions, head_dim, rope_base=10000.0):
+    """The reference suite's test oracle (test_rope_correction.py:14-31), restated:
+    rotate row i of x (second-to-last dim) by positions[i], interleaved, in fp32."""
+    inv = 1.0 / (rope_base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    result = x.clone().float()
+    for i, pos in enumerate(positions):
+        theta = float(pos) * inv
+        c, s = torch.cos(theta), torch.sin(theta)
+        even = result[..., i, 0::2].clone()
+        odd = result[..., i, 1::2].clone()
+        result[..., i, 0::2] = even * c - odd * s
+        result[..., i, 1::2] = even * s + odd * c
+    return result.to(x.dtype)
+
+
+def _close(a, b, atol, rtol, msg=""):
+    torch.testing.assert_close(a, b, atol=atol, rtol=rtol, msg=msg or None)
+
+
+# ------------------------------------------------------------------------------------------
+# RoPE: reference cases (test_rope_correction.py)
+# ------------------------------------------------------------------------------------------
+
+def check_rope_reference_cases(impl) -> None:
+    # identity, :37-47
+    k = _randn((4, 8, 128), 1, torch.float16)
+    pos = torch.tensor([0, 3, 7], dtype=torch.int32)
+    _close(impl.rope_correct_k(k, pos, pos, head_dim=128), k, 1e-3, 1e-3)
+    # exact move 5 -> 10, :49-83
+    raw = _randn((4, 1, 128), 2)
+    k5 = apply_rope_from_scratch(raw, torch.tensor([5]), 128)
+    k10 = apply_rope_from_scratch(raw, torch.tensor([10]), 128)
+    padded = torch.zeros(4, 11, 128)
+    padded[:, 5] = k5[:, 0]
+    out = impl.rope_correct_k(padded, torch.tensor([5], dtype=torch.int32),
+                              torch.tensor([10], dtype=torch.int32), head_dim=128)
+    _close(out[:, 5], k10[:, 0], 1e-4, 1e-4)
+    # reorder, :85-117
+    raw = _randn((4, 4, 64), 3)
+    dpos = torch.arange(4, dtype=torch.int32)
+    tpos = torch.tensor([2, 3, 0, 1], dtype=torch.int32)
+    out = impl.rope_correct_k(apply_rope_from_scratch(raw, dpos, 64), dpos, tpos, head_dim=64)
+    _close(out, apply_rope_from_scratch(raw, tpos, 64), 1e-3, 1e-3)
+    # negative delta, :119-144
+    raw = _randn((2, 1, 64), 4)
+    padded = torch.zeros(2, 101, 64)
+    padded[:, 100] = apply_rope_from_scratch(raw, torch.tensor([100]), 64)[:, 0]
+    out = impl.rope_correct_k(padded, torch.tensor([100], dtype=torch.int32),
+                              torch.tensor([50], dtype=torch.int32), head_dim=64)
+    _close(out[:, 100], apply_rope_from_scratch(raw, torch.tensor([50]), 64)[:, 0], 1e-3, 1e-3)
+    # composition identity, :294-323
+    k = _randn((2, 10, 64), 5)
+    s1 = impl.rope_correct_k(k, torch.tensor([3], dtype=torch.int32),
+                             torch.tensor([8], dtype=torch.int32), head_dim=64)
+    s2 = impl.rope_correct_k(s1, torch.tensor([3], dtype=torch.int32),
+                             torch.tensor([-2], dtype=torch.int32), head_dim=64)
+    _close(s2[:, 3], k[:, 3], 1e-3, 1e-3)
+    # bases, :325-353
+    for base in (500.0, 10000.0, 1e6):
+        raw = _randn((2, 1, 32), 6)
+        padded = torch.zeros(2, 11, 32)
+        padded[:, 0] = apply_rope_from_scratch(raw, torch.tensor([0]), 32, base)[:, 0]
+        out = impl.rope_correct_k(padded, torch.tensor([0], dtype=torch.int32),
+                                  torch.tensor([10], dtype=torch.int32), head_dim=32,
+                                  rope_base=base)
+        _close(out[:, 0], apply_rope_from_scratch(raw, torch.tensor([10]), 32, base)[:, 0],
+               1e-3, 1e-3, f"base {base}")
+
+
+def check_rope_paged_reference_cases(impl) -> None:
+    nb, h, bs, d = 4, 2, 16, 64
+    # V unchanged, :162-191
+    kv = torch.zeros(nb, 2, h, bs, d)
+    donor = _randn((2, h, 32, d), 7)
+    bt = torch.arange(nb, dtype=torch.int32)
+    dp = torch.tensor([0, 1, 2], dtype=torch.int32)
+    tp = torch.tensor([5, 10, 15], dtype=torch.int32)
+    impl.rope_correct_scatter_paged(kv, donor, bt, dp, tp)
+    for a, b in zip(dp.tolist(), tp.tolist()):
+        _close(kv[b // bs, 1, :, b % bs], donor[1, :, a], 1e-6, 1e-6)
+    # K corrected, :193-233
+    kv = torch.zeros(nb, 2, h, bs, d)
+    raw = _randn((h, 1, d), 8)
+    donor = torch.zeros(2, h, 32, d)
+    donor[0, :, 3] = apply_rope_from_scratch(raw, torch.tensor([3]), d)[:, 0]
+    donor[1] = _randn((h, 32, d), 9)
+    impl.rope_correct_scatter_paged(kv, donor, bt, torch.tensor([3], dtype=torch.int32),
+                                    torch.tensor([7], dtype=torch.int32))
+    _close(kv[0, 0, :, 7], apply_rope_from_scratch(raw, torch.tensor([7]), d)[:, 0], 1e-3, 1e-3)
+    # permute swap, :235-264
+    kv = _randn((2, 2, h, bs, d), 10)
+    v0, v1 = kv[0, 1, :, 0].clone(), kv[0, 1, :, 1].clone()
+    impl.permute_paged_kv_with_rope(kv, torch.arange(2, dtype=torch.int32), [(0, 1), (1, 0)])
+    _close(kv[0, 1, :, 1], v0, 1e-6, 1e-6)
+    _close(kv[0, 1, :, 0], v1, 1e-6, 1e-6)
+
+
+def check_nope_reference_cases(impl) -> None:
+    """test_rope_correction.py:452-637: NoPE identity, NoPE == delta for many deltas, NoPE
+    matches fresh RoPE at the target, V copied exactly."""
+    def single(raw, pos, d, base=10000.0):
+        return apply_rope_from_scratch(raw.unsqueeze(1), torch.tensor([pos]), d, base)[:, 0]
+
+    def cache(h, d, seq, bs=16):
+        nb = (seq + bs - 1) // bs + 2
+        return (torch.zeros(nb, 2, h, bs, d, dtype=torch.float16),
+                torch.arange((seq + bs - 1) // bs, dtype=torch.int32))
+
+    raw = _randn((4, 64), 11)
+    kv, bt = cache(4, 64, 32)
+    kv[0, 0, :, 5] = single(raw, 5, 64).half()
+    impl.nope_permute_paged_kv(kv, bt, [(5, 5)])
+    _close(kv[0, 0, :, 5].float(), single(raw, 5, 64), 5e-3, 5e-3)
+    raw = _randn((4, 128), 12)
+    kv, bt = cache(4, 128, 64)
+    kv[0, 0, :, 7] = single(raw, 7, 128).half()
+    impl.nope_permute_paged_kv(kv, bt, [(7, 23)])
+    _close(kv[1, 0, :, 7].float(), single(raw, 23, 128), 1e-2, 1e-2)
+    for delta in (0, 1, 5, 50, 100, 256, 1000):
+        raw = _randn((8, 128), 13)
+        tgt = 5 + delta
+        kd, bt = cache(8, 128, max(tgt + 16, 128))
+        kn, _ = cache(8, 128, max(tgt + 16, 128))
+        kd[0, 0, :, 5] = single(raw, 5, 128).half()
+        kn[0, 0, :, 5] = single(raw, 5, 128).half()
+        impl.permute_paged_kv_with_rope(kd, bt, [(5, tgt)])
+        impl.nope_permute_paged_kv(kn, bt, [(5, tgt)])
+        _close(kn[tgt // 16, 0, :, tgt % 16].float(), kd[tgt // 16, 0, :, tgt % 16].float(),
+               5e-3, 5e-3, f"delta {delta}")
+    kv, bt = cache(4, 64, 32)
+    v = _randn((4, 64), 14, torch.float16)
+    kv[0, 1, :, 2] = v
+    impl.nope_permute_paged_kv(kv, bt, [(2, 10)])
+    assert torch.equal(kv[0, 1, :, 10], v)
+
+
+def check_nope_sequential_v(impl) -> None:
+    """V rows move pair by pair in list order (rope_correction.py:650-653): after the swap
+    [(0, 1), (1, 0)] both rows hold the original row 0."""
+    kv = _randn((2, 2, 2, 16, 32), 15)
+    v0 = kv[0, 1, :, 0].clone()
+    impl.nope_permute_paged_kv(kv, torch.arange(2, dtype=torch.int32), [(0, 1), (1, 0)])
+    assert torch.equal(kv[0, 1, :, 0], v0) and torch.equal(kv[0, 1, :, 1], v0)
+
+
+def check_apply_rope_delta(impl) -> None:
+    """apply_rope_delta_inplace: delta then -delta restores K (semblend_connector.py:609-616),
+    V untouched, both layouts, the returned count, the delta-0 and empty shortcuts."""
+    kv = _randn((6, 2, 2, 16, 64), 16)
+    bt = torch.tensor([3, 1, 4, 0], dtype=torch.int32)
+    orig = kv.clone()
+    pos = [0, 7, 16, 33, 63, 64, 100]          # 64 and 100 lie past the 4-block table
+    assert impl.apply_rope_delta_inplace(kv, bt, pos, 77) == 5
+    assert torch.equal(kv[:, 1], orig[:, 1])
+    assert not torch.allclose(kv[3, 0, :, 0], orig[3, 0, :, 0])
+    impl.apply_rope_delta_inplace(kv, bt, pos, -77)
+    _close(kv, orig, 1e-5, 1e-5)
+    assert impl.apply_rope_delta_inplace(kv, bt, pos, 0) == 0
+    assert impl.apply_rope_delta_inplace(kv, bt, [], 5) == 0
+    # vLLM layout [2, NB, bs, H, D] must rotate the same rows the same way
+    std = _randn((6, 2, 2, 16, 64), 17)
+    vllm = std.permute(1, 0, 3, 2, 4).contiguous()
+    impl.apply_rope_delta_inplace(std, bt, [5, 40], 9)
+    impl.apply_rope_delta_inplace(vllm, bt, [5, 40], 9)
+    assert torch.equal(vllm.permute(1, 0, 3, 2, 4), std)
+
+
+# ------------------------------------------------------------------------------------------
+# RoPE: float64 golden vectors and invariants
+# ------------------------------------------------------------------------------------------
+
+def check_rope_golden(impl) -> None:
+    g = np.load(GOLDEN / "rope_golden.npz")
+    i = 0
+    while f"c{i}_raw" in g:
+        base = float(g[f"c{i}_base"])
+        k_at_d = torch.from_numpy(g[f"c{i}_k_at_d"])
+        dpos = torch.from_numpy(g[f"c{i}_dpos"])
+        tpos = torch.from_numpy(g[f"c{i}_tpos"])
+        d = k_at_d.shape[-1]
+        # place each cached row at its donor slot of a [H, S, D] tensor, one row per pair
+        n = dpos.shape[0]
+        local = torch.arange(n, dtype=torch.int32)
+        out = impl.rope_correct_k(k_at_d, local, local + (tpos - dpos), head_dim=d,
+                                  rope_base=base)
+        want = torch.from_numpy(g[f"c{i}_corrected"])
+        err = (out.double() - want).abs().max().item()
+        assert err < 2e-5, f"case {i}: max error {err} vs the float64 correction"
+        err_t = (out.double() - torch.from_numpy(g[f"c{i}_k_at_t"])).abs().max().item()
+        assert err_t < 5e-5, f"case {i}: max error {err_t} vs RoPE computed at the target"
+        i += 1
+    assert i >= 4
+
+
+def check_rope_invariants(impl) -> None:
+    k = _randn((3, 40, 64), 18)
+    pos = torch.arange(40, dtype=torch.int32)
+    g = _gen(19)
+    a = torch.randint(-500, 500, (40,), generator=g, dtype=torch.int32)
+    b = torch.randint(-500, 500, (40,), generator=g, dtype=torch.int32)
+    ra = impl.rope_correct_k(k, pos, pos + a, head_dim=64, rope_base=1e4)
+    # norms of every interleaved pair are preserved
+    def pn(x):
+        return torch.sqrt(x[..., 0::2] ** 2 + x[..., 1::2] ** 2)
+    _close(pn(ra), pn(k), 1e-5, 1e-5)
+    # group law R(b) R(a) = R(a + b)
+    rab = impl.rope_correct_k(ra, pos, pos + b, head_dim=64, rope_base=1e4)
+    r_sum = impl.rope_correct_k(k, pos, pos + a + b, head_dim=64, rope_base=1e4)
+    _close(rab, r_sum, 1e-4, 1e-4)
+    # a rotation by +1 of pair i is by exactly inv_freq[i] radians: compare with cos/sin
+    e = torch.zeros(1, 1, 64)
+    e[..., 0::2] = 1.0
+    r1 = impl.rope_correct_k(e, torch.tensor([0], dtype=torch.int32),
+                             torch.tensor([1], dtype=torch.int32), head_dim=64, rope_base=1e4)
+    f64 = 1.0 / 1e4 ** (np.arange(0, 64, 2) / 64.0)
+    _close(r1[0, 0, 0::2].double(), torch.from_numpy(np.cos(f64)), 1e-6, 1e-6)
+    _close(r1[0, 0, 1::2].double(), torch.from_numpy(np.sin(f64)), 1e-6, 1e-6)
+
+
+# ------------------------------------------------------------------------------------------
+# Scatter
+# ------------------------------------------------------------------------------------------
+
+def check_scatter_reference_cases(impl) -> None:
+    # test_triton_kernels.py:82-168
+    target = torch.zeros(2, 2, 4, 16, 32, dtype=torch.float16)
+    donor = _randn((2, 2, 4, 8, 32), 20, torch.float16)
+    dp = torch.tensor([0, 2, 4, 6], dtype=torch.int32)
+    tp = torch.tensor([1, 3, 7, 12], dtype=torch.int32)
+    impl.scatter_donor_kv(target, donor, dp, tp)
+    for a, b in zip(dp.tolist(), tp.tolist()):
+        assert torch.equal(target[:, :, :, b], donor[:, :, :, a])
+    for p in (0, 2, 4):
+        assert torch.all(target[:, :, :, p] == 0)
+    full = torch.zeros(2, 2, 4, 16, 32, dtype=torch.float16)
+    donor = _randn((2, 2, 4, 16, 32), 21, torch.float16)
+    ar = torch.arange(16, dtype=torch.int32)
+    impl.scatter_donor_kv(full, donor, ar, ar)
+    assert torch.equal(full, donor)
+    # test_triton_kernels.py:208-302
+    kv = torch.zeros(8, 2, 2, 4, 16, dtype=torch.float16)
+    donor = _randn((2, 2, 8, 16), 22, torch.float16)
+    impl.scatter_donor_kv_paged(kv, donor, torch.tensor([3, 5], dtype=torch.int32),
+                                torch.tensor([0, 4], dtype=torch.int32),
+                                torch.tensor([1, 5], dtype=torch.int32))
+    assert torch.equal(kv[3, :, :, 1], donor[:, :, 0])
+    assert torch.equal(kv[5, :, :, 1], donor[:, :, 4])
+    kv = torch.zeros(4, 2, 1, 4, 8, dtype=torch.float16)
+    donor = _randn((2, 1, 4, 8), 23, torch.float16)
+    impl.scatter_donor_kv_paged(kv, donor, torch.tensor([1], dtype=torch.int32),
+                                torch.tensor([0, 1], dtype=torch.int32),
+                                torch.tensor([2, 8], dtype=torch.int32))
+    assert torch.equal(kv[1, :, :, 2], donor[:, :, 0])
+    kv[1, :, :, 2] = 0
+    assert torch.all(kv == 0)
+
+
+def check_scatter_golden(impl) -> None:
+    g = np.load(GOLDEN / "scatter_golden.npz")
+    kv = torch.from_numpy(g["p_kv"].copy())
+    impl.scatter_donor_kv_paged(kv, torch.from_numpy(g["p_donor"]), torch.from_numpy(g["p_bt"]),
+                                torch.from_numpy(g["p_dpos"]), torch.from_numpy(g["p_tpos"]))
+    assert torch.equal(kv.double(), torch.from_numpy(g["p_out"])), "paged scatter golden"
+    tgt = torch.from_numpy(g["f_target"].copy())
+    impl.scatter_donor_kv(tgt, torch.from_numpy(g["f_donor"]), torch.from_numpy(g["f_dpos"]),
+                          torch.from_numpy(g["f_tpos"]))
+    assert torch.equal(tgt.double(), torch.from_numpy(g["f_out"])), "flat scatter golden"
+
+
+# ------------------------------------------------------------------------------------------
+# Attention
+# ------------------------------------------------------------------------------------------
+
+def check_attention_reference_cases(impl) -> None:
+    # test_triton_kernels.py:396-493
+    q, k, v = (_randn((2, 8, 16), s) for s in (30, 31, 32))
+    scale = 1.0 / math.sqrt(16)
+    res = impl.partial_prefill_attention(q, k, v, torch.ones(8, dtype=torch.bool), scale)
+    for h in range(2):
+        for pos in range(8):
+            w = torch.softmax(q[h, pos:pos + 1] @ k[h, :pos + 1].T * scale, dim=-1)
+            _close(res[h, pos], (w @ v[h, :pos + 1]).squeeze(0), 1e-4, 1e-3)
+    mask = torch.tensor([True, False] * 4)
+    res = impl.partial_prefill_attention(q, k, v, mask)
+    for pos in (1, 3, 5, 7):
+        assert torch.all(res[:, pos] == 0)
+    q1, k1, v1 = (_randn((1, 4, 8), s) for s in (33, 34, 35))
+    res = impl.partial_prefill_attention(q1, k1, v1, torch.tensor([False, False, False, True]))
+    w = torch.softmax(q1[0, 3:4] @ k1[0].T / math.sqrt(8), dim=-1)
+    _close(res[0, 3], (w @ v1[0]).squeeze(0), 1e-4, 1e-3)
+    res = impl.partial_prefill_attention(q1, k1, v1, torch.zeros(4, dtype=torch.bool))
+    assert torch.all(res == 0)
+
+
+def check_attention_golden(impl) -> None:
+    g = np.load(GOLDEN / "attention_golden.npz")
+    i = 0
+    while f"d{i}_q" in g:
+        out = impl.partial_prefill_attention(
+            torch.from_numpy(g[f"d{i}_q"]), torch.from_numpy(g[f"d{i}_k"]),
+            torch.from_numpy(g[f"d{i}_v"]), torch.from_numpy(g[f"d{i}_mask"]),
+            float(g[f"d{i}_scale"]))
+        err = (out.double() - torch.from_numpy(g[f"d{i}_out"])).abs().max().item()
+        assert err < 1e-5, f"dense case {i}: max error {err}"
+        i += 1
+    out = impl.partial_attention_paged(torch.from_numpy(g["g_q"]), torch.from_numpy(g["g_kv"]),
+                                       torch.from_numpy(g["g_bt"]), torch.from_numpy(g["g_pos"]))
+    err = (out.double() - torch.from_numpy(g["g_out"])).abs().max().item()
+    assert err < 1e-5, f"GQA paged case: max error {err}"
+
+
+def check_gqa_matches_dense(impl) -> None:
+    """Paged GQA attention equals the dense MHA computation on the gathered, head-expanded
+    K/V (the reference computation applied per query head)."""
+    nb, hkv, hq, bs, d, seq = 12, 2, 8, 16, 32, 150
+    kv = _randn((nb, 2, hkv, bs, d), 40)
+    bt = torch.randperm(nb, generator=_gen(41))[:10].to(torch.int32)
+    pos = torch.tensor([0, 3, 17, 64, 99, 149], dtype=torch.int32)
+    q = _randn((pos.shape[0], hq, d), 42)
+    out = impl.partial_attention_paged(q, kv, bt, pos)
+    t = torch.arange(seq)
+    kd = kv[bt[t // bs].long(), 0, :, t % bs].permute(1, 0, 2)
+    vd = kv[bt[t // bs].long(), 1, :, t % bs].permute(1, 0, 2)
+    g = hq // hkv
+    qd = torch.zeros(hq, seq, d)
+    mask = torch.zeros(seq, dtype=torch.bool)
+    for r, p in enumerate(pos.tolist()):
+        qd[:, p] = q[r]
+        mask[p] = True
+    dense = impl.partial_prefill_attention(qd, kd.repeat_interleave(g, 0),
+                                           vd.repeat_interleave(g, 0), mask)
+    _close(out, dense[:, pos.long()].permute(1, 0, 2), 1e-5, 1e-5)
+
+
+# ------------------------------------------------------------------------------------------
+# Projection and orchestrator
+# ------------------------------------------------------------------------------------------
+
+def check_projection_and_prefill(impl) -> None:
+    # test_triton_kernels.py:313-385
+    x = _randn((8, 32), 50, torch.float16)
+    w = _randn((48, 32), 51, torch.float16)
+    b = _randn((48,), 52, torch.float16)
+    out = impl.masked_qkv_projection(x, w, torch.ones(8, dtype=torch.bool), b)
+    _close(out, torch.nn.functional.linear(x.float(), w.float(), b.float()).half(), 1e-2, 1e-2)
+    mask = torch.tensor([True, False] * 4)
+    out = impl.masked_qkv_projection(x, w, mask)
+    assert torch.all(out[~mask] == 0) and not torch.any(torch.all(out[mask] == 0, dim=1))
+    # test_triton_kernels.py:504-713
+    seq, hid, h, d, L = 16, 32, 4, 8, 2
+    hs = _randn((seq, hid), 53, torch.float16)
+    donor = _randn((L, 2, h, 10, d), 54, torch.float16)
+    wq = _randn((3 * h * d, hid), 55, torch.float16)
+    wo = _randn((hid, h * d), 56, torch.float16)
+    dp = torch.tensor([0, 2, 4, 6, 8], dtype=torch.int32)
+    tp = torch.tensor([0, 3, 6, 9, 12], dtype=torch.int32)
+    cm = torch.ones(seq, dtype=torch.bool)
+    cm[tp.long()] = False
+    out, kv, computed, reused, ratio = impl.partial_prefill(hs, donor, wq, wo, dp, tp, cm, h, d)
+    assert (computed, reused) == (11, 5) and abs(ratio - 11 / 16) < 1e-9
+    assert out.shape == (seq, hid) and kv.shape == (L, 2, h, seq, d)
+    for a, c in zip(dp.tolist(), tp.tolist()):
+        assert torch.equal(kv[:, :, :, c], donor[:, :, :, a])
+    assert torch.all(out[~cm] == 0)
+
+
+ALL_CHECKS = [
+    check_rope_reference_cases,
+    check_rope_paged_reference_cases,
+    check_nope_reference_cases,
+    check_nope_sequential_v,
+    check_apply_rope_delta,
+    check_rope_golden,
+    check_rope_invariants,
+    check_scatter_reference_cases,
+    check_scatter_golden,
+    check_attention_reference_cases,
+    check_attention_golden,
+    check_gqa_matches_dense,
+    check_projection_and_prefill,
+]

@@ -1,0 +1,103 @@
+"""The C ABI library (no GPU): it loads, exports every function include/semblend_hip.h
+declares with the argument counts the ctypes binding uses, and rejects invalid arguments with
+SB_ERR_INVALID_ARGUMENT before launching anything."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from semblend_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "semblend_hip.h"
+
+
+def _declared() -> dict[str, int]:
+    """Function name -> parameter count, parsed from the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|int64_t|const char\*)\s+(sb_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_header_declares_the_abi():
+    decl = _declared()
+    assert "sb_version" in decl and "sb_last_error_string" in decl
+    assert set(_lib.SIGNATURES) | set(_lib.SIZE_QUERIES) | {"sb_version", "sb_last_error_string"} \
+        == set(decl)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for name, nparams in _declared().items():
+        assert hasattr(lib, name), name
+        if name in _lib.SIGNATURES:
+            assert len(_lib.SIGNATURES[name]) == nparams, name
+        if name in _lib.SIZE_QUERIES:
+            assert len(_lib.SIZE_QUERIES[name]) == nparams, name
+
+
+def test_version():
+    assert _lib.version().startswith("semblend_hip ") and "gfx950" in _lib.version()
+
+
+def _i64(*v):
+    return (ctypes.c_int64 * len(v))(*v)
+
+
+def test_invalid_arguments_are_rejected_without_launch():
+    lib = _lib.lib()
+    fake = 4096  # never dereferenced: validation fails first
+    st = _i64(1, 1, 1, 1, 1)
+    # bad dtype
+    rc = lib.sb_scatter_donor_kv(fake, fake, fake, fake, 4, 1, 1, 8, 4, 4, st, st, 7, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT
+    assert b"invalid dtype" in lib.sb_last_error_string()
+    # null pointers
+    rc = lib.sb_scatter_donor_kv_paged(None, fake, fake, fake, fake, 4, 1, 16, 8, 4, 4, 1, st,
+                                       st, 2, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"null" in lib.sb_last_error_string()
+    # non-contiguous head_dim
+    bad = _i64(1, 1, 1, 1, 2)
+    rc = lib.sb_rope_correct_scatter_paged(fake, fake, fake, fake, fake, fake, 4, 1, 16, 8, 4,
+                                           4, 1, bad, _i64(1, 1, 1, 1), 2, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"contiguous" in lib.sb_last_error_string()
+    # odd head_dim for RoPE
+    rc = lib.sb_apply_rope_delta_inplace(fake, fake, fake, None, 3, 5, fake, 1, 16, 7, 4, 1,
+                                         _i64(1, 1, 1, 1), 2, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"even" in lib.sb_last_error_string()
+    # GQA head counts
+    rc = lib.sb_partial_attention_paged(fake, fake, fake, fake, fake, None, 0, 4, 7, 2, 128,
+                                        16, 8, 4, 1.0, _i64(1, 1, 1), _i64(1, 1, 1),
+                                        _i64(1, 1, 1, 1, 1), 2, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"multiple" in lib.sb_last_error_string()
+    # workspace too small for the dense drop-in
+    rc = lib.sb_partial_prefill_attention(fake, fake, fake, fake, fake, fake, 8, 2, 64, 128,
+                                          0.1, _i64(1, 1, 1), _i64(1, 1, 1), _i64(1, 1, 1),
+                                          _i64(1, 1, 1), 2, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"workspace" in lib.sb_last_error_string()
+
+
+def test_empty_calls_are_no_ops():
+    lib = _lib.lib()
+    st = _i64(1, 1, 1, 1, 1)
+    assert lib.sb_scatter_donor_kv_paged(None, None, None, None, None, 0, 1, 16, 8, 4, 4, 1, st,
+                                         st, 2, None) == _lib.SB_OK
+    assert lib.sb_apply_rope_delta_inplace(None, None, None, None, 0, 5, None, 1, 16, 8, 4, 1,
+                                           _i64(1, 1, 1, 1), 2, None) == _lib.SB_OK
+    assert lib.sb_last_error_string() == b""
+
+
+@pytest.mark.parametrize("dtype,expect_split", [(2, True), (0, False)])
+def test_workspace_size_queries(dtype, expect_split):
+    # 7B attention workload: 2458 rows, 28/4 heads, 16384 tokens in blocks of 16
+    n = _lib.size_query("sb_partial_attention_paged_workspace_size", 2458, 28, 4, 128, 16, 1024,
+                        dtype)
+    assert (n > 0) == expect_split  # fp32 takes the unsplit VALU kernel
+    dense = _lib.size_query("sb_partial_prefill_attention_workspace_size", 4, 1000, 128, dtype)
+    assert dense >= 1001 * 4

@@ -1,0 +1,198 @@
+"""Host-side logic of the package (no GPU): partial-attention plans, PositionMapping, module
+aliases, the sequential-copy resolution of NoPE V moves, the position normalisation of
+apply_rope_delta_inplace, the inv_freq table, and rejection of CPU tensors."""
+
+from __future__ import annotations
+
+import random
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref_cpu
+from semblend_amd import compat
+from semblend_amd import partial_attention as pa
+from semblend_amd import rope_correction as rc
+from semblend_amd import triton_kernels as tk
+from semblend_amd.pipeline import PositionMapping
+
+# ---- plans (synapse_kv_connector/tests/test_partial_attention.py) ----
+
+COPY = "copy_from_donor"
+
+
+def _acts(spec):
+    out = []
+    for kind, t, d in spec:
+        a = {"action": kind, "targetPos": t}
+        if d is not None:
+            a["donorPos"] = d
+        out.append(a)
+    return out
+
+
+def test_plan_basic():
+    plan = pa.build_attention_plan(
+        "d1", 5, 5, [0, 1, 3, 4], [2],
+        _acts([(COPY, 0, 0), (COPY, 1, 1), ("placeholder", 2, None), (COPY, 3, 3), (COPY, 4, 4)]),
+        num_layers=4)
+    assert (plan.target_len, plan.donor_len, plan.donor_id) == (5, 5, "d1")
+    assert (plan.num_reuse_positions, plan.num_partial_positions, plan.num_full_layers) == (4, 1, 0)
+    assert len(plan.layer_masks) == 4
+    assert abs(plan.computation_ratio - 0.2) < 1e-6
+    np.testing.assert_array_equal(pa.compute_attention_mask(plan, 0),
+                                  [False, False, True, False, False])
+    assert pa.compute_attention_mask(plan, 0).dtype == bool
+    assert pa.compute_donor_kv_indices(plan, 1) == [(0, 0), (1, 1), (3, 3), (4, 4)]
+
+
+def test_plan_layer_hints_and_ratio():
+    plan = pa.build_attention_plan(
+        "d2", 4, 4, [0, 1, 2], [3],
+        _acts([(COPY, 0, 0), (COPY, 1, 1), (COPY, 2, 2), ("placeholder", 3, None)]),
+        layer_hints=[{"recomputeAll": False, "deviationScore": 0.1},
+                     {"recomputeAll": True, "deviationScore": 0.5},
+                     {"recompute_all": False, "deviation_score": 0.2},
+                     {"recomputeAll": True, "deviationScore": 0.8}],
+        num_layers=4)
+    assert plan.num_full_layers == 2
+    assert [m.recompute_all for m in plan.layer_masks] == [False, True, False, True]
+    assert plan.layer_masks[2].deviation_score == 0.2
+    assert abs(plan.computation_ratio - 0.625) < 1e-6
+    assert pa.compute_attention_mask(plan, 1).all()
+    assert pa.compute_donor_kv_indices(plan, 1) == []
+    assert pa.compute_attention_mask(plan, 99).all()
+    assert pa.compute_donor_kv_indices(plan, 99) == []
+
+
+def test_plan_full_recompute_and_full_reuse():
+    plan = pa.build_attention_plan("d3", 3, 3, [], [0, 1, 2],
+                                   _acts([("placeholder", i, None) for i in range(3)]), num_layers=2)
+    assert plan.num_partial_positions == 3 and abs(plan.computation_ratio - 1.0) < 1e-6
+    plan = pa.build_attention_plan("d4", 3, 3, [0, 1, 2], [],
+                                   _acts([(COPY, i, i) for i in range(3)]), num_layers=2)
+    assert plan.num_reuse_positions == 3 and abs(plan.computation_ratio) < 1e-6
+
+
+def test_plan_ignores_recompute_action():
+    """build_attention_plan maps only copy_from_donor and placeholder
+    (semblend_core/partial_attention.py:140-156): a "recompute" slot adds no mask entry."""
+    plan = pa.build_attention_plan("d", 3, 3, [0], [1, 2],
+                                   _acts([(COPY, 0, 0), ("recompute", 1, None),
+                                          ("placeholder", 2, None)]), num_layers=1)
+    np.testing.assert_array_equal(pa.compute_attention_mask(plan, 0), [False, False, True])
+    assert plan.num_partial_positions == 2
+
+
+def test_multi_donor_plan():
+    acts = [{"action": COPY, "targetPos": 0, "donorPos": 4, "donorId": "a"},
+            {"action": COPY, "targetPos": 1, "donorPos": 9, "donorId": "b"},
+            {"action": COPY, "targetPos": 2, "donorPos": 5, "donorId": "a"},
+            {"action": "recompute", "targetPos": 3},
+            {"action": "placeholder", "targetPos": 4}]
+    plan = pa.build_multi_donor_attention_plan(5, acts, num_layers=3)
+    assert plan.donor_id == "a" and plan.donor_len == 10
+    assert plan.donor_map == ((0, "a"), (1, "b"), (2, "a"))
+    assert (plan.num_reuse_positions, plan.num_partial_positions) == (3, 1)
+    np.testing.assert_array_equal(pa.compute_attention_mask(plan, 0),
+                                  [False, False, False, True, False])
+    assert pa.compute_donor_kv_indices(plan, 2) == [(4, 0), (9, 1), (5, 2)]
+    assert abs(plan.computation_ratio - 1 / 5) < 1e-9
+    empty = pa.build_multi_donor_attention_plan(0, [], num_layers=0)
+    assert empty.donor_id == "" and empty.computation_ratio == 1.0
+
+
+def test_plan_types_frozen_and_enum_values():
+    m = pa.PositionMask(target_pos=0, mode=pa.AttentionMode.REUSE, donor_pos=3)
+    assert m.donor_pos == 3
+    assert pa.PositionMask(1, pa.AttentionMode.PARTIAL).donor_pos is None
+    with pytest.raises(AttributeError):
+        m.target_pos = 1  # type: ignore[misc]
+    assert [e.value for e in pa.AttentionMode] == ["full", "reuse", "partial", "skip_layer"]
+    assert pa.LayerMask(0, False, 0.0).verification_source == "bathtub"
+
+
+def test_position_mapping():
+    assert not PositionMapping([0, 1, 2], [0, 1, 2]).needs_correction
+    pm = PositionMapping([0, 1, 2, 3], [2, 3, 0, 1])
+    assert pm.needs_correction and pm.num_pairs == 4
+    assert PositionMapping().num_pairs == 0
+
+
+def test_compat_aliases():
+    names = compat.install()
+    assert "semblend_core.rope_correction" in names
+    import semblend_core.rope_correction as a  # noqa: E402
+    import synapse_kv_connector.triton_kernels as b  # noqa: E402
+    from synapse_kv_connector.partial_attention import build_attention_plan  # noqa: E402
+    assert a is rc and b is tk and build_attention_plan is pa.build_attention_plan
+    assert a.HAS_TRITON is False
+    for mod in ("semblend_core", "synapse_kv_connector"):
+        sys.modules.pop(mod + ".rope_correction", None)
+
+
+# ---- sequential V moves of nope_permute_paged_kv ----
+
+def test_sequential_v_moves_matches_brute_force():
+    rng = random.Random(7)
+    for _ in range(200):
+        n = rng.randint(1, 12)
+        perm = [(rng.randrange(10), rng.randrange(10)) for _ in range(n)]
+        state = {i: i for i in range(10)}   # position -> original row it holds
+        for s, t in perm:
+            state[t] = state[s]
+        moves = rc._sequential_v_moves(perm)
+        resolved = {i: i for i in range(10)}
+        for t, s in moves:
+            resolved[t] = s
+        assert resolved == state, perm
+
+
+# ---- apply_rope_delta_inplace host normalisation ----
+
+def test_rotation_counts():
+    counts, n = rc._rotation_counts([0, 5, 17, 17, 40, 127, 128, 300, -1, 64], 16, 8)
+    assert n == 8  # 128 and 300 lie past the 8-block table
+    assert counts == {0: 1, 5: 1, 17: 2, 40: 1, 127: 2, 64: 1}
+    with pytest.raises(IndexError):
+        rc._rotation_counts([-200], 16, 8)
+
+
+def test_rotation_counts_agree_with_oracle_count():
+    kv = torch.randn(10, 2, 2, 16, 8)
+    bt = torch.tensor([4, 2, 0, 9], dtype=torch.int32)
+    pos = [0, 3, 16, 16, 63, 64, 70, -1, -20]
+    _, n = rc._rotation_counts(pos, 16, 4)
+    assert n == ref_cpu.apply_rope_delta_inplace(kv, bt, pos, 3)
+
+
+def test_inv_freq_table_is_the_reference_expression():
+    for base, d in ((10000.0, 128), (1e6, 128), (5e5, 64), (500.0, 32)):
+        got = rc.inv_freq_table(base, d, torch.device("cpu"))
+        assert torch.equal(got, ref_cpu.inv_freq(base, d))
+
+
+# ---- no CPU path ----
+
+def test_cpu_tensors_are_rejected():
+    kv = torch.zeros(4, 2, 1, 4, 8)
+    donor = torch.zeros(2, 1, 8, 8)
+    idx = torch.tensor([0], dtype=torch.int32)
+    bt = torch.tensor([0, 1], dtype=torch.int32)
+    calls = [
+        lambda: tk.scatter_donor_kv(torch.zeros(1, 2, 1, 8, 8), torch.zeros(1, 2, 1, 8, 8), idx, idx),
+        lambda: tk.scatter_donor_kv_paged(kv, donor, bt, idx, idx),
+        lambda: tk.partial_prefill_attention(torch.zeros(1, 4, 8), torch.zeros(1, 4, 8),
+                                             torch.zeros(1, 4, 8), torch.ones(4, dtype=torch.bool)),
+        lambda: tk.partial_prefill_attention_paged(torch.zeros(1, 1, 8), kv, bt, idx),
+        lambda: rc.rope_correct_scatter_paged(kv, donor, bt, idx, idx),
+        lambda: rc.rope_correct_k(torch.zeros(1, 4, 8), idx, idx, head_dim=8),
+        lambda: rc.apply_rope_delta_inplace(kv, bt, [0], 3),
+        lambda: rc.permute_paged_kv_with_rope(kv, bt, [(0, 1)]),
+        lambda: rc.nope_permute_paged_kv(kv, bt, [(0, 1)]),
+    ]
+    for call in calls:
+        with pytest.raises(RuntimeError, match="device tensors"):
+            call()
