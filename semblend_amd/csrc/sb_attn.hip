@@ -16,11 +16,14 @@
 //   * O^T += V^T P^T with the same MFMA: P^T comes straight from the S^T accumulators
 //     (after exp2 and conversion) as the B operand; the key order inside each 16-key step is
 //     permuted consistently in both operands, so no cross-lane shuffles are needed. V is
-//     stored transposed in LDS (Vt[d][key]) so each lane reads its 8 keys as two 8-byte words.
+//     stored transposed in LDS (Vt[d][key]) with the middle key quads of every 16-key group
+//     swapped, so the 8 keys a lane needs are contiguous: one ds_read_b128 per fragment
+//     (two 8-byte reads at the natural column order run 4x slower on gfx950).
 //   * K/V tiles are double-buffered: the global loads of tile i+1 are issued into registers
 //     before tile i is computed and written to the other LDS buffer afterwards, so one
-//     barrier per tile separates the stages. The block-table slice of the chunk is staged in
-//     LDS once, so tile addresses need no dependent global load.
+//     barrier per tile separates the stages. Row addresses come from per-tile key-offset
+//     tables in LDS (built from the chunk's block-table slice, also staged in LDS), so the
+//     loads are branch-free and need no index arithmetic.
 //   * Online softmax in the log2 domain with a lazily updated reference max: the running
 //     reference only moves (and O is only rescaled) when a row's max grows by more than
 //     2^8, which keeps every p <= 256 and removes almost all rescaling work. O / l is
@@ -40,8 +43,14 @@ namespace sb {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kTileRows = 128;  // flattened query rows per workgroup
+constexpr int kWaveRows = 32;   // flattened query rows per MFMA row group
+#ifndef SB_ATTN_ROW_GROUPS
+#define SB_ATTN_ROW_GROUPS 1
+#endif
+// Row groups per wave: each K/V fragment read from LDS feeds this many MFMAs.
+constexpr int kRowGroups = SB_ATTN_ROW_GROUPS;
 constexpr int kTileKeys = 64;   // keys per LDS tile
 constexpr int kBtLds = 1024;    // block-table entries staged per chunk
 constexpr float kLazyMax = 8.f; // log2 growth of a row max that forces a rescale
@@ -73,6 +82,7 @@ struct AttnArgs {
   int ksplit;                 // keys per work item (multiple of kTileKeys)
   int max_chunks;             // ceil(kv_len / ksplit)
   int64_t n_tiles;            // row tiles per kv head used for the partial layout
+  int tile_rows;              // flattened query rows per workgroup tile
   float* part_o;              // [Hkv][n_tiles][max_chunks][128][D] fp32, or nullptr
   float* part_ml;             // [Hkv][n_tiles][max_chunks][128][2] fp32 (m, l)
 };
@@ -145,6 +155,14 @@ template <> struct Mma<SB_DTYPE_F16> {
   __device__ __forceinline__ static uint16_t cvt1(float f) { return f32_to_f16(f); }
 };
 
+// Column of key `k` (0..63) in the transposed V tile. Within every 16-key group the middle
+// two quads are swapped (bits 2 and 3 of k exchanged), so that the keys one lane feeds to
+// a 16-wide PV step -- {4h..4h+3, 8+4h..8+4h+3} for lane half h -- are contiguous.
+// Adjacent key pairs stay adjacent, so the transposing store writes whole dwords.
+__device__ __forceinline__ int vt_column(int k) {
+  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
 // Work-item decode shared by the attention and merge kernels.
 struct Item {
   int kvh;
@@ -164,20 +182,23 @@ __device__ __forceinline__ Item decode_item(const AttnArgs& a, int64_t n_tiles_l
   return it;
 }
 
-template <int DT, int D>
-__global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnArgs a) {
+template <int DT, int D, int RG>
+__global__ __launch_bounds__(256, RG == 1 ? 2 : 1) void attn_mfma_kernel(AttnArgs a) {
   using M = Mma<DT>;
   using vec8 = typename M::vec8;
-  constexpr int KSTR = D + 8;          // K tile row stride (elements)
-  constexpr int VSTR = kTileKeys + 4;  // transposed V row stride (elements)
-  constexpr int NKS = D / 16;          // QK^T k-steps
-  constexpr int NDT = D / 32;          // PV output d-tiles
-  constexpr int CH = D / 8;            // 16-byte chunks per row
+  constexpr int TR = kWaveRows * RG * 4;  // flattened rows per workgroup tile
+  constexpr int KSTR = D + 8;             // K tile row stride (elements)
+  constexpr int VSTR = kTileKeys + 8;     // transposed V row stride (elements, 144 bytes)
+  constexpr int NKS = D / 16;             // QK^T k-steps
+  constexpr int NDT = D / 32;             // PV output d-tiles
+  constexpr int CH = D / 8;               // 16-byte chunks per row
   constexpr int KLD = kTileKeys * CH / 256;  // K vectors loaded per thread per tile
   constexpr int VLD = CH / 8;                // V key-pair passes per thread per tile
   __shared__ __align__(16) uint16_t Ks[2][kTileKeys * KSTR];
   __shared__ __align__(16) uint16_t Vt[2][D * VSTR];
   __shared__ int bt_s[kBtLds];
+  __shared__ uint64_t kofs[2][kTileKeys];  // per-key byte offsets of K rows (double-buffered)
+  __shared__ uint64_t vofs[2][kTileKeys];  // ... and of V rows
   __shared__ int red_max[4];
 
   const int tid = threadIdx.x;
@@ -188,26 +209,32 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnArgs a) {
 
   const int64_t n_rows = attn_num_rows(a);
   const int64_t rows_kv = n_rows * a.group;
-  const int64_t n_tiles_live = (rows_kv + kTileRows - 1) / kTileRows;
+  const int64_t n_tiles_live = (rows_kv + TR - 1) / TR;
   const Item item = decode_item(a, n_tiles_live);
   if (item.tile < 0 || item.chunk >= a.max_chunks) return;  // uniform, before any barrier
   const int kvh = item.kvh;
 
-  // This lane's query row.
-  const int row_in_tile = wave * 32 + lq;
-  const int64_t r = item.tile * kTileRows + row_in_tile;
-  int p = -1;
-  int64_t qrow = 0;
-  int qh = 0;
-  if (r < rows_kv) {
-    const int64_t pi = r / a.group;
-    qh = kvh * a.group + static_cast<int>(r - pi * a.group);
-    p = a.positions[pi];
-    if (p >= a.kv_len) p = static_cast<int>(a.kv_len - 1);
-    qrow = a.q_by_position ? p : pi;
-    if (p < 0) p = -1;
+  // This lane's query rows: one per row group.
+  int p[RG], qh[RG];
+  int64_t qrow[RG];
+  int pmax_l = -1;
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    const int64_t r = item.tile * TR + (wave * RG + g) * kWaveRows + lq;
+    p[g] = -1;
+    qrow[g] = 0;
+    qh[g] = 0;
+    if (r < rows_kv) {
+      const int64_t pi = r / a.group;
+      qh[g] = kvh * a.group + static_cast<int>(r - pi * a.group);
+      int pp = a.positions[pi];
+      if (pp >= a.kv_len) pp = static_cast<int>(a.kv_len - 1);
+      qrow[g] = a.q_by_position ? pp : pi;
+      p[g] = pp < 0 ? -1 : pp;
+    }
+    pmax_l = max(pmax_l, p[g]);
   }
-  const int pmax_w = wave_max_i(p);
+  const int pmax_w = wave_max_i(pmax_l);
   if (lane == 0) red_max[wave] = pmax_w;
   __syncthreads();
   const int kend = max(max(red_max[0], red_max[1]), max(red_max[2], red_max[3])) + 1;
@@ -215,220 +242,272 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(AttnArgs a) {
   if (k0 >= kend) return;  // uniform: kend comes from shared memory
   const int k1 = min(k0 + a.ksplit, kend);
   const int nchunks = (kend + a.ksplit - 1) / a.ksplit;
-  const int plim = min(p, k1 - 1);                 // keys beyond the chunk are masked
-  const int pmin_w = wave_min_i(p >= 0 ? plim : 0x7fffffff);
+  int plim[RG];  // keys beyond the chunk are masked as well
+  int pmin_l = 0x7fffffff;
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    plim[g] = min(p[g], k1 - 1);
+    if (p[g] >= 0) pmin_l = min(pmin_l, plim[g]);
+  }
+  const int pmin_w = wave_min_i(pmin_l);
   const int pmax_c = min(pmax_w, k1 - 1);
 
-  vec8 qf[NKS];
-  {
-    const char* qp = a.q + qrow * a.q_s_row + qh * a.q_s_head;
+  // Q fragments (B operand). For a negative scale Q is negated, so that the softmax can
+  // always take its max over the raw scores: scale * q.k = |scale| * (-q).k.
+  const uint32_t qflip = a.scale_log2 < 0.f ? 0x80008000u : 0u;
+  const float c = fabsf(a.scale_log2);
+  vec8 qf[RG][NKS];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    const char* qp = a.q + qrow[g] * a.q_s_row + qh[g] * a.q_s_head;
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
       uint4 w = make_uint4(0, 0, 0, 0);
-      if (p >= 0) w = *reinterpret_cast<const uint4*>(qp + (16 * s + 8 * lg) * 2);
-      qf[s] = __builtin_bit_cast(vec8, w);
+      if (p[g] >= 0) w = *reinterpret_cast<const uint4*>(qp + (16 * s + 8 * lg) * 2);
+      w.x ^= qflip; w.y ^= qflip; w.z ^= qflip; w.w ^= qflip;
+      qf[g][s] = __builtin_bit_cast(vec8, w);
     }
   }
 
-  // Stage the chunk's block-table slice.
+  // Stage the chunk's block-table slice, then the key-offset tables of the first two tiles.
   int lb0 = 0;
-  const bool bt_in_lds = a.paged && a.bs_log2 >= 0;
-  if (bt_in_lds) {
-    lb0 = k0 >> a.bs_log2;
-    const int nb = ((k1 - 1) >> a.bs_log2) - lb0 + 1;
+  if (a.paged) {
+    lb0 = static_cast<int>(k0 / a.block_size);
+    const int nb = static_cast<int>((k1 - 1) / a.block_size) - lb0 + 1;
     for (int i = tid; i < nb; i += 256) bt_s[i] = clamp_block(a, a.block_table[lb0 + i]);
     __syncthreads();
   }
-  auto row_addr = [&](const char* base, int64_t s_head, int64_t s_seq, int key) -> const char* {
-    if (bt_in_lds) {
-      const int pb = bt_s[(key >> a.bs_log2) - lb0];
-      return base + pb * a.s_block + kvh * s_head +
-             static_cast<int64_t>(key & ((1 << a.bs_log2) - 1)) * a.s_pos;
-    }
-    return key_row(a, base, s_head, s_seq, key, kvh);
-  };
-
-  // Register staging of one tile.
-  uint4 kreg[KLD];
-  uint4 vreg[VLD][2];
-  auto load_tile = [&](int t0) {
-#pragma unroll
-    for (int i = 0; i < KLD; ++i) {
-      const int key = i * (256 / CH) + tid / CH;
-      const int kk = t0 + key;
-      kreg[i] = make_uint4(0, 0, 0, 0);
-      if (kk < k1)
-        kreg[i] = *reinterpret_cast<const uint4*>(row_addr(a.k, a.k_s_head, a.k_s_seq, kk) +
-                                                  (tid % CH) * 16);
-    }
-#pragma unroll
-    for (int ps = 0; ps < VLD; ++ps) {
-      const int m = tid & 31;
-      const int ch = (tid >> 5) + 8 * ps;
-      const int kk = t0 + 2 * m;
-      vreg[ps][0] = make_uint4(0, 0, 0, 0);
-      vreg[ps][1] = make_uint4(0, 0, 0, 0);
-      if (kk < k1)
-        vreg[ps][0] = *reinterpret_cast<const uint4*>(
-            row_addr(a.v, a.v_s_head, a.v_s_seq, kk) + ch * 16);
-      if (kk + 1 < k1)
-        vreg[ps][1] = *reinterpret_cast<const uint4*>(
-            row_addr(a.v, a.v_s_head, a.v_s_seq, kk + 1) + ch * 16);
+  const char* kbase = a.k + kvh * a.k_s_head;
+  const char* vbase = a.v + kvh * a.v_s_head;
+  // Byte offsets of key `key` (clamped into [k0, k1)) relative to kbase / vbase.
+  auto fill_offsets = [&](int buf, int t0, int i) {
+    const int key = min(t0 + i, k1 - 1);
+    if (a.paged) {
+      const int lb = key / static_cast<int>(a.block_size);
+      const uint64_t off = static_cast<uint64_t>(bt_s[lb - lb0]) * a.s_block +
+                           static_cast<uint64_t>(key - lb * a.block_size) * a.s_pos;
+      kofs[buf][i] = off;
+      vofs[buf][i] = off;
+    } else {
+      kofs[buf][i] = static_cast<uint64_t>(key) * a.k_s_seq;
+      vofs[buf][i] = static_cast<uint64_t>(key) * a.v_s_seq;
     }
   };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KLD; ++i) {
-      const int key = i * (256 / CH) + tid / CH;
-      *reinterpret_cast<uint4*>(&Ks[buf][key * KSTR + (tid % CH) * 8]) = kreg[i];
-    }
-#pragma unroll
-    for (int ps = 0; ps < VLD; ++ps) {
-      const int m = tid & 31;
-      const int ch = (tid >> 5) + 8 * ps;
-      const uint32_t x0[4] = {vreg[ps][0].x, vreg[ps][0].y, vreg[ps][0].z, vreg[ps][0].w};
-      const uint32_t x1[4] = {vreg[ps][1].x, vreg[ps][1].y, vreg[ps][1].z, vreg[ps][1].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t lo = (x0[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        const uint32_t hi = (x1[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        *reinterpret_cast<uint32_t*>(&Vt[buf][(ch * 8 + e) * VSTR + 2 * m]) = lo | (hi << 16);
-      }
-    }
-  };
-
-  const float c = a.scale_log2;
-  float m_ref = -INFINITY;  // reference max (log2 domain) O and l are relative to
-  float l_run = 0.f;
-  f32x16_t o[NDT];
-#pragma unroll
-  for (int t = 0; t < NDT; ++t)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[t][i] = 0.f;
-
-  load_tile(k0);
-  store_tile(0);
+  if (tid < kTileKeys) fill_offsets(0, k0, tid);
+  else if (tid < 2 * kTileKeys) fill_offsets(1, k0 + kTileKeys, tid - kTileKeys);
   __syncthreads();
 
-  int buf = 0;
-  for (int t0 = k0; t0 < k1; t0 += kTileKeys) {
+  float m_ref[RG], l_run[RG];
+  f32x16_t o[RG][NDT];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    m_ref[g] = -INFINITY;  // reference max (log2 domain) O and l are relative to
+    l_run[g] = 0.f;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[g][t][i] = 0.f;
+  }
+
+  // Software pipeline over tiles of kTileKeys keys. Iteration t0 issues the global loads of
+  // tile t0 + kTileKeys into registers, computes tile t0 from LDS buffer `buf`, then writes
+  // the registers to the other buffer; one barrier per iteration. The first iteration
+  // (t0 = k0 - kTileKeys) only stages tile k0. Loads are unconditional: every offset in the
+  // tables is a valid row.
+  int buf = 1;
+  for (int t0 = k0 - kTileKeys; t0 < k1; t0 += kTileKeys) {
     const bool more = t0 + kTileKeys < k1;
-    if (more) load_tile(t0 + kTileKeys);
+    // Native vector types (not HIP's uint4 struct) keep the staging values in registers.
+    u32x4_t kreg[KLD];
+    u32x4_t vreg[VLD][2];
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < KLD; ++i) {
+        const int key = i * (256 / CH) + tid / CH;
+        kreg[i] =
+            *reinterpret_cast<const u32x4_t*>(kbase + kofs[buf ^ 1][key] + (tid % CH) * 16);
+      }
+#pragma unroll
+      for (int ps = 0; ps < VLD; ++ps) {
+        const int m = tid & 31;
+        const int ch = (tid >> 5) + 8 * ps;
+        vreg[ps][0] = *reinterpret_cast<const u32x4_t*>(vbase + vofs[buf ^ 1][2 * m] + ch * 16);
+        vreg[ps][1] =
+            *reinterpret_cast<const u32x4_t*>(vbase + vofs[buf ^ 1][2 * m + 1] + ch * 16);
+      }
+    }
+    if (t0 >= k0 && t0 + 2 * kTileKeys < k1 && tid < kTileKeys)
+      fill_offsets(buf, t0 + 2 * kTileKeys, tid);
 
-    if (t0 <= pmax_c) {
-      // ---- S^T = K Q^T for two 32-key subtiles ----
-      f32x16_t s[2];
+    if (t0 >= k0 && t0 <= pmax_c) {
+      // ---- S^T = K Q^T for both 32-key halves. (half, k-step) pairs alternate halves, so
+      // two independent accumulation chains interleave; K fragments stream through a
+      // 4-deep ring so every ds_read is issued four MFMAs before it is consumed. ----
+      constexpr int NQ = 2 * NKS;
+      f32x16_t s[RG][2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int g = 0; g < RG; ++g)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[j][i] = 0.f;
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const vec8 kf = *reinterpret_cast<const vec8*>(
-              &Ks[buf][(32 * j + lq) * KSTR + 16 * ks + 8 * lg]);
-          s[j] = M::mma(kf, qf[ks], s[j]);
+          for (int i = 0; i < 16; ++i) s[g][j][i] = 0.f;
+      vec8 ring[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+        ring[n] = *reinterpret_cast<const vec8*>(
+            &Ks[buf][(32 * (n & 1) + lq) * KSTR + 16 * (n >> 1) + 8 * lg]);
+#pragma unroll
+      for (int n = 0; n < NQ; ++n) {
+        const vec8 kf = ring[n & 3];
+        if (n + 4 < NQ) {
+          const int m = n + 4;
+          ring[n & 3] = *reinterpret_cast<const vec8*>(
+              &Ks[buf][(32 * (m & 1) + lq) * KSTR + 16 * (m >> 1) + 8 * lg]);
+        }
+#pragma unroll
+        for (int g = 0; g < RG; ++g) s[g][n & 1] = M::mma(kf, qf[g][n >> 1], s[g][n & 1]);
+      }
+      // ---- causal / chunk-end mask, only on tiles that cross some row's last key ----
+      if (t0 + kTileKeys - 1 > pmin_w) {
+#pragma unroll
+        for (int g = 0; g < RG; ++g)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int lim = plim[g] - (t0 + 32 * j + 4 * lg);  // key offset limit of this lane
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+              if (8 * (i >> 2) + (i & 3) > lim) s[g][j][i] = -INFINITY;
+          }
+      }
+      // ---- tile row max; the reference moves (and O is rescaled) only when a row's max
+      // grows by more than 2^kLazyMax, which is rare after the first tiles ----
+      float mx[RG];
+      bool bump_any = false;
+#pragma unroll
+      for (int g = 0; g < RG; ++g) {
+        float v = fmaxf(s[g][0][0], s[g][1][0]);
+#pragma unroll
+        for (int i = 1; i < 16; ++i) v = fmaxf(v, fmaxf(s[g][0][i], s[g][1][i]));
+        mx[g] = fmaxf(v, __shfl_xor(v, 32, 64)) * c;
+        bump_any |= mx[g] > m_ref[g] + kLazyMax;
+      }
+      if (__any(bump_any)) {
+#pragma unroll
+        for (int g = 0; g < RG; ++g) {
+          const bool bump = mx[g] > m_ref[g] + kLazyMax;
+          const float m_new = bump ? mx[g] : m_ref[g];
+          // 1 when this row keeps its reference, 0 when it had none (O and l are still 0).
+          const float alpha = bump ? __builtin_amdgcn_exp2f(m_ref[g] - m_new) : 1.f;
+          l_run[g] *= alpha;
+#pragma unroll
+          for (int t = 0; t < NDT; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[g][t][i] *= alpha;
+          m_ref[g] = m_new;
         }
       }
-      // ---- online softmax (log2 domain, lazy reference) ----
-      const bool need_mask = t0 + kTileKeys - 1 > pmin_w;
-      float mx = -INFINITY;
+      // ---- P = exp2(s * c - m) and O^T += V^T P^T. V fragments (two 8-byte reads each)
+      // stream through a 4-deep ring over the (half, step, d-tile) sequence. ----
+      vec8 pb[RG][2][2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int g = 0; g < RG; ++g) {
+        const float nm = m_ref[g] == -INFINITY ? 0.f : -m_ref[g];
+        float lsum = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float v = s[j][i] * c;
-          if (need_mask) {
-            const int kk = t0 + 32 * j + 8 * (i >> 2) + 4 * lg + (i & 3);
-            if (kk > plim) v = -INFINITY;
+        for (int j = 0; j < 2; ++j) {
+          float pf[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            pf[i] = __builtin_amdgcn_exp2f(fmaf(s[g][j][i], c, nm));
+            lsum += pf[i];
           }
-          s[j][i] = v;
-          mx = fmaxf(mx, v);
+          pb[g][j][0] = M::cvt8(pf);
+          pb[g][j][1] = M::cvt8(pf + 8);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // Move the reference only when the max grows by more than 2^kLazyMax.
-      const bool bump = mx > m_ref + kLazyMax;
-      if (__any(bump)) {
-        const float m_new = bump ? mx : m_ref;
-        // 1 when this row keeps its reference, 0 when it had none (O and l are still 0).
-        const float alpha = bump ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.f;
-        l_run *= alpha;
-#pragma unroll
-        for (int t = 0; t < NDT; ++t)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) o[t][i] *= alpha;
-        m_ref = m_new;
+        l_run[g] += lsum;
       }
-      const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
-      float lsum = 0.f;
+      constexpr int NV = 4 * NDT;  // (half, step, d-tile) triples
+      vec8 vring[4];
+      // With the column permutation of vt_column, the 8 keys a lane needs for one step are
+      // 16 contiguous bytes: a single ds_read_b128.
+      auto vfrag = [&](int n) -> vec8 {
+        const int t = n % NDT, st = (n / NDT) & 1, j = n / (2 * NDT);
+        return *reinterpret_cast<const vec8*>(
+            &Vt[buf][(32 * t + lq) * VSTR + 32 * j + 16 * st + 8 * lg]);
+      };
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int n = 0; n < 4; ++n) vring[n] = vfrag(n);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float pv = __builtin_amdgcn_exp2f(s[j][i] - m_use);
-          s[j][i] = pv;
-          lsum += pv;
-        }
-      l_run += lsum;
-
-      // ---- O^T += V^T P^T ----
+      for (int n = 0; n < NV; ++n) {
+        const vec8 va = vring[n & 3];
+        if (n + 4 < NV) vring[n & 3] = vfrag(n + 4);
+        const int t = n % NDT, st = (n / NDT) & 1, j = n / (2 * NDT);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+        for (int g = 0; g < RG; ++g) o[g][t] = M::mma(va, pb[g][j][st], o[g][t]);
+      }
+    }
+    if (more) {
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          float pf[8];
+      for (int i = 0; i < KLD; ++i) {
+        const int key = i * (256 / CH) + tid / CH;
+        *reinterpret_cast<u32x4_t*>(&Ks[buf ^ 1][key * KSTR + (tid % CH) * 8]) = kreg[i];
+      }
 #pragma unroll
-          for (int e = 0; e < 8; ++e) pf[e] = s[j][8 * st + e];
-          const vec8 pb = M::cvt8(pf);
-          const int kb = 32 * j + 16 * st + 4 * lg;
+      for (int ps = 0; ps < VLD; ++ps) {
+        const int m = tid & 31;
+        const int ch = (tid >> 5) + 8 * ps;
+        const int col = vt_column(2 * m);
 #pragma unroll
-          for (int t = 0; t < NDT; ++t) {
-            const uint16_t* vrow = &Vt[buf][(32 * t + lq) * VSTR + kb];
-            const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-            const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
-            const vec8 va = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-            o[t] = M::mma(va, pb, o[t]);
-          }
+        for (int w = 0; w < 4; ++w) {
+          // (key 2m, key 2m+1) pairs of elements 2w and 2w+1 of the 8-element chunk
+          const uint32_t lo = __builtin_amdgcn_perm(vreg[ps][1][w], vreg[ps][0][w], 0x05040100u);
+          const uint32_t hi = __builtin_amdgcn_perm(vreg[ps][1][w], vreg[ps][0][w], 0x07060302u);
+          *reinterpret_cast<uint32_t*>(&Vt[buf ^ 1][(ch * 8 + 2 * w) * VSTR + col]) = lo;
+          *reinterpret_cast<uint32_t*>(&Vt[buf ^ 1][(ch * 8 + 2 * w + 1) * VSTR + col]) = hi;
         }
       }
     }
-    if (more) store_tile(buf ^ 1);
     __syncthreads();
     buf ^= 1;
   }
 
-  // ---- finish: lane holds d = 32t + 8*(i/4) + 4*lg + (i%4) of its row ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if (p < 0) return;
-  if (nchunks == 1) {
-    const float inv = 1.f / l_tot;
-    char* op = a.o + qrow * a.o_s_row + qh * a.o_s_head;
+  // ---- finish: lane holds d = 32t + 8*(i/4) + 4*lg + (i%4) of each of its rows ----
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
+  for (int g = 0; g < RG; ++g) {
+    const float l_tot = l_run[g] + __shfl_xor(l_run[g], 32, 64);
+    if (p[g] < 0) continue;
+    const int row_in_tile = (wave * RG + g) * kWaveRows + lq;
+    if (nchunks == 1) {
+      const float inv = 1.f / l_tot;
+      char* op = a.o + qrow[g] * a.o_s_row + qh[g] * a.o_s_head;
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int d0 = 32 * t + 8 * qd + 4 * lg;
-        const uint32_t w0 = static_cast<uint32_t>(M::cvt1(o[t][4 * qd] * inv)) |
-                            (static_cast<uint32_t>(M::cvt1(o[t][4 * qd + 1] * inv)) << 16);
-        const uint32_t w1 = static_cast<uint32_t>(M::cvt1(o[t][4 * qd + 2] * inv)) |
-                            (static_cast<uint32_t>(M::cvt1(o[t][4 * qd + 3] * inv)) << 16);
-        *reinterpret_cast<uint2*>(op + d0 * 2) = make_uint2(w0, w1);
-      }
-  } else {
-    const int64_t slot =
-        ((static_cast<int64_t>(kvh) * a.n_tiles + item.tile) * a.max_chunks + item.chunk) *
-            kTileRows + row_in_tile;
-    float* po = a.part_o + slot * D;
+      for (int t = 0; t < NDT; ++t)
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
+        for (int qd = 0; qd < 4; ++qd) {
+          const int d0 = 32 * t + 8 * qd + 4 * lg;
+          const uint32_t w0 = static_cast<uint32_t>(M::cvt1(o[g][t][4 * qd] * inv)) |
+                              (static_cast<uint32_t>(M::cvt1(o[g][t][4 * qd + 1] * inv)) << 16);
+          const uint32_t w1 = static_cast<uint32_t>(M::cvt1(o[g][t][4 * qd + 2] * inv)) |
+                              (static_cast<uint32_t>(M::cvt1(o[g][t][4 * qd + 3] * inv)) << 16);
+          *reinterpret_cast<uint2*>(op + d0 * 2) = make_uint2(w0, w1);
+        }
+    } else {
+      const int64_t slot =
+          ((static_cast<int64_t>(kvh) * a.n_tiles + item.tile) * a.max_chunks + item.chunk) *
+              TR + row_in_tile;
+      float* po = a.part_o + slot * D;
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int d0 = 32 * t + 8 * qd + 4 * lg;
-        *reinterpret_cast<float4*>(po + d0) =
-            make_float4(o[t][4 * qd], o[t][4 * qd + 1], o[t][4 * qd + 2], o[t][4 * qd + 3]);
-      }
-    if (lg == 0)
-      *reinterpret_cast<float2*>(a.part_ml + slot * 2) =
-          make_float2(l_tot > 0.f ? m_ref : -INFINITY, l_tot);
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const int d0 = 32 * t + 8 * qd + 4 * lg;
+          *reinterpret_cast<float4*>(po + d0) = make_float4(
+              o[g][t][4 * qd], o[g][t][4 * qd + 1], o[g][t][4 * qd + 2], o[g][t][4 * qd + 3]);
+        }
+      if (lg == 0)
+        *reinterpret_cast<float2*>(a.part_ml + slot * 2) =
+            make_float2(l_tot > 0.f ? m_ref[g] : -INFINITY, l_tot);
+    }
   }
 }
 
@@ -438,16 +517,18 @@ template <int DT>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
   __shared__ int red[4];
   const int tid = threadIdx.x;
+  const int TR = a.tile_rows;              // 128 or 256
   const int64_t n_rows = attn_num_rows(a);
   const int64_t rows_kv = n_rows * a.group;
-  const int64_t n_tiles_live = (rows_kv + kTileRows - 1) / kTileRows;
+  const int64_t n_tiles_live = (rows_kv + TR - 1) / TR;
   const int kvh = static_cast<int>(blockIdx.x % a.num_kv_heads);
   const int64_t tile = static_cast<int64_t>(blockIdx.x / a.num_kv_heads);
   if (tile >= n_tiles_live) return;
-  // Two threads per row, each owning half of head_dim.
-  const int row_in_tile = tid >> 1;
-  const int half = tid & 1;
-  const int64_t r = tile * kTileRows + row_in_tile;
+  // 256 / TR threads per row, each owning a contiguous part of head_dim.
+  const int tpr = 256 / TR;
+  const int row_in_tile = tid / tpr;
+  const int part = tid % tpr;
+  const int64_t r = tile * TR + row_in_tile;
   int p = -1;
   int64_t qrow = 0;
   int qh = 0;
@@ -468,20 +549,20 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
   const int64_t base = (static_cast<int64_t>(kvh) * a.n_tiles + tile) * a.max_chunks;
   float mmax = -INFINITY;
   for (int ch = 0; ch < nchunks; ++ch)
-    mmax = fmaxf(mmax, a.part_ml[((base + ch) * kTileRows + row_in_tile) * 2]);
+    mmax = fmaxf(mmax, a.part_ml[((base + ch) * TR + row_in_tile) * 2]);
   float lsum = 0.f;
   for (int ch = 0; ch < nchunks; ++ch) {
     const float2 ml =
-        *reinterpret_cast<const float2*>(a.part_ml + ((base + ch) * kTileRows + row_in_tile) * 2);
+        *reinterpret_cast<const float2*>(a.part_ml + ((base + ch) * TR + row_in_tile) * 2);
     if (ml.x != -INFINITY) lsum += __builtin_amdgcn_exp2f(ml.x - mmax) * ml.y;
   }
   const float inv = 1.f / lsum;
   char* op = a.o + qrow * a.o_s_row + qh * a.o_s_head;
-  const int d_begin = half * (D / 2);
-  for (int d = d_begin; d < d_begin + D / 2; d += 4) {
+  const int d_begin = part * (D / tpr);
+  for (int d = d_begin; d < d_begin + D / tpr; d += 4) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int ch = 0; ch < nchunks; ++ch) {
-      const int64_t slot = (base + ch) * kTileRows + row_in_tile;
+      const int64_t slot = (base + ch) * TR + row_in_tile;
       const float m = a.part_ml[slot * 2];
       if (m == -INFINITY) continue;
       const float w = __builtin_amdgcn_exp2f(m - mmax);
@@ -630,7 +711,10 @@ __global__ void zero_rows_kernel(char* out, const uint8_t* mask, int64_t num_hea
 
 namespace {
 
-constexpr int kAssumedSlots = 512;  // resident workgroups of the MFMA kernel on 256 CUs
+// Resident workgroups of the MFMA kernel on 256 CUs (one 4-wave workgroup per CU with two
+// row groups per wave, two with one), and how many work items per slot the split aims for.
+constexpr int kResidentSlots = kRowGroups == 1 ? 512 : 256;
+constexpr int kItemsPerSlot = 1;
 
 bool mfma_path(int32_t dtype, int64_t head_dim) {
   return (dtype == SB_DTYPE_BF16 || dtype == SB_DTYPE_F16) &&
@@ -641,6 +725,7 @@ bool mfma_path(int32_t dtype, int64_t head_dim) {
 struct Plan {
   int ksplit;
   int max_chunks;
+  int tile_rows;
   int64_t n_tiles;
   int64_t part_bytes;  // bytes of partials (O then m/l), 0 when no tile splits
 };
@@ -648,24 +733,26 @@ struct Plan {
 Plan make_plan(int64_t rows_upper, int64_t group, int64_t num_kv_heads, int64_t kv_len,
                int64_t head_dim, int64_t block_size, bool paged) {
   Plan pl{};
-  pl.n_tiles = (rows_upper * group + kTileRows - 1) / kTileRows;
+  pl.tile_rows = kWaveRows * kRowGroups * 4;
+  pl.n_tiles = (rows_upper * group + pl.tile_rows - 1) / pl.tile_rows;
   const int64_t kv_pad = (kv_len + kTileKeys - 1) / kTileKeys * kTileKeys;
-  // Aim for items no longer than the average work per resident workgroup, assuming the
-  // rows' key ranges average half the context.
-  int64_t ks = pl.n_tiles * num_kv_heads * (kv_len / 2) / kAssumedSlots;
+  // Items no longer than the average work per slot (assuming the rows' key ranges average
+  // half the context), so that longest-first scheduling balances the CUs.
+  int64_t ks = pl.n_tiles * num_kv_heads * (kv_len / 2) / (kResidentSlots * kItemsPerSlot);
   ks = ks / kTileKeys * kTileKeys;
   if (ks < 512) ks = 512;
   if (paged) {
-    int64_t cap = static_cast<int64_t>(kBtLds) * block_size / kTileKeys * kTileKeys;
+    const int64_t cap = static_cast<int64_t>(kBtLds) * block_size / kTileKeys * kTileKeys;
     if (ks > cap) ks = cap;
   }
   if (ks > kv_pad) ks = kv_pad;
   if (ks < kTileKeys) ks = kTileKeys;
-  int64_t chunks = (kv_len + ks - 1) / ks;
+  const int64_t chunks = (kv_len + ks - 1) / ks;
   pl.ksplit = static_cast<int>(ks);
   pl.max_chunks = static_cast<int>(chunks < 1 ? 1 : chunks);
   if (pl.max_chunks > 1)
-    pl.part_bytes = num_kv_heads * pl.n_tiles * pl.max_chunks * kTileRows * (head_dim + 2) * 4;
+    pl.part_bytes =
+        num_kv_heads * pl.n_tiles * pl.max_chunks * pl.tile_rows * (head_dim + 2) * 4;
   return pl;
 }
 
@@ -679,11 +766,12 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
     a.ksplit = pl.ksplit;
     a.max_chunks = pl.max_chunks;
     a.n_tiles = pl.n_tiles;
+    a.tile_rows = pl.tile_rows;
     if (pl.part_bytes > 0) {
       if (!workspace || workspace_bytes < pl.part_bytes)
         return fail(fn, "workspace too small for the split-key partials");
       a.part_o = static_cast<float*>(workspace);
-      a.part_ml = a.part_o + a.num_kv_heads * pl.n_tiles * pl.max_chunks * kTileRows *
+      a.part_ml = a.part_o + a.num_kv_heads * pl.n_tiles * pl.max_chunks * pl.tile_rows *
                                  static_cast<int64_t>(a.head_dim);
     }
     const int64_t gx = pl.n_tiles * a.num_kv_heads * pl.max_chunks;
@@ -692,7 +780,7 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
     dim3 mgrid(static_cast<unsigned>(pl.n_tiles * a.num_kv_heads));
 #define SB_ATT_CASE(DT, D)                                                              \
   if (dtype == DT && a.head_dim == D) {                                                 \
-    hipLaunchKernelGGL((attn_mfma_kernel<DT, D>), grid, dim3(256), 0, st, a);           \
+    hipLaunchKernelGGL((attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(256), 0, st, a);           \
     if (pl.max_chunks > 1)                                                              \
       hipLaunchKernelGGL((attn_merge_kernel<DT>), mgrid, dim3(256), 0, st, a);          \
     return check_launch(fn);                                                            \
