@@ -16,7 +16,10 @@ One step is one pass of the path over synthetic inputs resident in HBM:
 The reported ``value`` is the attention phase's throughput in TFLOP/s (useful causal FLOPs
 4 * D * Hq * sum(p + 1)); the scatter and RoPE phases are reported in GB/s of useful bytes
 (each moved row read once and written once). Every phase is timed with HIP events on the
-stream its kernels run on; ``ms_per_step`` is the sum of the three phase times.
+stream its kernels run on; ``ms_per_step`` is the sum of the three phase times. Each library
+kernel launch in the timed region is also bracketed by HIP events inside the library
+(``kernels``); ``roofline`` prices the MFMA attention kernel's average launch against the
+bf16 peak. ``phases.copy_ceiling`` is a plain 1 GiB device copy, the achievable HBM rate.
 The CPU baseline times the oracle (a restatement of the reference's CPU path) on a bounded
 sample of the same workload on the host's cores.
 
@@ -41,6 +44,18 @@ L, HKV, HQ, D, BS = 28, 4, 28, 128, 16
 CTX, N_RECOMPUTE, CHUNK = 16384, 2458, 256
 ROPE_TOKENS, ROPE_BASE = 8192, 1e6
 POOL_BLOCKS = 2048
+
+# Library kernels whose launches are timed with HIP events over the timed region.
+KERNELS = ("attn_mfma", "attn_merge", "move_rows", "rope_rows", "rope_index", "fill_i32")
+
+# HBM bytes per launch on this workload, from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
+# this script, scaled by what the same counters read for the 1 GiB copy of copy_ceiling()
+# (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); kernel changes call for a new measurement.
+MEASURED_TRAFFIC_BYTES = {
+    "attn_mfma": (2 * 72350 + 40892) * 1024,
+    "move_rows": (2 * 390420 + 779860) * 1024,
+    "rope_rows": (2 * 114899 + 229379) * 1024,
+}
 
 
 def log(msg: str) -> None:
@@ -95,6 +110,34 @@ def build_inputs(dev: torch.device):
     return inp
 
 
+def copy_ceiling(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> float:
+    """Achievable HBM bandwidth of a plain device copy (read + write), GB/s."""
+    a = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    gbps = 2.0 * nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del a, b
+    return gbps
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(inp, budget_s: float = 20.0) -> dict:
     """Oracle (reference CPU path restated) on a bounded sample, on the host's cores."""
     from oracle import ref_cpu as ref
@@ -117,6 +160,7 @@ def cpu_baseline(inp, budget_s: float = 20.0) -> dict:
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
+        "host": {"cpu_count": os.cpu_count(), "torch_threads": cores, "model": cpu_model()},
         "sample": f"partial attention, {n_sample} of {pos.shape[0]} recompute rows (random), "
                   f"28q/4kv x 128, 16384-token paged context, bf16 in / fp32 math; "
                   f"{dt:.2f} s",
@@ -155,6 +199,7 @@ def main() -> int:
               "Run with --gpus 1.", file=sys.stderr)
         return 2
 
+    from semblend_amd import _lib
     from semblend_amd import rope_correction as rc
     from semblend_amd import triton_kernels as tk
 
@@ -192,6 +237,7 @@ def main() -> int:
 
     log(f"timing {args.steps} steps")
     ev = {name: [] for name, _ in phases}
+    _lib.kernel_timing(True)
     t_wall0 = time.perf_counter()
     for i in range(args.steps):
         for name, fn in phases:
@@ -203,12 +249,24 @@ def main() -> int:
             ev[name].append((e0, e1))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall0
+    _lib.kernel_timing(False)
+    kernels = {}
+    for name in KERNELS:
+        total, n = _lib.kernel_time(name)
+        if n:
+            kernels[name] = {"launches": n, "avg_us": round(1e3 * total / n, 2)}
+    copy_gbps = copy_ceiling(dev)
+    log("kernels (avg us): " + ", ".join(f"{k} {v['avg_us']}" for k, v in kernels.items())
+        + f"; copy ceiling {copy_gbps:.0f} GB/s")
     ms = {name: [a.elapsed_time(b) for a, b in pairs] for name, pairs in ev.items()}
     med = {name: sorted(v)[len(v) // 2] for name, v in ms.items()}
     avg = {name: sum(v) / len(v) for name, v in ms.items()}
     ms_per_step = sum(avg.values())
 
     attn_tflops = attn_flops / (avg["attention"] * 1e-3) / 1e12
+    # Dominant kernel: the MFMA attention kernel, one launch per step.
+    mfma_us = kernels["attn_mfma"]["avg_us"]
+    mfma_tflops = attn_flops / (mfma_us * 1e-6) / 1e12
     scatter_gbps = scatter_bytes / (avg["scatter"] * 1e-3) / 1e9
     rope_gbps = rope_bytes / (avg["rope"] * 1e-3) / 1e9
     log(f"attention {avg['attention']:.3f} ms ({attn_tflops:.1f} TFLOP/s), "
@@ -241,11 +299,12 @@ def main() -> int:
         },
         "roofline": {
             "bound": "mfma",
-            "achieved": round(attn_tflops, 2),
+            "kernel": "attn_mfma_kernel",
+            "achieved": round(mfma_tflops, 2),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "frac": round(mfma_tflops / BF16_PEAK_TFLOPS, 4),
+            "traffic": MEASURED_TRAFFIC_BYTES["attn_mfma"],
         },
         "phases": {
             "attention": {"ms": round(avg["attention"], 4), "ms_median": round(med["attention"], 4),
@@ -253,11 +312,19 @@ def main() -> int:
                           "frac_of_peak": round(attn_tflops / BF16_PEAK_TFLOPS, 4)},
             "scatter": {"ms": round(avg["scatter"], 4), "ms_median": round(med["scatter"], 4),
                         "gbps": round(scatter_gbps, 1),
+                        "kernel_gbps": round(scatter_bytes / (kernels["move_rows"]["avg_us"] * 1e-6) / 1e9, 1),
+                        "traffic_bytes": MEASURED_TRAFFIC_BYTES["move_rows"],
                         "frac_of_peak": round(scatter_gbps / HBM_PEAK_GBS, 4)},
             "rope": {"ms": round(avg["rope"], 4), "ms_median": round(med["rope"], 4),
                      "gbps": round(rope_gbps, 1),
+                     "kernel_gbps": round(rope_bytes / (kernels["rope_rows"]["avg_us"] * 1e-6) / 1e9, 1),
+                     "traffic_bytes": MEASURED_TRAFFIC_BYTES["rope_rows"],
                      "frac_of_peak": round(rope_gbps / HBM_PEAK_GBS, 4)},
+            "copy_ceiling": {"gbps": round(copy_gbps, 1),
+                             "frac_of_peak": round(copy_gbps / HBM_PEAK_GBS, 4),
+                             "what": "1 GiB device-to-device copy (torch copy_), 10 repeats"},
         },
+        "kernels": kernels,
     }
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle on host cores)")

@@ -204,6 +204,22 @@ int sb_partial_attention_paged(void* out, const void* q, const void* kv_cache,
                                const int64_t* q_strides, const int64_t* o_strides,
                                const int64_t* kv_strides, int32_t dtype, void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Kernel timing (instrumentation for benchmarks; no reference counterpart)
+ * ---------------------------------------------------------------------------------------- */
+
+/* enable != 0 clears the timing log and starts attaching a pair of HIP timing events to every
+ * launch of the library's kernels (hipExtLaunchKernel start/stop events, stamped with the
+ * kernel's own start and end, so no extra work enters the stream); enable == 0 stops logging
+ * (the log stays readable). At most 65536 launches are logged. Kernel names:
+ * "move_rows", "rope_rows", "rope_index", "fill_i32", "attn_mfma", "attn_valu", "attn_merge",
+ * "mask_compact", "zero_rows". */
+int sb_kernel_timing_enable(int32_t enable);
+
+/* Sum of the logged durations (ms) and number of logged launches of one kernel. Waits for the
+ * logged events to complete. */
+int sb_kernel_timing_read(const char* kernel, double* total_ms, int64_t* launches);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,8 @@ SIGNATURES: dict[str, list] = {
                                      _f32, _i64p, _i64p, _i64p, _i64p, _i32, _vp],
     "sb_partial_attention_paged": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                    _i64, _i64, _i64, _f32, _i64p, _i64p, _i64p, _i32, _vp],
+    "sb_kernel_timing_enable": [_i32],
+    "sb_kernel_timing_read": [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), _i64p],
 }
 
 # Size queries (return int64_t, not a status code).
@@ -189,3 +191,41 @@ def as_index(t, device: torch.device) -> torch.Tensor:
     if t.dtype != torch.int32:
         t = t.to(torch.int32)
     return t.contiguous().reshape(-1)
+
+
+_ADDR_TABLES: dict[tuple, torch.Tensor] = {}
+_ADDR_TABLES_MAX = 64
+
+
+def address_table(tensors, device: torch.device) -> torch.Tensor:
+    """Device int64 array of the tensors' base addresses (the per-layer tables of the
+    multi-layer entry points).
+
+    Tables are cached by (device, addresses), so repeated calls over the same layer tensors
+    enqueue no host-to-device copy; a new table is copied from pinned memory without blocking
+    the host. Keying by the addresses themselves keeps a cached table correct even when the
+    tensors are freed and others reuse the memory.
+    """
+    key = (device, tuple(t.data_ptr() for t in tensors))
+    tab = _ADDR_TABLES.get(key)
+    if tab is None:
+        if len(_ADDR_TABLES) >= _ADDR_TABLES_MAX:
+            _ADDR_TABLES.pop(next(iter(_ADDR_TABLES)))
+        host = torch.tensor(key[1], dtype=torch.int64).pin_memory()
+        tab = host.to(device, non_blocking=True)
+        _ADDR_TABLES[key] = tab
+    return tab
+
+
+def kernel_timing(enable: bool) -> None:
+    """Start (clearing the log) or stop attaching HIP timing events to the library's kernel
+    launches (stamped by the runtime with each kernel's start and end)."""
+    call("sb_kernel_timing_enable", 1 if enable else 0)
+
+
+def kernel_time(kernel: str) -> tuple[float, int]:
+    """(total milliseconds, launches) logged for one kernel since timing was last enabled."""
+    total = ctypes.c_double(0.0)
+    n = ctypes.c_int64(0)
+    call("sb_kernel_timing_read", kernel.encode(), ctypes.byref(total), ctypes.byref(n))
+    return total.value, n.value

@@ -780,9 +780,9 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
     dim3 mgrid(static_cast<unsigned>(pl.n_tiles * a.num_kv_heads));
 #define SB_ATT_CASE(DT, D)                                                              \
   if (dtype == DT && a.head_dim == D) {                                                 \
-    hipLaunchKernelGGL((attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(256), 0, st, a);           \
+    SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(256), st, a); \
     if (pl.max_chunks > 1)                                                              \
-      hipLaunchKernelGGL((attn_merge_kernel<DT>), mgrid, dim3(256), 0, st, a);          \
+      SB_LAUNCH("attn_merge", (attn_merge_kernel<DT>), mgrid, dim3(256), st, a);        \
     return check_launch(fn);                                                            \
   }
     SB_ATT_CASE(SB_DTYPE_BF16, 128)
@@ -794,9 +794,9 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
   if (a.head_dim > kValuMaxDim) return fail(fn, "head_dim above 512 is not supported");
   if (rows_upper > 0x7fffffff) return fail(fn, "too many rows");
   dim3 grid(static_cast<unsigned>(rows_upper), static_cast<unsigned>(a.num_kv_heads * a.group));
-  if (dtype == SB_DTYPE_F32) hipLaunchKernelGGL(attn_valu_kernel<SB_DTYPE_F32>, grid, dim3(64), 0, st, a);
-  else if (dtype == SB_DTYPE_BF16) hipLaunchKernelGGL(attn_valu_kernel<SB_DTYPE_BF16>, grid, dim3(64), 0, st, a);
-  else hipLaunchKernelGGL(attn_valu_kernel<SB_DTYPE_F16>, grid, dim3(64), 0, st, a);
+  if (dtype == SB_DTYPE_F32) SB_LAUNCH("attn_valu", attn_valu_kernel<SB_DTYPE_F32>, grid, dim3(64), st, a);
+  else if (dtype == SB_DTYPE_BF16) SB_LAUNCH("attn_valu", attn_valu_kernel<SB_DTYPE_BF16>, grid, dim3(64), st, a);
+  else SB_LAUNCH("attn_valu", attn_valu_kernel<SB_DTYPE_F16>, grid, dim3(64), st, a);
   return check_launch(fn);
 }
 
@@ -860,13 +860,14 @@ extern "C" int sb_partial_prefill_attention(void* out, const void* q, const void
     const int64_t total = num_heads * seq_len * vpr;
     const dim3 grid(static_cast<unsigned>((total + 255) / 256));
     char* o = static_cast<char*>(out);
-    if (vb >= 16) hipLaunchKernelGGL(zero_rows_kernel<16>, grid, dim3(256), 0, st, o, compute_mask, num_heads, seq_len, os[0] * es, os[1] * es, vpr);
-    else if (vb == 8) hipLaunchKernelGGL(zero_rows_kernel<8>, grid, dim3(256), 0, st, o, compute_mask, num_heads, seq_len, os[0] * es, os[1] * es, vpr);
-    else if (vb == 4) hipLaunchKernelGGL(zero_rows_kernel<4>, grid, dim3(256), 0, st, o, compute_mask, num_heads, seq_len, os[0] * es, os[1] * es, vpr);
-    else hipLaunchKernelGGL(zero_rows_kernel<2>, grid, dim3(256), 0, st, o, compute_mask, num_heads, seq_len, os[0] * es, os[1] * es, vpr);
+    const int64_t sh = os[0] * es, ss = os[1] * es;
+    if (vb >= 16) SB_LAUNCH("zero_rows", zero_rows_kernel<16>, grid, dim3(256), st, o, compute_mask, num_heads, seq_len, sh, ss, vpr);
+    else if (vb == 8) SB_LAUNCH("zero_rows", zero_rows_kernel<8>, grid, dim3(256), st, o, compute_mask, num_heads, seq_len, sh, ss, vpr);
+    else if (vb == 4) SB_LAUNCH("zero_rows", zero_rows_kernel<4>, grid, dim3(256), st, o, compute_mask, num_heads, seq_len, sh, ss, vpr);
+    else SB_LAUNCH("zero_rows", zero_rows_kernel<2>, grid, dim3(256), st, o, compute_mask, num_heads, seq_len, sh, ss, vpr);
   }
-  hipLaunchKernelGGL(mask_compact_kernel, dim3(1), dim3(1024), 0, st, compute_mask, seq_len,
-                     pos, pos + seq_len);
+  SB_LAUNCH("mask_compact", mask_compact_kernel, dim3(1), dim3(1024), st, compute_mask, seq_len,
+            pos, pos + seq_len);
   int rc = check_launch(fn);
   if (rc) return rc;
 

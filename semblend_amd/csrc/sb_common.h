@@ -1,6 +1,7 @@
 // Shared device/host helpers for libsemblend_hip (gfx950, wave64).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string>
@@ -16,6 +17,30 @@ void set_error(const std::string& msg);
 void clear_error();
 int fail(const char* fn, const std::string& msg);            // SB_ERR_INVALID_ARGUMENT
 int check_launch(const char* fn);                            // hipGetLastError -> code
+
+// Timing events of one kernel launch while kernel timing is enabled
+// (sb_kernel_timing_enable): two pooled HIP events, logged under `name`, which the launch
+// passes to hipExtLaunchKernelGGL so that the runtime stamps them with the kernel's own start
+// and end. Both are null (no timing) when timing is off.
+class KernelTimer {
+ public:
+  explicit KernelTimer(const char* name);
+  hipEvent_t start() const { return start_; }
+  hipEvent_t stop() const { return stop_; }
+
+ private:
+  hipEvent_t start_ = nullptr;
+  hipEvent_t stop_ = nullptr;
+};
+
+// Launches KERNEL (parenthesise template-ids) with no dynamic LDS on STREAM, logged under NAME
+// when kernel timing is enabled.
+#define SB_LAUNCH(NAME, KERNEL, GRID, BLOCK, STREAM, ...)                                 \
+  do {                                                                                   \
+    ::sb::KernelTimer sb_kt_(NAME);                                                      \
+    hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, 0, STREAM, sb_kt_.start(), sb_kt_.stop(), \
+                          0, __VA_ARGS__);                                               \
+  } while (0)
 
 inline int64_t elem_size(int32_t dtype) {
   return dtype == SB_DTYPE_F32 ? 4 : (dtype == SB_DTYPE_F16 || dtype == SB_DTYPE_BF16) ? 2 : 0;

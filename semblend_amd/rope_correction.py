@@ -167,7 +167,7 @@ def _check_uniform(ts: list[torch.Tensor], name: str) -> None:
 
 
 def _layer_table(ts: list[torch.Tensor], dev: torch.device) -> torch.Tensor:
-    return torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64).to(dev)
+    return _lib.address_table(ts, dev)
 
 
 def _rope_k(out: torch.Tensor, k: torch.Tensor, dpos, tpos, head_dim, rope_base) -> None:

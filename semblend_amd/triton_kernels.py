@@ -160,8 +160,8 @@ def scatter_donor_kv_paged_layers(
     if ref.dtype != dref.dtype:
         raise TypeError("kv_caches and donor_kvs must share a dtype")
     nb_total, _, num_heads, block_size, head_dim = ref.shape
-    kv_tab = torch.tensor([t.data_ptr() for t in kv_caches], dtype=torch.int64).to(dev)
-    d_tab = torch.tensor([t.data_ptr() for t in donor_kvs], dtype=torch.int64).to(dev)
+    kv_tab = _lib.address_table(kv_caches, dev)
+    d_tab = _lib.address_table(donor_kvs, dev)
     bt = _lib.as_index(block_table, dev)
     dpos = _lib.as_index(donor_positions, dev)
     tpos = _lib.as_index(target_positions, dev)

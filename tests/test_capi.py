@@ -101,3 +101,11 @@ def test_workspace_size_queries(dtype, expect_split):
     assert (n > 0) == expect_split  # fp32 takes the unsplit VALU kernel
     dense = _lib.size_query("sb_partial_prefill_attention_workspace_size", 4, 1000, 128, dtype)
     assert dense >= 1001 * 4
+
+
+def test_kernel_timing_log_without_launches():
+    _lib.kernel_timing(True)
+    assert _lib.kernel_time("attn_mfma") == (0.0, 0)
+    _lib.kernel_timing(False)
+    rc = _lib.lib().sb_kernel_timing_read(None, None, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT
