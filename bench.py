@@ -52,7 +52,7 @@ KERNELS = ("attn_mfma", "attn_merge", "move_rows", "rope_rows", "rope_index", "f
 # this script, scaled by what the same counters read for the 1 GiB copy of copy_ceiling()
 # (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); kernel changes call for a new measurement.
 MEASURED_TRAFFIC_BYTES = {
-    "attn_mfma": (2 * 72350 + 40892) * 1024,
+    "attn_mfma": (2 * 66209 + 43788) * 1024,
     "move_rows": (2 * 390420 + 779860) * 1024,
     "rope_rows": (2 * 114899 + 229379) * 1024,
 }

@@ -7,27 +7,24 @@
 //
 // MFMA path (bf16 / fp16, head_dim 64 or 128). The query rows of one KV head are flattened
 // as (row, q-head-in-group), so the whole GQA group shares every K/V tile. A workgroup owns
-// 128 flattened rows (4 waves x 32) and one chunk of the key range, walked in tiles of 64
-// keys staged in LDS:
+// 32 flattened rows per wave and one chunk of the key range, walked in tiles of 64 keys:
 //   * S^T = K Q^T with v_mfma_f32_32x32x16: K tile rows are the A operand (one ds_read_b128
-//     per lane per 16-wide k-step), Q stays in registers as the B operand. In the S^T
-//     accumulator each lane owns ONE query row and 16 keys, so row max / row sum need only
-//     in-lane work plus one exchange with lane ^ 32.
-//   * O^T += V^T P^T with the same MFMA: P^T comes straight from the S^T accumulators
-//     (after exp2 and conversion) as the B operand; the key order inside each 16-key step is
-//     permuted consistently in both operands, so no cross-lane shuffles are needed. V is
-//     stored transposed in LDS (Vt[d][key]) with the middle key quads of every 16-key group
-//     swapped, so the 8 keys a lane needs are contiguous: one ds_read_b128 per fragment
-//     (two 8-byte reads at the natural column order run 4x slower on gfx950).
-//   * K/V tiles are double-buffered: the global loads of tile i+1 are issued into registers
-//     before tile i is computed and written to the other LDS buffer afterwards, so one
-//     barrier per tile separates the stages. Row addresses come from per-tile key-offset
-//     tables in LDS (built from the chunk's block-table slice, also staged in LDS), so the
-//     loads are branch-free and need no index arithmetic.
-//   * Online softmax in the log2 domain with a lazily updated reference max: the running
-//     reference only moves (and O is only rescaled) when a row's max grows by more than
-//     2^8, which keeps every p <= 256 and removes almost all rescaling work. O / l is
-//     unchanged by the choice of reference.
+//     per lane per 16-wide k-step), Q stays in registers as the B operand, pre-multiplied by
+//     scale * log2(e). The accumulator starts at -m_ref, so the MFMA yields s - m_ref in the
+//     log2 domain. In the S^T accumulator each lane owns ONE query row and 16 keys.
+//   * O^T += V^T P^T with the same MFMA: P^T comes straight from the S^T accumulators (after
+//     exp2 and conversion) as the B operand. V stays in [key][d] layout in LDS; each A-operand
+//     fragment is two ds_read_b64_tr_b16 transpose loads, which hand every lane 4 consecutive
+//     keys of its d column in the key order of the P^T accumulator elements.
+//   * Tiles move global -> LDS with global_load_lds_dwordx4 (no register staging). The 16-byte
+//     chunks of every row are XOR-swizzled so that the fragment reads are conflict-free.
+//   * Softmax reference per row: seeded with the row's first live tile max; afterwards it only
+//     moves (rescaling O and l) when a tile's sum of P exceeds kPMax, which the v_dot2 sum of
+//     the rounded P values shows at the cost of one compare. O / l is unchanged by the choice
+//     of reference.
+//   * Cross-tile pipeline: S(i+1) is computed on the matrix cores while P(i) is formed on the
+//     vector ALUs, then O += V(i)^T P(i). K runs two tiles ahead and V one, in two LDS stages
+//     each; one barrier per tile.
 // Load balance: the key range of each row tile is split into chunks of `ksplit` keys. Work
 // items are ordered (chunk ascending, tile descending), so with ascending positions the
 // largest items start first. Tiles that need more than one chunk write unnormalised fp32
@@ -37,6 +34,8 @@
 // step, one key per lane for the scores and the PV sum over the chunk per output dimension.
 
 #include "sb_common.h"
+
+#include <type_traits>
 
 namespace sb {
 
@@ -51,9 +50,20 @@ constexpr int kWaveRows = 32;   // flattened query rows per MFMA row group
 #endif
 // Row groups per wave: each K/V fragment read from LDS feeds this many MFMAs.
 constexpr int kRowGroups = SB_ATTN_ROW_GROUPS;
-constexpr int kTileKeys = 64;   // keys per LDS tile
+#ifndef SB_ATTN_TILE_KEYS
+#define SB_ATTN_TILE_KEYS 64
+#endif
+#ifndef SB_ATTN_OCCUPANCY
+#define SB_ATTN_OCCUPANCY 2
+#endif
+#ifndef SB_ATTN_WAVES
+#define SB_ATTN_WAVES 4
+#endif
+constexpr int kTileKeys = SB_ATTN_TILE_KEYS;  // keys per LDS tile (32 or 64)
+constexpr int kWaves = SB_ATTN_WAVES;         // waves per workgroup (each owns 32 rows)
+constexpr int kThreads = 64 * kWaves;
+constexpr int kHalves = kTileKeys / 32;       // 32-key MFMA blocks per tile
 constexpr int kBtLds = 1024;    // block-table entries staged per chunk
-constexpr float kLazyMax = 8.f; // log2 growth of a row max that forces a rescale
 
 struct AttnArgs {
   const char* q;        // query rows
@@ -130,6 +140,7 @@ __device__ __forceinline__ int wave_min_i(int v) {
 template <int DT> struct Mma;
 template <> struct Mma<SB_DTYPE_BF16> {
   using vec8 = bf16x8_t;
+  using elem = __bf16;
   __device__ __forceinline__ static f32x16_t mma(vec8 a, vec8 b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
@@ -140,9 +151,24 @@ template <> struct Mma<SB_DTYPE_BF16> {
     return r;
   }
   __device__ __forceinline__ static uint16_t cvt1(float f) { return f32_to_bf16(f); }
+  // acc + sum of the 8 (rounded) elements of v, two per v_dot2.
+  __device__ __forceinline__ static float sum8(vec8 v, float acc) {
+    typedef __bf16 x2 __attribute__((ext_vector_type(2)));
+    const x2 one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const x2 pr = {v[2 * e], v[2 * e + 1]};
+      acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
+    }
+    return acc;
+  }
+  // Largest tile sum of P accepted without moving the reference max (bf16 keeps fp32's
+  // exponent range, so only fp32 overflow of O bounds it).
+  static constexpr float kPMax = 0x1p64f;
 };
 template <> struct Mma<SB_DTYPE_F16> {
   using vec8 = f16x8_t;
+  using elem = _Float16;
   __device__ __forceinline__ static f32x16_t mma(vec8 a, vec8 b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
@@ -153,15 +179,41 @@ template <> struct Mma<SB_DTYPE_F16> {
     return r;
   }
   __device__ __forceinline__ static uint16_t cvt1(float f) { return f32_to_f16(f); }
+  __device__ __forceinline__ static float sum8(vec8 v, float acc) {
+    typedef _Float16 x2 __attribute__((ext_vector_type(2)));
+    const x2 one = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const x2 pr = {v[2 * e], v[2 * e + 1]};
+      acc = __builtin_amdgcn_fdot2(pr, one, acc, false);
+    }
+    return acc;
+  }
+  // fp16 P saturates at 65504: keep every p below 2^8.
+  static constexpr float kPMax = 256.f;
 };
 
-// Column of key `k` (0..63) in the transposed V tile. Within every 16-key group the middle
-// two quads are swapped (bits 2 and 3 of k exchanged), so that the keys one lane feeds to
-// a 16-wide PV step -- {4h..4h+3, 8+4h..8+4h+3} for lane half h -- are contiguous.
-// Adjacent key pairs stay adjacent, so the transposing store writes whole dwords.
-__device__ __forceinline__ int vt_column(int k) {
-  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+// 16-byte chunk position of chunk c of row r in the swizzled K and V tiles (CH chunks per
+// row). K fragments are read as 16 bytes per lane from 32 consecutive rows at one chunk:
+// rows r..r+15 land on distinct chunk positions. V is read with transpose loads that touch
+// 4 consecutive rows x 32-64 bytes: rows r..r+3 land on disjoint 64-byte bank ranges.
+template <int CH>
+__device__ __forceinline__ int kswz(int r, int c) {
+  return c ^ (r & (CH - 1));
 }
+template <int CH>
+__device__ __forceinline__ int vswz(int r, int c) {
+  return CH >= 16 ? c ^ (4 * (r & 3)) : c ^ (4 * ((r >> 1) & 1));
+}
+
+#define SB_GLOBAL __attribute__((address_space(1)))
+#define SB_LDS __attribute__((address_space(3)))
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Waits until this wave's outstanding vector-memory operations (including direct-to-LDS
+// loads) are complete: s_waitcnt vmcnt(0), other counters untouched.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Work-item decode shared by the attention and merge kernels.
 struct Item {
@@ -183,23 +235,23 @@ __device__ __forceinline__ Item decode_item(const AttnArgs& a, int64_t n_tiles_l
 }
 
 template <int DT, int D, int RG>
-__global__ __launch_bounds__(256, RG == 1 ? 2 : 1) void attn_mfma_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kThreads, RG == 1 ? SB_ATTN_OCCUPANCY * 4 / kWaves : 1) void
+attn_mfma_kernel(AttnArgs a) {
   using M = Mma<DT>;
   using vec8 = typename M::vec8;
-  constexpr int TR = kWaveRows * RG * 4;  // flattened rows per workgroup tile
-  constexpr int KSTR = D + 8;             // K tile row stride (elements)
-  constexpr int VSTR = kTileKeys + 8;     // transposed V row stride (elements, 144 bytes)
+  constexpr int TR = kWaveRows * RG * kWaves;  // flattened rows per workgroup tile
   constexpr int NKS = D / 16;             // QK^T k-steps
   constexpr int NDT = D / 32;             // PV output d-tiles
   constexpr int CH = D / 8;               // 16-byte chunks per row
-  constexpr int KLD = kTileKeys * CH / 256;  // K vectors loaded per thread per tile
-  constexpr int VLD = CH / 8;                // V key-pair passes per thread per tile
-  __shared__ __align__(16) uint16_t Ks[2][kTileKeys * KSTR];
-  __shared__ __align__(16) uint16_t Vt[2][D * VSTR];
+  constexpr int NLD = kTileKeys * CH / kThreads;  // direct-to-LDS loads per thread per tile
+  // K and V tiles: kTileKeys rows of D elements, unpadded, 16-byte chunks XOR-swizzled by
+  // row (kswz / vswz) so that the fragment reads below are free of bank conflicts.
+  __shared__ __align__(16) uint16_t Ks[2][kTileKeys * D];
+  __shared__ __align__(16) uint16_t Vs[2][kTileKeys * D];
   __shared__ int bt_s[kBtLds];
-  __shared__ uint64_t kofs[2][kTileKeys];  // per-key byte offsets of K rows (double-buffered)
-  __shared__ uint64_t vofs[2][kTileKeys];  // ... and of V rows
-  __shared__ int red_max[4];
+  __shared__ uint64_t kofs[3][kTileKeys];  // per-key byte offsets of K rows (3-slot ring)
+  __shared__ uint64_t vofs[3][kTileKeys];  // ... and of V rows
+  __shared__ int red_max[kWaves];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -237,7 +289,10 @@ __global__ __launch_bounds__(256, RG == 1 ? 2 : 1) void attn_mfma_kernel(AttnArg
   const int pmax_w = wave_max_i(pmax_l);
   if (lane == 0) red_max[wave] = pmax_w;
   __syncthreads();
-  const int kend = max(max(red_max[0], red_max[1]), max(red_max[2], red_max[3])) + 1;
+  int kend = red_max[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) kend = max(kend, red_max[w]);
+  kend += 1;
   const int k0 = item.chunk * a.ksplit;
   if (k0 >= kend) return;  // uniform: kend comes from shared memory
   const int k1 = min(k0 + a.ksplit, kend);
@@ -252,56 +307,65 @@ __global__ __launch_bounds__(256, RG == 1 ? 2 : 1) void attn_mfma_kernel(AttnArg
   const int pmin_w = wave_min_i(pmin_l);
   const int pmax_c = min(pmax_w, k1 - 1);
 
-  // Q fragments (B operand). For a negative scale Q is negated, so that the softmax can
-  // always take its max over the raw scores: scale * q.k = |scale| * (-q).k.
-  const uint32_t qflip = a.scale_log2 < 0.f ? 0x80008000u : 0u;
-  const float c = fabsf(a.scale_log2);
+  // Q fragments (B operand), pre-multiplied by scale * log2(e) and rounded to the input
+  // type, so that the MFMA yields scores in the log2 domain directly.
   vec8 qf[RG][NKS];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
     const char* qp = a.q + qrow[g] * a.q_s_row + qh[g] * a.q_s_head;
 #pragma unroll
     for (int s = 0; s < NKS; ++s) {
-      uint4 w = make_uint4(0, 0, 0, 0);
-      if (p[g] >= 0) w = *reinterpret_cast<const uint4*>(qp + (16 * s + 8 * lg) * 2);
-      w.x ^= qflip; w.y ^= qflip; w.z ^= qflip; w.w ^= qflip;
-      qf[g][s] = __builtin_bit_cast(vec8, w);
+      vec8 v = {};
+      if (p[g] >= 0) v = *reinterpret_cast<const vec8*>(qp + (16 * s + 8 * lg) * 2);
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = static_cast<float>(v[e]) * a.scale_log2;
+      qf[g][s] = M::cvt8(f);
     }
   }
 
-  // Stage the chunk's block-table slice, then the key-offset tables of the first two tiles.
+  // Stage the chunk's block-table slice, then the key-offset tables of the first three tiles.
   int lb0 = 0;
   if (a.paged) {
     lb0 = static_cast<int>(k0 / a.block_size);
     const int nb = static_cast<int>((k1 - 1) / a.block_size) - lb0 + 1;
-    for (int i = tid; i < nb; i += 256) bt_s[i] = clamp_block(a, a.block_table[lb0 + i]);
+    for (int i = tid; i < nb; i += kThreads) bt_s[i] = clamp_block(a, a.block_table[lb0 + i]);
     __syncthreads();
   }
   const char* kbase = a.k + kvh * a.k_s_head;
   const char* vbase = a.v + kvh * a.v_s_head;
   // Byte offsets of key `key` (clamped into [k0, k1)) relative to kbase / vbase.
-  auto fill_offsets = [&](int buf, int t0, int i) {
+  auto fill_offsets = [&](int slot, int t0, int i) {
     const int key = min(t0 + i, k1 - 1);
     if (a.paged) {
-      const int lb = key / static_cast<int>(a.block_size);
+      const int lb = a.bs_log2 >= 0 ? key >> a.bs_log2 : key / static_cast<int>(a.block_size);
       const uint64_t off = static_cast<uint64_t>(bt_s[lb - lb0]) * a.s_block +
                            static_cast<uint64_t>(key - lb * a.block_size) * a.s_pos;
-      kofs[buf][i] = off;
-      vofs[buf][i] = off;
+      kofs[slot][i] = off;
+      vofs[slot][i] = off;
     } else {
-      kofs[buf][i] = static_cast<uint64_t>(key) * a.k_s_seq;
-      vofs[buf][i] = static_cast<uint64_t>(key) * a.v_s_seq;
+      kofs[slot][i] = static_cast<uint64_t>(key) * a.k_s_seq;
+      vofs[slot][i] = static_cast<uint64_t>(key) * a.v_s_seq;
     }
   };
-  if (tid < kTileKeys) fill_offsets(0, k0, tid);
-  else if (tid < 2 * kTileKeys) fill_offsets(1, k0 + kTileKeys, tid - kTileKeys);
+  if (tid < 3 * kTileKeys) fill_offsets(tid / kTileKeys, k0 + (tid / kTileKeys) * kTileKeys,
+                                        tid % kTileKeys);
   __syncthreads();
 
+  // Softmax state per row: O and l are relative to a reference max m_ref (log2 domain).
+  // negm holds -m_ref in every accumulator slot and seeds the QK^T accumulation, so the MFMA
+  // output is already s - m_ref. A row is "seeded" once m_ref is its first live tile's max;
+  // rows with no key in this chunk start seeded (their scores are all masked).
   float m_ref[RG], l_run[RG];
+  bool seeded[RG];
+  f32x16_t negm[RG];
   f32x16_t o[RG][NDT];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
-    m_ref[g] = -INFINITY;  // reference max (log2 domain) O and l are relative to
+    m_ref[g] = 0.f;
+    seeded[g] = plim[g] < k0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) negm[g][i] = 0.f;
     l_run[g] = 0.f;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
@@ -309,167 +373,223 @@ __global__ __launch_bounds__(256, RG == 1 ? 2 : 1) void attn_mfma_kernel(AttnArg
       for (int i = 0; i < 16; ++i) o[g][t][i] = 0.f;
   }
 
-  // Software pipeline over tiles of kTileKeys keys. Iteration t0 issues the global loads of
-  // tile t0 + kTileKeys into registers, computes tile t0 from LDS buffer `buf`, then writes
-  // the registers to the other buffer; one barrier per iteration. The first iteration
-  // (t0 = k0 - kTileKeys) only stages tile k0. Loads are unconditional: every offset in the
-  // tables is a valid row.
-  int buf = 1;
-  for (int t0 = k0 - kTileKeys; t0 < k1; t0 += kTileKeys) {
-    const bool more = t0 + kTileKeys < k1;
-    // Native vector types (not HIP's uint4 struct) keep the staging values in registers.
-    u32x4_t kreg[KLD];
-    u32x4_t vreg[VLD][2];
-    if (more) {
+  // Tiles move from global memory straight into LDS (global_load_lds_dwordx4: each wave
+  // instruction fills 1 KB of consecutive 16-byte slots; every lane fetches the chunk that
+  // the swizzled layout puts in its slot). Loads are unconditional: every offset is a valid
+  // row.
+  auto load_rows = [&](const char* base, const uint64_t* ofs, uint16_t* dst, bool is_k) {
+    // All row offsets first (back-to-back LDS reads, one wait), then the loads.
+    uint64_t ro[NLD];
 #pragma unroll
-      for (int i = 0; i < KLD; ++i) {
-        const int key = i * (256 / CH) + tid / CH;
-        kreg[i] =
-            *reinterpret_cast<const u32x4_t*>(kbase + kofs[buf ^ 1][key] + (tid % CH) * 16);
-      }
+    for (int q = 0; q < NLD; ++q) ro[q] = ofs[(q * kThreads + tid) / CH];
 #pragma unroll
-      for (int ps = 0; ps < VLD; ++ps) {
-        const int m = tid & 31;
-        const int ch = (tid >> 5) + 8 * ps;
-        vreg[ps][0] = *reinterpret_cast<const u32x4_t*>(vbase + vofs[buf ^ 1][2 * m] + ch * 16);
-        vreg[ps][1] =
-            *reinterpret_cast<const u32x4_t*>(vbase + vofs[buf ^ 1][2 * m + 1] + ch * 16);
-      }
+    for (int q = 0; q < NLD; ++q) {
+      const int sl = q * kThreads + tid;     // 16-byte slot within the tile
+      const int row = sl / CH;
+      const int pos = sl % CH;
+      const int chunk = is_k ? kswz<CH>(row, pos) : vswz<CH>(row, pos);
+      __builtin_amdgcn_global_load_lds((const SB_GLOBAL void*)(base + ro[q] + 16 * chunk),
+                                       (SB_LDS void*)(dst + (q * kThreads + wave * 64) * 8), 16, 0,
+                                       0);
     }
-    if (t0 >= k0 && t0 + 2 * kTileKeys < k1 && tid < kTileKeys)
-      fill_offsets(buf, t0 + 2 * kTileKeys, tid);
+  };
+  auto load_k = [&](int slot, int stage) { load_rows(kbase, kofs[slot], Ks[stage], true); };
+  auto load_v = [&](int slot, int stage) { load_rows(vbase, vofs[slot], Vs[stage], false); };
 
-    if (t0 >= k0 && t0 <= pmax_c) {
-      // ---- S^T = K Q^T for both 32-key halves. (half, k-step) pairs alternate halves, so
-      // two independent accumulation chains interleave; K fragments stream through a
-      // 4-deep ring so every ds_read is issued four MFMAs before it is consumed. ----
-      constexpr int NQ = 2 * NKS;
-      f32x16_t s[RG][2];
+  // K fragment of (half n % kHalves, k-step n / kHalves): key row 32 * half + lq, 16-byte
+  // chunk 2 * kstep + lg.
+  auto kfrag = [&](int stage, int n) -> vec8 {
+    const int r = 32 * (n % kHalves) + lq;
+    const int c = 2 * (n / kHalves) + lg;
+    return *reinterpret_cast<const vec8*>(&Ks[stage][r * D + 8 * kswz<CH>(r, c)]);
+  };
+  // V^T fragment of (d-tile t, step st, half j) for the A operand: lane (lq, lg) needs
+  // d = 32t + lq at keys 32j + 16st + {4lg..4lg+3, 8+4lg..8+4lg+3} (the key order of the
+  // P^T accumulator elements). Two ds_read_b64_tr_b16: in each group of 16 lanes, lane i
+  // reads 4 consecutive d of key row kb + i/4, and the transpose hands lane i the 4 keys
+  // kb..kb+3 of column d0 + i.
+  const int grp = lane >> 4, gi = lane & 15;
+  auto vfrag = [&](int stage, int n) -> vec8 {
+    const int t = n % NDT, st = (n / NDT) & 1, j = n / (2 * NDT);
+    const int d = 32 * t + 16 * (grp & 1) + 4 * (gi & 3);
+    u32x2_t h[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int row = 32 * j + 16 * st + 4 * lg + 8 * e + (gi >> 2);
+      const int idx = row * D + 8 * vswz<CH>(row, d >> 3) + (d & 7);
+      h[e] = __builtin_bit_cast(
+          u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((SB_LDS s16x4_t*)&Vs[stage][idx]));
+    }
+    const u32x4_t w = {h[0].x, h[0].y, h[1].x, h[1].y};
+    return __builtin_bit_cast(vec8, w);
+  };
+  using Scores = f32x16_t[RG][kHalves];
+  // S^T - m_ref = K Q^T - m_ref for one tile. (half, k-step) pairs alternate halves, so two
+  // independent accumulation chains interleave; K fragments stream through a 4-deep ring.
+  auto qk = [&](int stage, Scores& sc) {
+    constexpr int NQ = kHalves * NKS;
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+#pragma unroll
+      for (int j = 0; j < kHalves; ++j) sc[g][j] = negm[g];
+    vec8 ring[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) ring[n] = kfrag(stage, n);
+#pragma unroll
+    for (int n = 0; n < NQ; ++n) {
+      const vec8 kf = ring[n & 3];
+      if (n + 4 < NQ) ring[n & 3] = kfrag(stage, n + 4);
+#pragma unroll
+      for (int g = 0; g < RG; ++g)
+        sc[g][n % kHalves] = M::mma(kf, qf[g][n / kHalves], sc[g][n % kHalves]);
+    }
+  };
+  // Causal / chunk-end mask, only for tiles that cross some row's last key.
+  auto mask = [&](int t0, Scores& sc) {
+    if (t0 + kTileKeys - 1 > pmin_w) {
 #pragma unroll
       for (int g = 0; g < RG; ++g)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < kHalves; ++j) {
+          const int lim = plim[g] - (t0 + 32 * j + 4 * lg);  // key offset limit of this lane
 #pragma unroll
-          for (int i = 0; i < 16; ++i) s[g][j][i] = 0.f;
-      vec8 ring[4];
-#pragma unroll
-      for (int n = 0; n < 4; ++n)
-        ring[n] = *reinterpret_cast<const vec8*>(
-            &Ks[buf][(32 * (n & 1) + lq) * KSTR + 16 * (n >> 1) + 8 * lg]);
-#pragma unroll
-      for (int n = 0; n < NQ; ++n) {
-        const vec8 kf = ring[n & 3];
-        if (n + 4 < NQ) {
-          const int m = n + 4;
-          ring[n & 3] = *reinterpret_cast<const vec8*>(
-              &Ks[buf][(32 * (m & 1) + lq) * KSTR + 16 * (m >> 1) + 8 * lg]);
+          for (int i = 0; i < 16; ++i)
+            if (8 * (i >> 2) + (i & 3) > lim) sc[g][j][i] = -INFINITY;
         }
+    }
+  };
+  // P = exp2(s - shift), rounded to the input type; the tile sum from the rounded values.
+  vec8 pb[RG][kHalves][2];
+  float tsum[RG];
+  auto exp_tile = [&](int g, const Scores& sc, float shift) {
+    float acc[kHalves][2];  // independent partial sums (v_dot2 accumulates in place)
 #pragma unroll
-        for (int g = 0; g < RG; ++g) s[g][n & 1] = M::mma(kf, qf[g][n >> 1], s[g][n & 1]);
+    for (int j = 0; j < kHalves; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float pf[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pf[e] = __builtin_amdgcn_exp2f(sc[g][j][8 * h + e] - shift);
+        pb[g][j][h] = M::cvt8(pf);
+        acc[j][h] = M::sum8(pb[g][j][h], 0.f);
       }
-      // ---- causal / chunk-end mask, only on tiles that cross some row's last key ----
-      if (t0 + kTileKeys - 1 > pmin_w) {
+    float t = 0.f;
 #pragma unroll
-        for (int g = 0; g < RG; ++g)
+    for (int j = 0; j < kHalves; ++j) t += acc[j][0] + acc[j][1];
+    tsum[g] = t;
+  };
+
+  // Software pipeline over tiles of kTileKeys keys. Iteration `it` computes S(it+1) = QK^T
+  // of the next tile while it turns S(it) into P(it) (MFMA and VALU work interleave in one
+  // block), then O += V(it)^T P(it). K has two LDS stages and runs two tiles ahead, V two
+  // stages and one tile ahead: at the top of iteration `it` the loads of K(it+2) and V(it+1)
+  // are issued into the stages that QK(it) and PV(it-1) released; each wave waits for its
+  // own loads before the iteration's single barrier. Key offsets come from a three-slot
+  // table ring (slot = tile mod 3) filled three tiles ahead.
+  const int ntiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
+  Scores s_cur, s_nxt;
+  load_k(0, 0);
+  if (ntiles > 1) load_k(1, 1);
+  load_v(0, 0);
+  wait_vmem();
+  __syncthreads();
+  qk(0, s_cur);
+  mask(k0, s_cur);
+  __syncthreads();  // K stage 0 is refilled at the top of the first iteration
+
+  auto iteration = [&](int it, auto has_next) {
+    constexpr bool NEXT = decltype(has_next)::value;
+    const int t0 = k0 + it * kTileKeys;
+    if (it + 2 < ntiles) load_k((it + 2) % 3, it & 1);
+    if (it + 1 < ntiles) load_v((it + 1) % 3, (it + 1) & 1);
+    // Offsets of tile it+3: kTileKeys / kWaves entries from each wave.
+    if (it + 3 < ntiles && lane < kTileKeys / kWaves)
+      fill_offsets(it % 3, t0 + 3 * kTileKeys, wave * (kTileKeys / kWaves) + lane);
+    const bool live = t0 <= pmax_c;
+    // ---- S(it+1) on the matrix cores while P(it) is formed on the vector ALUs ----
+    if (NEXT) qk((it + 1) & 1, s_nxt);
+    bool bad_any = false;
+    bool bad[RG];
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const int lim = plim[g] - (t0 + 32 * j + 4 * lg);  // key offset limit of this lane
+    for (int g = 0; g < RG; ++g) {
+      exp_tile(g, s_cur, 0.f);
+      const float pair = tsum[g] + __shfl_xor(tsum[g], 32, 64);
+      bad[g] = !seeded[g] || !(pair <= M::kPMax);
+      bad_any |= bad[g];
+    }
+    if (NEXT) {
+      // Interleave: each QK^T MFMA is followed by one LDS fragment read and a share of the
+      // softmax VALU work (exp, conversion, sums), so the vector ALUs run under the MFMAs.
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-              if (8 * (i >> 2) + (i & 3) > lim) s[g][j][i] = -INFINITY;
-          }
+      for (int n = 0; n < kHalves * NKS; ++n) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
       }
-      // ---- tile row max; the reference moves (and O is rescaled) only when a row's max
-      // grows by more than 2^kLazyMax, which is rare after the first tiles ----
-      float mx[RG];
-      bool bump_any = false;
+    }
+    if (NEXT) mask(t0 + kTileKeys, s_nxt);
+    // ---- rare: seed the reference with the first live tile's max, or move it up when a
+    // tile would push P past kPMax; O and l are rescaled by 2^(m_old - m_new) and the
+    // already computed S(it+1) is shifted to the new reference ----
+    if (__any(bad_any)) {
 #pragma unroll
       for (int g = 0; g < RG; ++g) {
-        float v = fmaxf(s[g][0][0], s[g][1][0]);
+        float v = s_cur[g][0][0];
 #pragma unroll
-        for (int i = 1; i < 16; ++i) v = fmaxf(v, fmaxf(s[g][0][i], s[g][1][i]));
-        mx[g] = fmaxf(v, __shfl_xor(v, 32, 64)) * c;
-        bump_any |= mx[g] > m_ref[g] + kLazyMax;
-      }
-      if (__any(bump_any)) {
+        for (int j = 0; j < kHalves; ++j)
 #pragma unroll
-        for (int g = 0; g < RG; ++g) {
-          const bool bump = mx[g] > m_ref[g] + kLazyMax;
-          const float m_new = bump ? mx[g] : m_ref[g];
-          // 1 when this row keeps its reference, 0 when it had none (O and l are still 0).
-          const float alpha = bump ? __builtin_amdgcn_exp2f(m_ref[g] - m_new) : 1.f;
+          for (int i = 0; i < 16; ++i) v = fmaxf(v, s_cur[g][j][i]);
+        const float mx = fmaxf(v, __shfl_xor(v, 32, 64));  // row max of s - m_ref
+        if (bad[g] && mx != -INFINITY) {
+          const float alpha = seeded[g] ? __builtin_amdgcn_exp2f(-mx) : 0.f;
           l_run[g] *= alpha;
 #pragma unroll
           for (int t = 0; t < NDT; ++t)
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[g][t][i] *= alpha;
-          m_ref[g] = m_new;
-        }
-      }
-      // ---- P = exp2(s * c - m) and O^T += V^T P^T. V fragments (two 8-byte reads each)
-      // stream through a 4-deep ring over the (half, step, d-tile) sequence. ----
-      vec8 pb[RG][2][2];
+          m_ref[g] += mx;
 #pragma unroll
-      for (int g = 0; g < RG; ++g) {
-        const float nm = m_ref[g] == -INFINITY ? 0.f : -m_ref[g];
-        float lsum = 0.f;
+          for (int i = 0; i < 16; ++i) negm[g][i] = -m_ref[g];
+          seeded[g] = true;
+          exp_tile(g, s_cur, mx);
+          if (NEXT) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          float pf[16];
+            for (int j = 0; j < kHalves; ++j)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            pf[i] = __builtin_amdgcn_exp2f(fmaf(s[g][j][i], c, nm));
-            lsum += pf[i];
+              for (int i = 0; i < 16; ++i) s_nxt[g][j][i] -= mx;
           }
-          pb[g][j][0] = M::cvt8(pf);
-          pb[g][j][1] = M::cvt8(pf + 8);
         }
-        l_run[g] += lsum;
       }
-      constexpr int NV = 4 * NDT;  // (half, step, d-tile) triples
-      vec8 vring[4];
-      // With the column permutation of vt_column, the 8 keys a lane needs for one step are
-      // 16 contiguous bytes: a single ds_read_b128.
-      auto vfrag = [&](int n) -> vec8 {
-        const int t = n % NDT, st = (n / NDT) & 1, j = n / (2 * NDT);
-        return *reinterpret_cast<const vec8*>(
-            &Vt[buf][(32 * t + lq) * VSTR + 32 * j + 16 * st + 8 * lg]);
-      };
+    }
 #pragma unroll
-      for (int n = 0; n < 4; ++n) vring[n] = vfrag(n);
+    for (int g = 0; g < RG; ++g) l_run[g] += tsum[g];
+    // ---- O^T += V^T P^T; V fragments stream through a 4-deep ring ----
+    if (live) {
+      constexpr int NV = 2 * kHalves * NDT;  // (half, step, d-tile) triples
+      const int vb = it & 1;
+      vec8 vring[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) vring[n] = vfrag(vb, n);
 #pragma unroll
       for (int n = 0; n < NV; ++n) {
         const vec8 va = vring[n & 3];
-        if (n + 4 < NV) vring[n & 3] = vfrag(n + 4);
+        if (n + 4 < NV) vring[n & 3] = vfrag(vb, n + 4);
         const int t = n % NDT, st = (n / NDT) & 1, j = n / (2 * NDT);
 #pragma unroll
         for (int g = 0; g < RG; ++g) o[g][t] = M::mma(va, pb[g][j][st], o[g][t]);
       }
     }
-    if (more) {
+    if (NEXT) {
 #pragma unroll
-      for (int i = 0; i < KLD; ++i) {
-        const int key = i * (256 / CH) + tid / CH;
-        *reinterpret_cast<u32x4_t*>(&Ks[buf ^ 1][key * KSTR + (tid % CH) * 8]) = kreg[i];
-      }
+      for (int g = 0; g < RG; ++g)
 #pragma unroll
-      for (int ps = 0; ps < VLD; ++ps) {
-        const int m = tid & 31;
-        const int ch = (tid >> 5) + 8 * ps;
-        const int col = vt_column(2 * m);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          // (key 2m, key 2m+1) pairs of elements 2w and 2w+1 of the 8-element chunk
-          const uint32_t lo = __builtin_amdgcn_perm(vreg[ps][1][w], vreg[ps][0][w], 0x05040100u);
-          const uint32_t hi = __builtin_amdgcn_perm(vreg[ps][1][w], vreg[ps][0][w], 0x07060302u);
-          *reinterpret_cast<uint32_t*>(&Vt[buf ^ 1][(ch * 8 + 2 * w) * VSTR + col]) = lo;
-          *reinterpret_cast<uint32_t*>(&Vt[buf ^ 1][(ch * 8 + 2 * w + 1) * VSTR + col]) = hi;
-        }
-      }
+        for (int j = 0; j < kHalves; ++j) s_cur[g][j] = s_nxt[g][j];
     }
+    wait_vmem();
     __syncthreads();
-    buf ^= 1;
-  }
+  };
+  for (int it = 0; it + 1 < ntiles; ++it) iteration(it, std::true_type{});
+  iteration(ntiles - 1, std::false_type{});
 
   // ---- finish: lane holds d = 32t + 8*(i/4) + 4*lg + (i%4) of each of its rows ----
 #pragma unroll
@@ -712,9 +832,13 @@ __global__ void zero_rows_kernel(char* out, const uint8_t* mask, int64_t num_hea
 namespace {
 
 // Resident workgroups of the MFMA kernel on 256 CUs (one 4-wave workgroup per CU with two
-// row groups per wave, two with one), and how many work items per slot the split aims for.
-constexpr int kResidentSlots = kRowGroups == 1 ? 512 : 256;
-constexpr int kItemsPerSlot = 1;
+// row groups per wave, SB_ATTN_OCCUPANCY with one), and how many work items per slot the
+// split aims for.
+constexpr int kResidentSlots = kRowGroups == 1 ? 256 * SB_ATTN_OCCUPANCY * 4 / kWaves : 256;
+#ifndef SB_ATTN_ITEMS_PER_SLOT
+#define SB_ATTN_ITEMS_PER_SLOT 1
+#endif
+constexpr int kItemsPerSlot = SB_ATTN_ITEMS_PER_SLOT;
 
 bool mfma_path(int32_t dtype, int64_t head_dim) {
   return (dtype == SB_DTYPE_BF16 || dtype == SB_DTYPE_F16) &&
@@ -733,7 +857,7 @@ struct Plan {
 Plan make_plan(int64_t rows_upper, int64_t group, int64_t num_kv_heads, int64_t kv_len,
                int64_t head_dim, int64_t block_size, bool paged) {
   Plan pl{};
-  pl.tile_rows = kWaveRows * kRowGroups * 4;
+  pl.tile_rows = kWaveRows * kRowGroups * kWaves;
   pl.n_tiles = (rows_upper * group + pl.tile_rows - 1) / pl.tile_rows;
   const int64_t kv_pad = (kv_len + kTileKeys - 1) / kTileKeys * kTileKeys;
   // Items no longer than the average work per slot (assuming the rows' key ranges average
@@ -780,7 +904,7 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
     dim3 mgrid(static_cast<unsigned>(pl.n_tiles * a.num_kv_heads));
 #define SB_ATT_CASE(DT, D)                                                              \
   if (dtype == DT && a.head_dim == D) {                                                 \
-    SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(256), st, a); \
+    SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(kThreads), st, a); \
     if (pl.max_chunks > 1)                                                              \
       SB_LAUNCH("attn_merge", (attn_merge_kernel<DT>), mgrid, dim3(256), st, a);        \
     return check_launch(fn);                                                            \
