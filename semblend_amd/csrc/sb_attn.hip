@@ -215,6 +215,30 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 // loads) are complete: s_waitcnt vmcnt(0), other counters untouched.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane i's chunk lands at
+// lds_wave + 16 i, where lds_wave is wave-uniform. Written as inline assembly on purpose:
+// the compiler treats a direct-to-LDS load it knows about as a pending write to the whole LDS
+// variable and waits for it (vmcnt(0)) before any later read of that variable, which would
+// serialise every prefetch with the tile being computed. Hidden from it, the loads overlap
+// the compute; the kernel orders them itself with wait_vmem() before each barrier that
+// publishes a tile. (Waits the compiler places for its own vector-memory loads stay safe:
+// completions are counted in order, so extra outstanding loads only make them stricter.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is named as clobbered on purpose
+__device__ __forceinline__ void dma_row_chunk(const char* src, const uint16_t* lds_wave) {
+  // The low 32 bits of a generic pointer into LDS are the LDS byte address.
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_wave)));
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off"
+      :
+      : "s"(m0), "v"(src)
+      : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // Work-item decode shared by the attention and merge kernels.
 struct Item {
   int kvh;
@@ -388,9 +412,7 @@ attn_mfma_kernel(AttnArgs a) {
       const int row = sl / CH;
       const int pos = sl % CH;
       const int chunk = is_k ? kswz<CH>(row, pos) : vswz<CH>(row, pos);
-      __builtin_amdgcn_global_load_lds((const SB_GLOBAL void*)(base + ro[q] + 16 * chunk),
-                                       (SB_LDS void*)(dst + (q * kThreads + wave * 64) * 8), 16, 0,
-                                       0);
+      dma_row_chunk(base + ro[q] + 16 * chunk, dst + (q * kThreads + wave * 64) * 8);
     }
   };
   auto load_k = [&](int slot, int stage) { load_rows(kbase, kofs[slot], Ks[stage], true); };
