@@ -14,7 +14,10 @@ from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "libsemblend_hip.so"
+# The library built in-tree next to this file; SEMBLEND_AMD_LIB names another build of the
+# same C ABI (for example one compiled with different tuning macros).
+LIB_PATH = Path(os.environ.get("SEMBLEND_AMD_LIB") or
+                Path(__file__).resolve().parent / "libsemblend_hip.so")
 
 SB_OK = 0
 SB_ERR_INVALID_ARGUMENT = 100001

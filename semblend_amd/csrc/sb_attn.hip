@@ -137,6 +137,15 @@ __device__ __forceinline__ int wave_min_i(int v) {
   return v;
 }
 
+// Value of v in lane (lane ^ 32): v_permlane32_swap exchanges the upper half of one register
+// with the lower half of another, so swapping v with itself and picking the moved half gives
+// the partner lane's value without a round trip through LDS.
+__device__ __forceinline__ float xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 template <int DT> struct Mma;
 template <> struct Mma<SB_DTYPE_BF16> {
   using vec8 = bf16x8_t;
@@ -535,7 +544,7 @@ attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
       exp_tile(g, s_cur, 0.f);
-      const float pair = tsum[g] + __shfl_xor(tsum[g], 32, 64);
+      const float pair = tsum[g] + xor32(tsum[g]);
       bad[g] = !seeded[g] || !(pair <= M::kPMax);
       bad_any |= bad[g];
     }
@@ -561,7 +570,7 @@ attn_mfma_kernel(AttnArgs a) {
         for (int j = 0; j < kHalves; ++j)
 #pragma unroll
           for (int i = 0; i < 16; ++i) v = fmaxf(v, s_cur[g][j][i]);
-        const float mx = fmaxf(v, __shfl_xor(v, 32, 64));  // row max of s - m_ref
+        const float mx = fmaxf(v, xor32(v));  // row max of s - m_ref
         if (bad[g] && mx != -INFINITY) {
           const float alpha = seeded[g] ? __builtin_amdgcn_exp2f(-mx) : 0.f;
           l_run[g] *= alpha;
@@ -616,7 +625,7 @@ attn_mfma_kernel(AttnArgs a) {
   // ---- finish: lane holds d = 32t + 8*(i/4) + 4*lg + (i%4) of each of its rows ----
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
-    const float l_tot = l_run[g] + __shfl_xor(l_run[g], 32, 64);
+    const float l_tot = l_run[g] + xor32(l_run[g]);
     if (p[g] < 0) continue;
     const int row_in_tile = (wave * RG + g) * kWaveRows + lq;
     if (nchunks == 1) {
@@ -655,39 +664,50 @@ attn_mfma_kernel(AttnArgs a) {
 
 // Combines the per-chunk partials of every row tile that needed more than one chunk:
 //   M = max_c m_c,  O = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.
+// One workgroup per (32 rows of a row tile, KV head); 8 threads per row, each owning D / 8
+// output elements, so the partial reads of a row are spread over 8 lanes.
 template <int DT>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
   __shared__ int red[4];
   const int tid = threadIdx.x;
-  const int TR = a.tile_rows;              // 128 or 256
+  const int TR = a.tile_rows;  // 128 or 256
+  const int parts = TR / 32;
   const int64_t n_rows = attn_num_rows(a);
   const int64_t rows_kv = n_rows * a.group;
   const int64_t n_tiles_live = (rows_kv + TR - 1) / TR;
   const int kvh = static_cast<int>(blockIdx.x % a.num_kv_heads);
-  const int64_t tile = static_cast<int64_t>(blockIdx.x / a.num_kv_heads);
+  const int64_t rest = blockIdx.x / a.num_kv_heads;
+  const int64_t tile = rest / parts;
+  const int part = static_cast<int>(rest % parts);
   if (tile >= n_tiles_live) return;
-  // 256 / TR threads per row, each owning a contiguous part of head_dim.
-  const int tpr = 256 / TR;
-  const int row_in_tile = tid / tpr;
-  const int part = tid % tpr;
-  const int64_t r = tile * TR + row_in_tile;
-  int p = -1;
-  int64_t qrow = 0;
-  int qh = 0;
-  if (r < rows_kv) {
-    const int64_t pi = r / a.group;
-    qh = kvh * a.group + static_cast<int>(r - pi * a.group);
-    p = a.positions[pi];
-    if (p >= a.kv_len) p = static_cast<int>(a.kv_len - 1);
-    qrow = a.q_by_position ? p : pi;
+  // kend of the whole row tile: the attention kernel chunked its key range by it.
+  int pm = -1;
+  for (int i = tid; i < TR; i += 256) {
+    const int64_t r = tile * TR + i;
+    if (r < rows_kv) {
+      int pp = a.positions[r / a.group];
+      if (pp >= a.kv_len) pp = static_cast<int>(a.kv_len - 1);
+      pm = max(pm, pp);
+    }
   }
-  const int pm = wave_max_i(p);
+  pm = wave_max_i(pm);
   if ((tid & 63) == 0) red[tid >> 6] = pm;
   __syncthreads();
   const int kend = max(max(red[0], red[1]), max(red[2], red[3])) + 1;
   const int nchunks = (kend + a.ksplit - 1) / a.ksplit;
-  if (nchunks <= 1 || p < 0) return;
+  if (nchunks <= 1) return;
+  const int row_in_tile = part * 32 + tid / 8;
+  const int64_t r = tile * TR + row_in_tile;
+  if (r >= rows_kv) return;
+  const int64_t pi = r / a.group;
+  const int qh = kvh * a.group + static_cast<int>(r - pi * a.group);
+  int p = a.positions[pi];
+  if (p < 0) return;
+  if (p >= a.kv_len) p = static_cast<int>(a.kv_len - 1);
+  const int64_t qrow = a.q_by_position ? p : pi;
   const int D = a.head_dim;
+  const int dpt = D / 8;
+  const int d_begin = (tid % 8) * dpt;
   const int64_t base = (static_cast<int64_t>(kvh) * a.n_tiles + tile) * a.max_chunks;
   float mmax = -INFINITY;
   for (int ch = 0; ch < nchunks; ++ch)
@@ -700,8 +720,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
   }
   const float inv = 1.f / lsum;
   char* op = a.o + qrow * a.o_s_row + qh * a.o_s_head;
-  const int d_begin = part * (D / tpr);
-  for (int d = d_begin; d < d_begin + D / tpr; d += 4) {
+  for (int d = d_begin; d < d_begin + dpt; d += 4) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int ch = 0; ch < nchunks; ++ch) {
       const int64_t slot = (base + ch) * TR + row_in_tile;
@@ -923,7 +942,7 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
     const int64_t gx = pl.n_tiles * a.num_kv_heads * pl.max_chunks;
     if (gx > 0x7fffffff) return fail(fn, "grid too large");
     dim3 grid(static_cast<unsigned>(gx));
-    dim3 mgrid(static_cast<unsigned>(pl.n_tiles * a.num_kv_heads));
+    dim3 mgrid(static_cast<unsigned>(pl.n_tiles * a.num_kv_heads * (pl.tile_rows / 32)));
 #define SB_ATT_CASE(DT, D)                                                              \
   if (dtype == DT && a.head_dim == D) {                                                 \
     SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(kThreads), st, a); \
