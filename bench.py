@@ -15,13 +15,15 @@ One step is one pass of the path over synthetic inputs resident in HBM:
 
 The reported ``value`` is the attention phase's throughput in TFLOP/s (useful causal FLOPs
 4 * D * Hq * sum(p + 1)); the scatter and RoPE phases are reported in GB/s of useful bytes
-(each moved row read once and written once). Every phase is timed with HIP events on the
-stream its kernels run on; ``ms_per_step`` is the sum of the three phase times. Each library
-kernel launch in the timed region is also bracketed by HIP events inside the library
-(``kernels``); ``roofline`` prices the MFMA attention kernel's average launch against the
-bf16 peak. ``phases.copy_ceiling`` is a plain 1 GiB device copy, the achievable HBM rate.
-The CPU baseline times the oracle (a restatement of the reference's CPU path) on a bounded
-sample of the same workload on the host's cores.
+(each moved row read once and written once). Each phase's launches are captured once into a
+HIP graph and the timed steps replay the graphs (as a serving loop would), so host launch
+overhead stays out of the phase times; every phase is timed with HIP events on the stream
+its kernels run on and ``ms_per_step`` is the sum of the three phase times. A separate eager
+pass brackets each library kernel launch with HIP events inside the library (``kernels``);
+``roofline`` prices the MFMA attention kernel's average launch against the bf16 peak.
+``phases.copy_ceiling`` is a plain 1 GiB device copy, the achievable HBM rate. The CPU
+baseline times the oracle (a restatement of the reference's CPU path, with its per-pair
+loops) on the whole workload on the host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
 """
@@ -138,22 +140,19 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(inp, budget_s: float = 20.0) -> dict:
-    """Oracle (reference CPU path restated) on a bounded sample, on the host's cores."""
+def cpu_baseline(inp) -> dict:
+    """Oracle (reference CPU path restated) on the whole workload, on the host's cores."""
     from oracle import ref_cpu as ref
 
     torch.set_num_threads(max(1, torch.get_num_threads()))
     cores = torch.get_num_threads()
-    g = torch.Generator("cpu").manual_seed(1)
     kv = inp["attn_kv"].cpu()
     bt = inp["block_table"].cpu()
     pos = inp["pos_cpu"]
     q = inp["attn_q"].cpu()
-    n_sample = 256
-    rows = torch.randperm(pos.shape[0], generator=g)[:n_sample].sort().values
-    flops = 4.0 * D * HQ * float((pos[rows].double() + 1).sum())
+    flops = 4.0 * D * HQ * float((pos.double() + 1).sum())
     t0 = time.perf_counter()
-    ref.partial_attention_paged(q[rows], kv, bt, pos[rows])
+    ref.partial_attention_paged(q, kv, bt, pos)
     dt = time.perf_counter() - t0
     out = {
         "value": flops / dt / 1e12,
@@ -161,29 +160,44 @@ def cpu_baseline(inp, budget_s: float = 20.0) -> dict:
         "cores": cores,
         "kind": "port",
         "host": {"cpu_count": os.cpu_count(), "torch_threads": cores, "model": cpu_model()},
-        "sample": f"partial attention, {n_sample} of {pos.shape[0]} recompute rows (random), "
-                  f"28q/4kv x 128, 16384-token paged context, bf16 in / fp32 math; "
-                  f"{dt:.2f} s",
+        "sample": f"whole workload: partial attention, all {pos.shape[0]} recompute rows, "
+                  f"28q/4kv x 128, 16384-token paged context, bf16 in / fp32 math {dt:.2f} s",
     }
-    # scatter and RoPE on smaller samples, reported alongside
-    n_pairs = 4096
-    sel = torch.randperm(inp["sc_d"].shape[0], generator=g)[:n_pairs]
-    cache = torch.zeros((POOL_BLOCKS, 2, HKV, BS, D), dtype=torch.bfloat16)
-    donor = inp["donors"][0].cpu()
+    # scatter (all pairs, all layers) and RoPE (the whole K) reported alongside
+    d_pos, t_pos = inp["sc_d"].cpu(), inp["sc_t"].cpu()
+    donors = [x.cpu() for x in inp["donors"]]
+    caches = [torch.zeros((POOL_BLOCKS, 2, HKV, BS, D), dtype=torch.bfloat16)
+              for _ in range(L)]
     t0 = time.perf_counter()
-    ref.scatter_donor_kv_paged(cache, donor, bt, inp["sc_d"].cpu()[sel], inp["sc_t"].cpu()[sel])
+    for layer in range(L):
+        ref.scatter_donor_kv_paged(caches[layer], donors[layer], bt, d_pos, t_pos)
     dt_s = time.perf_counter() - t0
-    out["scatter_gbps"] = n_pairs * 2 * HKV * D * 2 * 2 / dt_s / 1e9
-    n_tok = 2048
-    k = inp["rope_k"][0][:, :, :n_tok].cpu()
+    out["scatter_gbps"] = float(d_pos.shape[0]) * L * 2 * HKV * D * 2 * 2 / dt_s / 1e9
+    del caches, donors
+    k = inp["rope_k"][0].cpu()
     t0 = time.perf_counter()
-    ref.rope_correct_k(k, inp["rope_d"].cpu()[:n_tok], inp["rope_t"].cpu()[:n_tok], head_dim=D,
+    ref.rope_correct_k(k, inp["rope_d"].cpu(), inp["rope_t"].cpu(), head_dim=D,
                        rope_base=ROPE_BASE)
     dt_r = time.perf_counter() - t0
     out["rope_gbps"] = k.numel() * 2 * 2 / dt_r / 1e9
-    out["sample"] += (f"; scatter {n_pairs} pairs x 1 layer {dt_s:.2f} s; "
-                      f"rope {n_tok} tokens x 28 layers x 4 heads {dt_r:.2f} s")
+    out["sample"] += (f"; scatter {d_pos.shape[0]} pairs x {L} layers {dt_s:.2f} s; "
+                      f"rope {ROPE_TOKENS} tokens x {L} layers x {HKV} heads {dt_r:.2f} s")
     return out
+
+
+def capture(fn) -> "torch.cuda.CUDAGraph":
+    """One launch sequence of fn captured as a HIP graph (after an eager run on the capture
+    stream, so that every cached device table already exists)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
 
 
 def main() -> int:
@@ -230,31 +244,51 @@ def main() -> int:
 
     phases = [("rope", phase_rope), ("scatter", phase_scatter), ("attention", phase_attn)]
     log(f"warmup {args.warmup}")
-    for i in range(args.warmup):
+    for i in range(max(1, args.warmup)):
         for _, fn in phases:
             fn(i)
     torch.cuda.synchronize()
 
-    log(f"timing {args.steps} steps")
-    ev = {name: [] for name, _ in phases}
+    # Per-kernel durations: an eager pass with HIP events attached to each library launch.
+    log(f"kernel timing pass ({args.steps} eager steps)")
     _lib.kernel_timing(True)
-    t_wall0 = time.perf_counter()
     for i in range(args.steps):
-        for name, fn in phases:
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record()
+        for _, fn in phases:
             fn(i)
-            e1.record()
-            ev[name].append((e0, e1))
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall0
     _lib.kernel_timing(False)
     kernels = {}
     for name in KERNELS:
         total, n = _lib.kernel_time(name)
         if n:
             kernels[name] = {"launches": n, "avg_us": round(1e3 * total / n, 2)}
+
+    log("capturing one HIP graph per phase")
+    graphs = {
+        "rope": [capture(lambda c=c: phase_rope(c)) for c in range(4)],
+        "scatter": [capture(lambda: phase_scatter(0))],
+        "attention": [capture(lambda: phase_attn(0))],
+    }
+    for name, gs in graphs.items():
+        for g in gs:
+            g.replay()
+    torch.cuda.synchronize()
+
+    log(f"timing {args.steps} steps (graph replays)")
+    ev = {name: [] for name, _ in phases}
+    torch.cuda.synchronize()
+    t_wall0 = time.perf_counter()
+    for i in range(args.steps):
+        for name, _ in phases:
+            gs = graphs[name]
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            gs[i % len(gs)].replay()
+            e1.record()
+            ev[name].append((e0, e1))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall0
     copy_gbps = copy_ceiling(dev)
     log("kernels (avg us): " + ", ".join(f"{k} {v['avg_us']}" for k, v in kernels.items())
         + f"; copy ceiling {copy_gbps:.0f} GB/s")

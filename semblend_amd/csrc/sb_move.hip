@@ -27,25 +27,38 @@ enum RowMode : int { ROW_FLAT_POS = 0, ROW_PAGED_POS = 1, ROW_INDEX = 2 };
 enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3 };
 
 // Launch shape and access hints, tuned on MI355X for the 7B-shape workloads (28 layers x
-// 4 KV heads x 128, bf16). 256-thread blocks with 4 rows in flight per thread: more rows in
-// flight per thread (8 or 16, or a two-batch software pipeline) were slower, as were
-// 128/512/1024-thread blocks. Nontemporal loads and stores (the rows are touched once:
-// 316 -> 291 us for the 1.6 GB scatter). About 4096 RoPE blocks: fewer leave the per-thread
-// set-up exposed, more repeat it (83.7 us at 4096, 88 at 1024, 115 at 16384).
+// 4 KV heads x 128, bf16). 256-thread blocks (128/512/1024 were slower). The pair movers keep
+// 4 rows in flight per thread and walk 2 layers x all heads of one plane (1.6 GB scatter:
+// 288 us; 4 layers 292, 7 layers 300, 8 rows in flight 298); the row-centric RoPE keeps 8
+// rows in flight (83.1 us for K[28,4,8192,128], 84.6 with 4). Nontemporal loads and stores:
+// the rows are touched once (316 -> 291 us for the scatter). About 4096 RoPE blocks: fewer
+// leave the per-thread set-up exposed, more repeat it (84.6 us at 4096, 86 at 2048, 90 at
+// 6144).
 #ifndef SB_MOVE_THREADS
 #define SB_MOVE_THREADS 256
 #endif
 #ifndef SB_MOVE_BATCH
 #define SB_MOVE_BATCH 4
 #endif
+#ifndef SB_ROPE_BATCH
+#define SB_ROPE_BATCH 8
+#endif
 #ifndef SB_ROPE_TARGET_BLOCKS
 #define SB_ROPE_TARGET_BLOCKS 4096
 #endif
+// Pair movers' access hints (nontemporal loads / stores).
+#ifndef SB_MOVE_NT_LOAD
+#define SB_MOVE_NT_LOAD 1
+#endif
+#ifndef SB_MOVE_NT_STORE
+#define SB_MOVE_NT_STORE 1
+#endif
 #ifndef SB_SCATTER_LPG
-#define SB_SCATTER_LPG 4
+#define SB_SCATTER_LPG 2
 #endif
 constexpr int kThreads = SB_MOVE_THREADS;
-constexpr int kBatch = SB_MOVE_BATCH;  // rows loaded before the first store
+constexpr int kBatch = SB_MOVE_BATCH;      // pair movers: rows loaded before the first store
+constexpr int kRopeBatch = SB_ROPE_BATCH;  // row-centric RoPE: the same
 
 struct RowSide {
   char* base;              // layer-0 base address (used when layers == nullptr)
@@ -275,7 +288,8 @@ __global__ __launch_bounds__(kThreads) void move_rows_kernel(MoveArgs a) {
       uint32_t w[kBatch][W];
 #pragma unroll
       for (int b = 0; b < kBatch; ++b)
-        if (r0 + b < nrows) load_vec<VB, true>(row_of(a.src, r0 + b) + src_off + vofs, w[b]);
+        if (r0 + b < nrows)
+          load_vec<VB, SB_MOVE_NT_LOAD>(row_of(a.src, r0 + b) + src_off + vofs, w[b]);
 #pragma unroll
       for (int b = 0; b < kBatch; ++b) {
         if (r0 + b >= nrows) continue;
@@ -295,7 +309,7 @@ __global__ __launch_bounds__(kThreads) void move_rows_kernel(MoveArgs a) {
           }
           pack_words<DT, W>(f, w[b]);
         }
-        store_vec<VB, true>(row_of(a.dst, r0 + b) + dst_off + vofs, w[b]);
+        store_vec<VB, SB_MOVE_NT_STORE>(row_of(a.dst, r0 + b) + dst_off + vofs, w[b]);
       }
     }
   }
@@ -320,6 +334,25 @@ __global__ void rope_index_kernel(const int32_t* dpos, int64_t num_pairs, int64_
   if (d < 0 || d >= seq_len) return;
   atomicAdd(&ws[d], 1);
   atomicMax(&ws[seq_len + d], static_cast<int32_t>(num_pairs - i));
+}
+
+// Both steps in one single-workgroup launch (zero the table, barrier, count), for tables and
+// pair lists small enough that one workgroup builds them in about the time of a launch.
+constexpr int kIndexThreads = 1024;
+constexpr int64_t kIndexFusedMax = 1 << 20;  // seq_len * 2 + num_pairs
+__global__ __launch_bounds__(kIndexThreads) void rope_index_fused_kernel(const int32_t* dpos,
+                                                                         int64_t num_pairs,
+                                                                         int64_t seq_len,
+                                                                         int32_t* ws) {
+  const int tid = threadIdx.x;
+  for (int64_t i = tid; i < 2 * seq_len; i += kIndexThreads) ws[i] = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < num_pairs; i += kIndexThreads) {
+    const int64_t d = dpos[i];
+    if (d < 0 || d >= seq_len) continue;
+    atomicAdd(&ws[d], 1);
+    atomicMax(&ws[seq_len + d], static_cast<int32_t>(num_pairs - i));
+  }
 }
 
 struct RopeRowsArgs {
@@ -409,13 +442,13 @@ __global__ __launch_bounds__(kThreads) void rope_rows_kernel(RopeRowsArgs a) {
 #pragma unroll
       for (int k = 0; k < NP; ++k) sincos_rn(delta * a.inv_freq[j * NP + k], &sn[k], &c[k]);
     }
-    for (int r0 = r_begin; r0 < r_end; r0 += kBatch) {
-      uint32_t w[kBatch][W];
+    for (int r0 = r_begin; r0 < r_end; r0 += kRopeBatch) {
+      uint32_t w[kRopeBatch][W];
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b)
+      for (int b = 0; b < kRopeBatch; ++b)
         if (r0 + b < r_end) load_vec<VB, true>(k_row(r0 + b) + vofs, w[b]);
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
+      for (int b = 0; b < kRopeBatch; ++b) {
         if (r0 + b >= r_end) continue;
         if (cnt == 1) {
           float f[E];
@@ -743,12 +776,17 @@ extern "C" int sb_rope_correct_k(void* out, const void* k, const int32_t* donor_
   // Per-position pair index: counts in ws[0:S], (P - first pair) in ws[S:2S].
   int32_t* ws = workspace;
   const int64_t n = 2 * seq_len;
-  SB_LAUNCH("fill_i32", fill_i32_kernel, dim3(static_cast<unsigned>((n + 255) / 256)),
-            dim3(256), st, ws, n, 0);
-  if (num_pairs > 0)
-    SB_LAUNCH("rope_index", rope_index_kernel,
-              dim3(static_cast<unsigned>((num_pairs + 255) / 256)), dim3(256), st, donor_pos,
-              num_pairs, seq_len, ws);
+  if (n + num_pairs <= kIndexFusedMax) {
+    SB_LAUNCH("rope_index", rope_index_fused_kernel, dim3(1), dim3(kIndexThreads), st,
+              donor_pos, num_pairs, seq_len, ws);
+  } else {
+    SB_LAUNCH("fill_i32", fill_i32_kernel, dim3(static_cast<unsigned>((n + 255) / 256)),
+              dim3(256), st, ws, n, 0);
+    if (num_pairs > 0)
+      SB_LAUNCH("rope_index", rope_index_kernel,
+                dim3(static_cast<unsigned>((num_pairs + 255) / 256)), dim3(256), st,
+                donor_pos, num_pairs, seq_len, ws);
+  }
   {
     int rc = check_launch(fn);
     if (rc) return rc;
