@@ -204,6 +204,36 @@ int sb_partial_attention_paged(void* out, const void* q, const void* kv_cache,
                                const int64_t* q_strides, const int64_t* o_strides,
                                const int64_t* kv_strides, int32_t dtype, void* stream);
 
+/* Batched GQA attention over a paged cache: num_reqs requests share kv_cache, request r
+ * has rows_per_req[r] query rows and the first blocks_per_req[r] entries of block-table row
+ * block_tables[r * block_table_stride ...]. q, out and positions hold the requests' rows back
+ * to back (positions are within each request). rows_per_req and blocks_per_req are HOST
+ * arrays: the launch plan is built on the host, so the call never synchronises. Requests run
+ * longest context first, up to 16 per launch; the result equals one
+ * sb_partial_attention_paged call per request.
+ * workspace: device buffer of sb_partial_attention_paged_varlen_workspace_size(...) bytes
+ * (may be 0, then workspace may be NULL).
+ * No reference counterpart: the reference runs one request per call; this replaces the
+ * per-request loop of its callers (synapse_kv_connector/model_runner_hook.py:519-585 walks
+ * one request's layers per hook). */
+int64_t sb_partial_attention_paged_varlen_workspace_size(int64_t num_reqs,
+                                                         const int64_t* rows_per_req,
+                                                         const int64_t* blocks_per_req,
+                                                         int64_t num_q_heads,
+                                                         int64_t num_kv_heads,
+                                                         int64_t head_dim, int64_t block_size,
+                                                         int32_t dtype);
+int sb_partial_attention_paged_varlen(void* out, const void* q, const void* kv_cache,
+                                      const int32_t* block_tables, int64_t block_table_stride,
+                                      const int32_t* positions, int64_t num_reqs,
+                                      const int64_t* rows_per_req,
+                                      const int64_t* blocks_per_req, void* workspace,
+                                      int64_t workspace_bytes, int64_t num_q_heads,
+                                      int64_t num_kv_heads, int64_t head_dim,
+                                      int64_t block_size, int64_t num_blocks_total, float scale,
+                                      const int64_t* q_strides, const int64_t* o_strides,
+                                      const int64_t* kv_strides, int32_t dtype, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Kernel timing (instrumentation for benchmarks; no reference counterpart)
  * ---------------------------------------------------------------------------------------- */

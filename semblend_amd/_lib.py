@@ -54,6 +54,9 @@ SIGNATURES: dict[str, list] = {
                                      _f32, _i64p, _i64p, _i64p, _i64p, _i32, _vp],
     "sb_partial_attention_paged": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                    _i64, _i64, _i64, _f32, _i64p, _i64p, _i64p, _i32, _vp],
+    "sb_partial_attention_paged_varlen": [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64p, _i64p,
+                                          _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+                                          _i64p, _i64p, _i64p, _i32, _vp],
     "sb_kernel_timing_enable": [_i32],
     "sb_kernel_timing_read": [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), _i64p],
 }
@@ -62,6 +65,8 @@ SIGNATURES: dict[str, list] = {
 SIZE_QUERIES: dict[str, list] = {
     "sb_partial_prefill_attention_workspace_size": [_i64, _i64, _i64, _i32],
     "sb_partial_attention_paged_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i64, _i32],
+    "sb_partial_attention_paged_varlen_workspace_size": [_i64, _i64p, _i64p, _i64, _i64, _i64,
+                                                         _i64, _i32],
 }
 
 _lib: ctypes.CDLL | None = None

@@ -35,7 +35,9 @@
 
 #include "sb_common.h"
 
+#include <algorithm>
 #include <type_traits>
+#include <vector>
 
 namespace sb {
 
@@ -64,6 +66,21 @@ constexpr int kWaves = SB_ATTN_WAVES;         // waves per workgroup (each owns 
 constexpr int kThreads = 64 * kWaves;
 constexpr int kHalves = kTileKeys / 32;       // 32-key MFMA blocks per tile
 constexpr int kBtLds = 1024;    // block-table entries staged per chunk
+
+// One request of a batched (varlen) launch: its rows, its block-table row, and where its work
+// items, merge workgroups and partial slots start in the launch.
+constexpr int kMaxReqs = 16;
+struct ReqSlice {
+  int64_t item_begin;   // first attention workgroup of the request
+  int64_t merge_begin;  // first merge workgroup
+  int64_t row_begin;    // first entry in positions (and q / out rows)
+  int64_t num_rows;
+  int64_t bt_begin;     // first entry of the request's block table
+  int64_t num_blocks;   // entries of that table
+  int64_t n_tiles;      // row tiles of the request (partial layout)
+  int64_t part_begin;   // first partial row slot
+  int max_chunks;
+};
 
 struct AttnArgs {
   const char* q;        // query rows
@@ -96,6 +113,43 @@ struct AttnArgs {
   float* part_o;              // [Hkv][n_tiles][max_chunks][128][D] fp32, or nullptr
   float* part_ml;             // [Hkv][n_tiles][max_chunks][128][2] fp32 (m, l)
 };
+
+// Kernel parameter: the call's arguments and, for a batched launch, the request table (read
+// in place from the kernel-argument segment).
+struct AttnBatch {
+  AttnArgs a;
+  int num_reqs;               // requests in `req` (0: one request, described by `a`)
+  ReqSlice req[kMaxReqs];
+};
+
+// Batched launch: selects the request that workgroup `b` (an index into the launch's
+// attention or merge grid) belongs to, narrows `a` to that request, and returns b relative to
+// the request's first workgroup. A single-request launch returns b unchanged.
+__device__ __forceinline__ int64_t select_request(const AttnBatch& batch, AttnArgs& a,
+                                                  int64_t b, bool merge) {
+  if (batch.num_reqs <= 0) return b;
+  int r = 0;
+  while (r + 1 < batch.num_reqs &&
+         b >= (merge ? batch.req[r + 1].merge_begin : batch.req[r + 1].item_begin))
+    ++r;
+  const ReqSlice& s = batch.req[r];
+  a.positions += s.row_begin;
+  if (!a.q_by_position) {
+    a.q += s.row_begin * a.q_s_row;
+    a.o += s.row_begin * a.o_s_row;
+  }
+  a.num_rows = s.num_rows;
+  a.block_table += s.bt_begin;
+  a.nb_per_seq = s.num_blocks;
+  a.kv_len = s.num_blocks * a.block_size;
+  a.n_tiles = s.n_tiles;
+  a.max_chunks = s.max_chunks;
+  if (a.part_o) {
+    a.part_o += s.part_begin * a.head_dim;
+    a.part_ml += s.part_begin * 2;
+  }
+  return b - (merge ? s.merge_begin : s.item_begin);
+}
 
 __device__ __forceinline__ int64_t attn_num_rows(const AttnArgs& a) {
   return a.count_ptr ? static_cast<int64_t>(*a.count_ptr) : a.num_rows;
@@ -255,10 +309,10 @@ struct Item {
   int chunk;
 };
 
-__device__ __forceinline__ Item decode_item(const AttnArgs& a, int64_t n_tiles_live) {
-  // blockIdx.x = (chunk * n_tiles + tile_rev) * Hkv + kvh; tiles taken in descending order.
+__device__ __forceinline__ Item decode_item(const AttnArgs& a, int64_t n_tiles_live,
+                                           int64_t b) {
+  // b = (chunk * n_tiles + tile_rev) * Hkv + kvh; tiles taken in descending order.
   Item it;
-  const int64_t b = blockIdx.x;
   it.kvh = static_cast<int>(b % a.num_kv_heads);
   const int64_t rest = b / a.num_kv_heads;
   const int64_t tile_rev = rest % a.n_tiles;
@@ -269,7 +323,9 @@ __device__ __forceinline__ Item decode_item(const AttnArgs& a, int64_t n_tiles_l
 
 template <int DT, int D, int RG>
 __global__ __launch_bounds__(kThreads, RG == 1 ? SB_ATTN_OCCUPANCY * 4 / kWaves : 1) void
-attn_mfma_kernel(AttnArgs a) {
+attn_mfma_kernel(const AttnBatch batch) {
+  AttnArgs a = batch.a;
+  const int64_t item_b = select_request(batch, a, blockIdx.x, false);
   using M = Mma<DT>;
   using vec8 = typename M::vec8;
   constexpr int TR = kWaveRows * RG * kWaves;  // flattened rows per workgroup tile
@@ -295,7 +351,7 @@ attn_mfma_kernel(AttnArgs a) {
   const int64_t n_rows = attn_num_rows(a);
   const int64_t rows_kv = n_rows * a.group;
   const int64_t n_tiles_live = (rows_kv + TR - 1) / TR;
-  const Item item = decode_item(a, n_tiles_live);
+  const Item item = decode_item(a, n_tiles_live, item_b);
   if (item.tile < 0 || item.chunk >= a.max_chunks) return;  // uniform, before any barrier
   const int kvh = item.kvh;
 
@@ -667,16 +723,18 @@ attn_mfma_kernel(AttnArgs a) {
 // One workgroup per (32 rows of a row tile, KV head); 8 threads per row, each owning D / 8
 // output elements, so the partial reads of a row are spread over 8 lanes.
 template <int DT>
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void attn_merge_kernel(const AttnBatch batch) {
   __shared__ int red[4];
+  AttnArgs a = batch.a;
+  const int64_t mb = select_request(batch, a, blockIdx.x, true);
   const int tid = threadIdx.x;
   const int TR = a.tile_rows;  // 128 or 256
   const int parts = TR / 32;
   const int64_t n_rows = attn_num_rows(a);
   const int64_t rows_kv = n_rows * a.group;
   const int64_t n_tiles_live = (rows_kv + TR - 1) / TR;
-  const int kvh = static_cast<int>(blockIdx.x % a.num_kv_heads);
-  const int64_t rest = blockIdx.x / a.num_kv_heads;
+  const int kvh = static_cast<int>(mb % a.num_kv_heads);
+  const int64_t rest = mb / a.num_kv_heads;
   const int64_t tile = rest / parts;
   const int part = static_cast<int>(rest % parts);
   if (tile >= n_tiles_live) return;
@@ -943,11 +1001,14 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
     if (gx > 0x7fffffff) return fail(fn, "grid too large");
     dim3 grid(static_cast<unsigned>(gx));
     dim3 mgrid(static_cast<unsigned>(pl.n_tiles * a.num_kv_heads * (pl.tile_rows / 32)));
+    AttnBatch one{};
+    one.a = a;
+    one.num_reqs = 0;
 #define SB_ATT_CASE(DT, D)                                                              \
   if (dtype == DT && a.head_dim == D) {                                                 \
-    SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(kThreads), st, a); \
+    SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(kThreads), st, one); \
     if (pl.max_chunks > 1)                                                              \
-      SB_LAUNCH("attn_merge", (attn_merge_kernel<DT>), mgrid, dim3(256), st, a);        \
+      SB_LAUNCH("attn_merge", (attn_merge_kernel<DT>), mgrid, dim3(256), st, one);      \
     return check_launch(fn);                                                            \
   }
     SB_ATT_CASE(SB_DTYPE_BF16, 128)
@@ -963,6 +1024,144 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
   else if (dtype == SB_DTYPE_BF16) SB_LAUNCH("attn_valu", attn_valu_kernel<SB_DTYPE_BF16>, grid, dim3(64), st, a);
   else SB_LAUNCH("attn_valu", attn_valu_kernel<SB_DTYPE_F16>, grid, dim3(64), st, a);
   return check_launch(fn);
+}
+
+// Batched (varlen) launches over several requests that share the paged cache: one common
+// key split for the batch (the average work per resident workgroup slot over all requests),
+// requests taken longest context first, at most kMaxReqs per launch.
+struct VarlenPlan {
+  int ksplit = 0;
+  int64_t part_bytes = 0;          // largest partial buffer of one launch
+  std::vector<int> order;          // requests, longest context first (empty ones dropped)
+  std::vector<int64_t> n_tiles, max_chunks, row_begin;
+};
+
+VarlenPlan make_varlen_plan(int64_t num_reqs, const int64_t* rows, const int64_t* blocks,
+                            int64_t block_size, int64_t group, int64_t num_kv_heads,
+                            int64_t head_dim) {
+  VarlenPlan pl;
+  const int tr = kWaveRows * kRowGroups * kWaves;
+  pl.n_tiles.assign(num_reqs, 0);
+  pl.max_chunks.assign(num_reqs, 1);
+  pl.row_begin.assign(num_reqs, 0);
+  int64_t work = 0, kv_max = 0, run = 0;
+  for (int64_t r = 0; r < num_reqs; ++r) {
+    pl.row_begin[r] = run;
+    run += rows[r];
+    pl.n_tiles[r] = (rows[r] * group + tr - 1) / tr;
+    const int64_t kv = blocks[r] * block_size;
+    if (rows[r] > 0 && blocks[r] > 0) {
+      pl.order.push_back(static_cast<int>(r));
+      work += pl.n_tiles[r] * num_kv_heads * (kv / 2);
+      kv_max = kv > kv_max ? kv : kv_max;
+    }
+  }
+  std::stable_sort(pl.order.begin(), pl.order.end(), [&](int x, int y) {
+    return blocks[x] * block_size > blocks[y] * block_size;
+  });
+  int64_t ks = work / kResidentSlots;
+  ks = ks / kTileKeys * kTileKeys;
+  if (ks < 512) ks = 512;
+  const int64_t cap = static_cast<int64_t>(kBtLds) * block_size / kTileKeys * kTileKeys;
+  if (ks > cap) ks = cap;
+  const int64_t kv_pad = (kv_max + kTileKeys - 1) / kTileKeys * kTileKeys;
+  if (ks > kv_pad) ks = kv_pad;
+  if (ks < kTileKeys) ks = kTileKeys;
+  pl.ksplit = static_cast<int>(ks);
+  for (size_t g0 = 0; g0 < pl.order.size(); g0 += kMaxReqs) {
+    int64_t part_rows = 0;
+    for (size_t i = g0; i < pl.order.size() && i < g0 + kMaxReqs; ++i) {
+      const int r = pl.order[i];
+      const int64_t kv = blocks[r] * block_size;
+      pl.max_chunks[r] = (kv + ks - 1) / ks;
+      if (pl.max_chunks[r] > 1) part_rows += num_kv_heads * pl.n_tiles[r] * pl.max_chunks[r] * tr;
+    }
+    const int64_t bytes = part_rows * (head_dim + 2) * 4;
+    if (bytes > pl.part_bytes) pl.part_bytes = bytes;
+  }
+  return pl;
+}
+
+// `a` describes the shared cache, q, out and strides; positions, q and out hold the requests'
+// rows back to back; request r's block table is block_tables[r * bt_stride ...].
+int launch_attention_varlen(const char* fn, AttnArgs a, int32_t dtype, int64_t num_reqs,
+                            const int64_t* rows, const int64_t* blocks, int64_t bt_stride,
+                            bool aligned16, void* workspace, int64_t workspace_bytes,
+                            hipStream_t st) {
+  const VarlenPlan pl = make_varlen_plan(num_reqs, rows, blocks, a.block_size, a.group,
+                                         a.num_kv_heads, a.head_dim);
+  if (!(mfma_path(dtype, a.head_dim) && aligned16)) {
+    // VALU path: one launch per request.
+    for (int r : pl.order) {
+      AttnArgs b = a;
+      b.positions = a.positions + pl.row_begin[r];
+      b.q = a.q + pl.row_begin[r] * a.q_s_row;
+      b.o = a.o + pl.row_begin[r] * a.o_s_row;
+      b.num_rows = rows[r];
+      b.block_table = a.block_table + r * bt_stride;
+      b.nb_per_seq = blocks[r];
+      b.kv_len = blocks[r] * a.block_size;
+      const int rc = launch_attention(fn, b, dtype, rows[r], aligned16, workspace,
+                                      workspace_bytes, st);
+      if (rc) return rc;
+    }
+    return SB_OK;
+  }
+  if (pl.part_bytes > 0 && (!workspace || workspace_bytes < pl.part_bytes))
+    return fail(fn, "workspace too small for the split-key partials");
+  const int tr = kWaveRows * kRowGroups * kWaves;
+  a.ksplit = pl.ksplit;
+  a.tile_rows = tr;
+  a.part_o = pl.part_bytes > 0 ? static_cast<float*>(workspace) : nullptr;
+  for (size_t g0 = 0; g0 < pl.order.size(); g0 += kMaxReqs) {
+    AttnBatch b{};
+    b.a = a;
+    b.num_reqs = 0;
+    int64_t items = 0, merges = 0, part_rows = 0, part_total = 0;
+    bool split = false;
+    for (size_t i = g0; i < pl.order.size() && i < g0 + kMaxReqs; ++i) {
+      const int r = pl.order[i];
+      if (pl.max_chunks[r] > 1) part_total += a.num_kv_heads * pl.n_tiles[r] * pl.max_chunks[r] * tr;
+    }
+    for (size_t i = g0; i < pl.order.size() && i < g0 + kMaxReqs; ++i) {
+      const int r = pl.order[i];
+      ReqSlice& sl = b.req[b.num_reqs++];
+      sl.item_begin = items;
+      sl.merge_begin = merges;
+      sl.row_begin = pl.row_begin[r];
+      sl.num_rows = rows[r];
+      sl.bt_begin = r * bt_stride;
+      sl.num_blocks = blocks[r];
+      sl.n_tiles = pl.n_tiles[r];
+      sl.max_chunks = static_cast<int>(pl.max_chunks[r]);
+      sl.part_begin = part_rows;
+      items += pl.n_tiles[r] * a.num_kv_heads * pl.max_chunks[r];
+      merges += pl.n_tiles[r] * a.num_kv_heads * (tr / 32);
+      if (pl.max_chunks[r] > 1) {
+        part_rows += a.num_kv_heads * pl.n_tiles[r] * pl.max_chunks[r] * tr;
+        split = true;
+      }
+    }
+    if (b.a.part_o) b.a.part_ml = b.a.part_o + part_total * a.head_dim;
+    if (items > 0x7fffffff || merges > 0x7fffffff) return fail(fn, "grid too large");
+    const dim3 grid(static_cast<unsigned>(items));
+    const dim3 mgrid(static_cast<unsigned>(merges));
+#define SB_ATT_VCASE(DT, D)                                                             \
+  if (dtype == DT && a.head_dim == D) {                                                 \
+    SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(kThreads), st, b); \
+    if (split) SB_LAUNCH("attn_merge", (attn_merge_kernel<DT>), mgrid, dim3(256), st, b); \
+    const int rc = check_launch(fn);                                                    \
+    if (rc) return rc;                                                                  \
+    continue;                                                                           \
+  }
+    SB_ATT_VCASE(SB_DTYPE_BF16, 128)
+    SB_ATT_VCASE(SB_DTYPE_BF16, 64)
+    SB_ATT_VCASE(SB_DTYPE_F16, 128)
+    SB_ATT_VCASE(SB_DTYPE_F16, 64)
+#undef SB_ATT_VCASE
+    return fail(fn, "internal: no MFMA kernel for this dtype / head_dim");
+  }
+  return SB_OK;
 }
 
 int log2_exact(int64_t v) {
@@ -1084,25 +1283,20 @@ extern "C" int64_t sb_partial_attention_paged_workspace_size(int64_t num_rows,
                         num_blocks_per_seq * block_size, head_dim, block_size, true);
 }
 
-extern "C" int sb_partial_attention_paged(void* out, const void* q, const void* kv_cache,
-                                          const int32_t* block_table, const int32_t* positions,
-                                          void* workspace, int64_t workspace_bytes,
-                                          int64_t num_rows, int64_t num_q_heads,
-                                          int64_t num_kv_heads, int64_t head_dim,
-                                          int64_t block_size, int64_t num_blocks_total,
-                                          int64_t num_blocks_per_seq, float scale,
-                                          const int64_t* qs, const int64_t* os,
-                                          const int64_t* kvs, int32_t dtype, void* stream) {
-  const char* fn = "sb_partial_attention_paged";
-  clear_error();
-  if (num_rows == 0 || num_q_heads == 0 || head_dim == 0) return SB_OK;
+namespace {
+
+// Shared argument checks and set-up of the paged entry points (single and batched).
+int paged_args(const char* fn, AttnArgs* pa, bool* aligned16, void* out, const void* q,
+               const void* kv_cache, const int32_t* block_table, const int32_t* positions,
+               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+               int64_t num_blocks_total, float scale, const int64_t* qs, const int64_t* os,
+               const int64_t* kvs, int32_t dtype) {
   if (elem_size(dtype) == 0) return fail(fn, "invalid dtype");
   if (!out || !q || !kv_cache || !block_table || !positions || !qs || !os || !kvs)
     return fail(fn, "null pointer argument");
   if (num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
     return fail(fn, "num_q_heads must be a multiple of num_kv_heads");
-  if (block_size <= 0 || num_blocks_per_seq <= 0 || num_blocks_total <= 0)
-    return fail(fn, "empty block table or pool");
+  if (block_size <= 0 || num_blocks_total <= 0) return fail(fn, "empty block table or pool");
   if (qs[2] != 1 || os[2] != 1 || kvs[4] != 1)
     return fail(fn, "head_dim must be contiguous (stride 1)");
   const int64_t es = elem_size(dtype);
@@ -1116,7 +1310,6 @@ extern "C" int sb_partial_attention_paged(void* out, const void* q, const void* 
   a.q_by_position = 0;
   a.positions = positions;
   a.count_ptr = nullptr;
-  a.num_rows = num_rows;
   a.k = static_cast<const char*>(kv_cache);
   a.v = static_cast<const char*>(kv_cache) + kvs[1] * es;
   a.k_s_head = kvs[2] * es;
@@ -1126,19 +1319,90 @@ extern "C" int sb_partial_attention_paged(void* out, const void* q, const void* 
   a.block_size = block_size;
   a.bs_log2 = log2_exact(block_size);
   a.nb_total = num_blocks_total;
-  a.nb_per_seq = num_blocks_per_seq;
   a.s_block = kvs[0] * es;
   a.s_pos = kvs[3] * es;
-  a.kv_len = num_blocks_per_seq * block_size;
   a.num_kv_heads = static_cast<int>(num_kv_heads);
   a.group = static_cast<int>(num_q_heads / num_kv_heads);
   a.head_dim = static_cast<int>(head_dim);
   a.scale = scale;
   a.scale_log2 = scale * 1.4426950408889634f;
-  const bool aligned16 =
-      vec_bytes({reinterpret_cast<int64_t>(q), reinterpret_cast<int64_t>(kv_cache),
-                 reinterpret_cast<int64_t>(out), qs[0] * es, qs[1] * es, os[0] * es,
-                 os[1] * es, kvs[0] * es, kvs[1] * es, kvs[2] * es, kvs[3] * es}) >= 16;
+  *aligned16 = vec_bytes({reinterpret_cast<int64_t>(q), reinterpret_cast<int64_t>(kv_cache),
+                          reinterpret_cast<int64_t>(out), qs[0] * es, qs[1] * es, os[0] * es,
+                          os[1] * es, kvs[0] * es, kvs[1] * es, kvs[2] * es, kvs[3] * es}) >= 16;
+  *pa = a;
+  return SB_OK;
+}
+
+}  // namespace
+
+extern "C" int sb_partial_attention_paged(void* out, const void* q, const void* kv_cache,
+                                          const int32_t* block_table, const int32_t* positions,
+                                          void* workspace, int64_t workspace_bytes,
+                                          int64_t num_rows, int64_t num_q_heads,
+                                          int64_t num_kv_heads, int64_t head_dim,
+                                          int64_t block_size, int64_t num_blocks_total,
+                                          int64_t num_blocks_per_seq, float scale,
+                                          const int64_t* qs, const int64_t* os,
+                                          const int64_t* kvs, int32_t dtype, void* stream) {
+  const char* fn = "sb_partial_attention_paged";
+  clear_error();
+  if (num_rows == 0 || num_q_heads == 0 || head_dim == 0) return SB_OK;
+  if (num_blocks_per_seq <= 0) return fail(fn, "empty block table or pool");
+  AttnArgs a;
+  bool aligned16 = false;
+  const int rc = paged_args(fn, &a, &aligned16, out, q, kv_cache, block_table, positions,
+                            num_q_heads, num_kv_heads, head_dim, block_size, num_blocks_total,
+                            scale, qs, os, kvs, dtype);
+  if (rc) return rc;
+  a.num_rows = num_rows;
+  a.nb_per_seq = num_blocks_per_seq;
+  a.kv_len = num_blocks_per_seq * block_size;
   return launch_attention(fn, a, dtype, num_rows, aligned16, workspace, workspace_bytes,
                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t sb_partial_attention_paged_varlen_workspace_size(
+    int64_t num_reqs, const int64_t* rows_per_req, const int64_t* blocks_per_req,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+    int32_t dtype) {
+  if (num_reqs <= 0 || !rows_per_req || !blocks_per_req || num_kv_heads <= 0 ||
+      num_q_heads % num_kv_heads != 0 || block_size <= 0)
+    return 0;
+  const int64_t group = num_q_heads / num_kv_heads;
+  if (!mfma_path(dtype, head_dim)) return 0;
+  return make_varlen_plan(num_reqs, rows_per_req, blocks_per_req, block_size, group,
+                          num_kv_heads, head_dim)
+      .part_bytes;
+}
+
+extern "C" int sb_partial_attention_paged_varlen(
+    void* out, const void* q, const void* kv_cache, const int32_t* block_tables,
+    int64_t block_table_stride, const int32_t* positions, int64_t num_reqs,
+    const int64_t* rows_per_req, const int64_t* blocks_per_req, void* workspace,
+    int64_t workspace_bytes, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t block_size, int64_t num_blocks_total, float scale, const int64_t* qs,
+    const int64_t* os, const int64_t* kvs, int32_t dtype, void* stream) {
+  const char* fn = "sb_partial_attention_paged_varlen";
+  clear_error();
+  if (num_reqs == 0 || num_q_heads == 0 || head_dim == 0) return SB_OK;
+  if (num_reqs < 0 || !rows_per_req || !blocks_per_req)
+    return fail(fn, "null per-request array");
+  int64_t total_rows = 0;
+  for (int64_t r = 0; r < num_reqs; ++r) {
+    if (rows_per_req[r] < 0 || blocks_per_req[r] < 0)
+      return fail(fn, "negative per-request row or block count");
+    if (rows_per_req[r] > 0 && blocks_per_req[r] > block_table_stride)
+      return fail(fn, "a request has more blocks than the block-table row holds");
+    total_rows += rows_per_req[r];
+  }
+  if (total_rows == 0) return SB_OK;
+  AttnArgs a;
+  bool aligned16 = false;
+  const int rc = paged_args(fn, &a, &aligned16, out, q, kv_cache, block_tables, positions,
+                            num_q_heads, num_kv_heads, head_dim, block_size, num_blocks_total,
+                            scale, qs, os, kvs, dtype);
+  if (rc) return rc;
+  return launch_attention_varlen(fn, a, dtype, num_reqs, rows_per_req, blocks_per_req,
+                                 block_table_stride, aligned16, workspace, workspace_bytes,
+                                 static_cast<hipStream_t>(stream));
 }

@@ -313,6 +313,79 @@ def partial_prefill_attention_paged(
     return out
 
 
+def partial_prefill_attention_paged_varlen(
+    query: torch.Tensor,
+    kv_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    compute_positions: torch.Tensor,
+    rows_per_request,
+    blocks_per_request,
+    scale: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Batched form of :func:`partial_prefill_attention_paged` for requests sharing one paged
+    cache (one layer), in one launch per 16 requests.
+
+    query: [sum(rows), num_q_heads, head_dim], the requests' rows back to back;
+    compute_positions: [sum(rows)] int32, each row's position within its own request;
+    block_tables: [num_requests, max_blocks] int32, request r using its first
+    ``blocks_per_request[r]`` entries; rows_per_request / blocks_per_request: host integer
+    sequences (the launch plan is built on the host, so the call never synchronises).
+    Returns [sum(rows), num_q_heads, head_dim]. Extension with no reference counterpart (the
+    reference runs one request per call); replaces a per-request loop over
+    :func:`partial_prefill_attention_paged`.
+    """
+    dev = _lib.require_device(query, kv_cache, block_tables)
+    rows = [int(r) for r in rows_per_request]
+    blocks = [int(b) for b in blocks_per_request]
+    if len(rows) != len(blocks):
+        raise ValueError("rows_per_request and blocks_per_request differ in length")
+    num_rows, num_q_heads, head_dim = query.shape
+    nb_total, _, num_kv_heads, block_size, hd = kv_cache.shape
+    if hd != head_dim:
+        raise ValueError("query and kv_cache head_dim differ")
+    if num_q_heads % num_kv_heads:
+        raise ValueError("num_q_heads must be a multiple of num_kv_heads")
+    if query.dtype != kv_cache.dtype:
+        raise TypeError("query and kv_cache must share a dtype")
+    if sum(rows) != num_rows:
+        raise ValueError("rows_per_request must sum to the number of query rows")
+    if block_tables.dim() != 2 or block_tables.shape[0] != len(rows):
+        raise ValueError("block_tables must be [num_requests, max_blocks]")
+    if any(b > block_tables.shape[1] for b in blocks):
+        raise ValueError("a request has more blocks than its block-table row")
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    if out is None:
+        out = torch.empty((num_rows, num_q_heads, head_dim), dtype=query.dtype, device=dev)
+    if num_rows == 0:
+        return out
+    q = query if query.stride(-1) == 1 else query.contiguous()
+    kv = kv_cache if kv_cache.stride(-1) == 1 else kv_cache.contiguous()
+    pos = _lib.as_index(compute_positions, dev)
+    if pos.shape[0] != num_rows:
+        raise ValueError("compute_positions must have one entry per query row")
+    bt = block_tables
+    if bt.dtype != torch.int32 or bt.stride(1) != 1:
+        bt = bt.to(torch.int32).contiguous()
+    rows_a = _lib.i64_array(rows)
+    blocks_a = _lib.i64_array(blocks)
+    dt = _lib.dtype_code(q)
+    ws_bytes = _lib.size_query("sb_partial_attention_paged_varlen_workspace_size", len(rows),
+                               rows_a, blocks_a, num_q_heads, num_kv_heads, head_dim,
+                               block_size, dt)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_partial_attention_paged_varlen",
+            out.data_ptr(), q.data_ptr(), kv.data_ptr(), bt.data_ptr(), bt.stride(0),
+            pos.data_ptr(), len(rows), rows_a, blocks_a, _lib.ptr(ws), ws_bytes, num_q_heads,
+            num_kv_heads, head_dim, block_size, nb_total, float(scale), _lib.strides(q),
+            _lib.strides(out), _lib.strides(kv), dt, _lib.stream_handle(dev),
+        )
+    return out
+
+
 # ------------------------------------------------------------------------------------------
 # Orchestrator
 # ------------------------------------------------------------------------------------------

@@ -1,0 +1,98 @@
+"""GPU parity: batched (multi-request) entry points against the oracle, request by request.
+
+Requests share one paged pool with their own (permuted, disjoint) block tables, as in a
+serving batch; each request's result must match the oracle run on that request alone.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import ref_cpu as ref
+from semblend_amd import triton_kernels as tk
+from tests.helpers import assert_attn_close, gen, randn
+
+pytestmark = pytest.mark.gpu
+
+
+def _batch(ctx, nrows, hq, hkv, d, dtype, seed, bs=16):
+    """Shared pool, per-request block tables (rows of a padded table), positions, queries."""
+    g = gen(seed)
+    nblk = [(c + bs - 1) // bs for c in ctx]
+    pool = sum(nblk) + 7
+    kv = randn((pool, 2, hkv, bs, d), dtype, seed + 1)
+    perm = torch.randperm(pool, generator=g)
+    tables = torch.full((len(ctx), max(nblk)), -1, dtype=torch.int32)
+    at = 0
+    for r, n in enumerate(nblk):
+        tables[r, :n] = perm[at:at + n].to(torch.int32)
+        at += n
+    pos = [torch.randperm(c, generator=g)[:n].sort().values.to(torch.int32)
+           for c, n in zip(ctx, nrows)]
+    q = randn((sum(nrows), hq, d), dtype, seed + 2)
+    return kv, tables, nblk, pos, q
+
+
+def _check(kv, tables, nblk, pos, q, out, nrows):
+    at = 0
+    for r, n in enumerate(nrows):
+        if n == 0:
+            continue
+        want = ref.partial_attention_paged(q[at:at + n], kv, tables[r, :nblk[r]], pos[r])
+        assert_attn_close(out[at:at + n], want)
+        at += n
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_varlen_llama_shape(dev, dtype):
+    ctx, nrows = [512, 1024, 1536, 2048], [40, 100, 200, 300]
+    kv, tables, nblk, pos, q = _batch(ctx, nrows, 32, 8, 128, dtype, 100)
+    out = tk.partial_prefill_attention_paged_varlen(
+        q.to(dev), kv.to(dev), tables.to(dev), torch.cat(pos).to(dev), nrows, nblk)
+    _check(kv, tables, nblk, pos, q, out, nrows)
+
+
+def test_varlen_matches_single_calls(dev):
+    ctx, nrows = [2048, 700, 1300], [150, 60, 90]
+    kv, tables, nblk, pos, q = _batch(ctx, nrows, 28, 4, 128, torch.bfloat16, 110)
+    kvd, qd = kv.to(dev), q.to(dev)
+    out = tk.partial_prefill_attention_paged_varlen(
+        qd, kvd, tables.to(dev), torch.cat(pos).to(dev), nrows, nblk)
+    at = 0
+    for r, n in enumerate(nrows):
+        single = tk.partial_prefill_attention_paged(qd[at:at + n], kvd,
+                                                    tables[r, :nblk[r]].to(dev),
+                                                    pos[r].to(dev))
+        # same arithmetic up to the split of the key range (fp32 partial merges)
+        assert float((out[at:at + n].float() - single.float()).abs().max()) <= 1e-2
+        at += n
+
+
+def test_varlen_empty_requests_and_many_launches(dev):
+    # 20 requests (two launches of at most 16), two of them without rows
+    ctx = [128 + 96 * i for i in range(20)]
+    nrows = [0 if i in (3, 11) else 5 + 3 * i for i in range(20)]
+    kv, tables, nblk, pos, q = _batch(ctx, nrows, 8, 2, 64, torch.bfloat16, 120)
+    out = tk.partial_prefill_attention_paged_varlen(
+        q.to(dev), kv.to(dev), tables.to(dev), torch.cat(pos).to(dev), nrows, nblk)
+    _check(kv, tables, nblk, pos, q, out, nrows)
+
+
+def test_varlen_fp32_per_request_path(dev):
+    ctx, nrows = [300, 640], [20, 33]
+    kv, tables, nblk, pos, q = _batch(ctx, nrows, 14, 2, 64, torch.float32, 130)
+    out = tk.partial_prefill_attention_paged_varlen(
+        q.to(dev), kv.to(dev), tables.to(dev), torch.cat(pos).to(dev), nrows, nblk)
+    _check(kv, tables, nblk, pos, q, out, nrows)
+
+
+def test_varlen_rejects_bad_plans(dev):
+    kv, tables, nblk, pos, q = _batch([256, 256], [4, 4], 8, 2, 64, torch.bfloat16, 140)
+    with pytest.raises(ValueError):
+        tk.partial_prefill_attention_paged_varlen(
+            q.to(dev), kv.to(dev), tables.to(dev), torch.cat(pos).to(dev), [4, 5], nblk)
+    with pytest.raises(ValueError):
+        tk.partial_prefill_attention_paged_varlen(
+            q.to(dev), kv.to(dev), tables.to(dev), torch.cat(pos).to(dev), [4, 4],
+            [nblk[0], tables.shape[1] + 1])
