@@ -64,16 +64,67 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def recompute_positions(g: torch.Generator) -> torch.Tensor:
-    """First 256 tokens + two random whole chunks + uniform scatter, 2458 in total."""
-    n_chunks = CTX // CHUNK
-    mask = torch.zeros(CTX, dtype=torch.bool)
-    mask[:CHUNK] = True
+def recompute_positions(g: torch.Generator, ctx: int = CTX,
+                        n_recompute: int = N_RECOMPUTE) -> torch.Tensor:
+    """First 256 tokens + two random whole chunks + uniform scatter, n_recompute in total
+    (chunks only while they fit the budget)."""
+    n_chunks = ctx // CHUNK
+    mask = torch.zeros(ctx, dtype=torch.bool)
+    mask[:min(CHUNK, n_recompute)] = True
     for c in (torch.randperm(n_chunks - 1, generator=g)[:2] + 1).tolist():
-        mask[c * CHUNK:(c + 1) * CHUNK] = True
+        if int(mask.sum()) + CHUNK <= n_recompute:
+            mask[c * CHUNK:(c + 1) * CHUNK] = True
     rest = (~mask).nonzero().flatten()
-    mask[rest[torch.randperm(rest.numel(), generator=g)[:N_RECOMPUTE - int(mask.sum())]]] = True
+    mask[rest[torch.randperm(rest.numel(), generator=g)[:n_recompute - int(mask.sum())]]] = True
     return mask.nonzero().flatten().to(torch.int32)
+
+
+# Llama-3-8B batch (four requests sharing one paged pool, all layers).
+LLAMA = {"layers": 32, "hq": 32, "hkv": 8, "d": 128, "theta": 5e5,
+         "ctx": (8192, 16384, 24576, 32768), "frac": (0.10, 0.15, 0.20, 0.30),
+         "pool_blocks": 8192, "delta": 4096}
+
+
+def llama_batch(dev: torch.device, layers: int = LLAMA["layers"], ctx=LLAMA["ctx"],
+                frac=LLAMA["frac"], pool_blocks: int = LLAMA["pool_blocks"],
+                max_delta: int = LLAMA["delta"], seed: int = 4):
+    """Synthetic Llama-3-8B KV-reuse batch: per-layer caches [pool, 2, 8, 16, 128] bf16 filled
+    with N(0, 1) (the recompute rows' fresh K/V), per-request donor buffers [2, 8, ctx, 128],
+    reuse pairs t -> d = t - delta with delta constant per 256-token chunk (uniform in
+    [-max_delta, max_delta], redrawn until the chunk's donor rows lie in the donor buffer),
+    recompute sets built like the 7B workload, and block tables drawn from one random
+    permutation of the pool. Returns (caches, requests, theta)."""
+    from semblend_amd.batch import ReuseRequest
+
+    g = torch.Generator("cpu").manual_seed(seed)
+    gd = torch.Generator(dev).manual_seed(seed)
+    hkv, d = LLAMA["hkv"], LLAMA["d"]
+    caches = [torch.randn((pool_blocks, 2, hkv, BS, d), generator=gd, device=dev,
+                          dtype=torch.bfloat16) for _ in range(layers)]
+    perm = torch.randperm(pool_blocks, generator=g)
+    requests, at = [], 0
+    for c, f in zip(ctx, frac):
+        nblk = (c + BS - 1) // BS
+        if at + nblk > pool_blocks:
+            raise ValueError("pool too small for the batch")
+        bt = perm[at:at + nblk].to(torch.int32)
+        at += nblk
+        pos_r = recompute_positions(g, c, int(round(c * f)))
+        keep = torch.ones(c, dtype=torch.bool)
+        keep[pos_r.long()] = False
+        t = torch.arange(c)[keep]
+        delta = torch.empty(c // CHUNK + 1, dtype=torch.int64)
+        for k in range(delta.numel()):
+            lo, hi = max(-max_delta, k * CHUNK + CHUNK - c), min(max_delta, k * CHUNK)
+            delta[k] = torch.randint(lo, hi + 1, (1,), generator=g)
+        dpos = t - delta[t // CHUNK]
+        donors = [torch.randn((2, hkv, c, d), generator=gd, device=dev, dtype=torch.bfloat16)
+                  for _ in range(layers)]
+        requests.append(ReuseRequest(block_table=bt.to(dev), donor_kvs=donors,
+                                     donor_positions=dpos.to(torch.int32).to(dev),
+                                     target_positions=t.to(torch.int32).to(dev),
+                                     compute_positions=pos_r.to(dev)))
+    return caches, requests, LLAMA["theta"]
 
 
 def build_inputs(dev: torch.device):

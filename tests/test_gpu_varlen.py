@@ -96,3 +96,36 @@ def test_varlen_rejects_bad_plans(dev):
         tk.partial_prefill_attention_paged_varlen(
             q.to(dev), kv.to(dev), tables.to(dev), torch.cat(pos).to(dev), [4, 4],
             [nblk[0], tables.shape[1] + 1])
+
+
+def test_kv_reuse_batch_llama_shape(dev):
+    """A reduced Llama-3-8B batch (2 layers; contexts 1K..4K; 10-30% recompute): RoPE
+    scatter of every request into the shared caches, then batched attention per layer, each
+    checked against the oracle on that request alone."""
+    import bench
+    from semblend_amd.batch import KVReuseBatch
+    from tests.helpers import assert_rope_close
+
+    caches, reqs, theta = bench.llama_batch(dev, layers=2, ctx=(1024, 2048, 3072, 4096),
+                                            pool_blocks=700, max_delta=1000, seed=7)
+    before = [c.cpu() for c in caches]
+    batch = KVReuseBatch(caches, reqs, rope_base=theta)
+    batch.scatter_rope()
+    for layer in range(2):
+        want = before[layer].clone()
+        for r in reqs:
+            ref.rope_correct_scatter_paged(want, r.donor_kvs[layer].cpu(), r.block_table.cpu(),
+                                           r.donor_positions.cpu(), r.target_positions.cpu(),
+                                           rope_base=theta)
+        got = caches[layer].cpu()
+        assert torch.equal(got[:, 1].view(torch.int16), want[:, 1].view(torch.int16))
+        assert_rope_close(got[:, 0], want[:, 0])
+    q = randn((batch.num_rows, 32, 128), torch.bfloat16, 150).to(dev)
+    for layer in range(2):
+        out = batch.attention(layer, q)
+        kv = caches[layer].cpu()
+        for i, r in enumerate(reqs):
+            a, b = batch.row_offsets[i], batch.row_offsets[i + 1]
+            want = ref.partial_attention_paged(q[a:b].cpu(), kv, r.block_table.cpu(),
+                                               r.compute_positions.cpu())
+            assert_attn_close(out[a:b], want)
