@@ -25,7 +25,7 @@ pass brackets each library kernel launch with HIP events inside the library (``k
 baseline times the oracle (a restatement of the reference's CPU path, with its per-pair
 loops) on the whole workload on the host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline] [--no-llama-batch]
 """
 
 from __future__ import annotations
@@ -54,9 +54,9 @@ KERNELS = ("attn_mfma", "attn_merge", "move_rows", "rope_rows", "rope_index", "f
 # this script, scaled by what the same counters read for the 1 GiB copy of copy_ceiling()
 # (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); kernel changes call for a new measurement.
 MEASURED_TRAFFIC_BYTES = {
-    "attn_mfma": (2 * 66209 + 43788) * 1024,
-    "move_rows": (2 * 390420 + 779860) * 1024,
-    "rope_rows": (2 * 114899 + 229379) * 1024,
+    "attn_mfma": (2 * 69196 + 43829) * 1024,
+    "move_rows": (2 * 390462 + 779859) * 1024,
+    "rope_rows": (2 * 114938 + 229392) * 1024,
 }
 
 
@@ -236,6 +236,98 @@ def cpu_baseline(inp) -> dict:
     return out
 
 
+def llama_batch_section(dev: torch.device, steps: int, cpu: bool) -> dict:
+    """The Llama-3-8B batch (four requests, 8K-32K contexts, 10-30% recompute, 32 layers):
+    RoPE scatter of every request into every layer's cache, then batched attention of all
+    requests layer by layer. Reported beside the headline workload."""
+    from semblend_amd import _lib
+    from semblend_amd.batch import KVReuseBatch
+
+    caches, reqs, theta = llama_batch(dev)
+    batch = KVReuseBatch(caches, reqs, rope_base=theta)
+    layers, hq, hkv, d = LLAMA["layers"], LLAMA["hq"], LLAMA["hkv"], LLAMA["d"]
+    gd = torch.Generator(dev).manual_seed(5)
+    q = torch.randn((batch.num_rows, hq, d), generator=gd, device=dev, dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+    pairs = sum(int(r.donor_positions.shape[0]) for r in reqs)
+    moved = float(pairs) * layers * 2 * hkv * d * 2 * 2
+    sum_p1 = sum(float((r.compute_positions.double() + 1).sum().cpu()) for r in reqs)
+    flops = 4.0 * d * hq * sum_p1 * layers
+
+    def step():
+        batch.scatter_rope()
+        for layer in range(layers):
+            batch.attention(layer, q, out=out)
+
+    step()
+    torch.cuda.synchronize()
+    _lib.kernel_timing(True)
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    t_sr, t_at = [], []
+    for _ in range(steps):
+        e[0].record()
+        batch.scatter_rope()
+        e[1].record()
+        for layer in range(layers):
+            batch.attention(layer, q, out=out)
+        e[2].record()
+        torch.cuda.synchronize()
+        t_sr.append(e[0].elapsed_time(e[1]))
+        t_at.append(e[1].elapsed_time(e[2]))
+    _lib.kernel_timing(False)
+    mfma_ms, n = _lib.kernel_time("attn_mfma")
+    sr_ms = sum(t_sr) / len(t_sr)
+    at_ms = sum(t_at) / len(t_at)
+    res = {
+        "workload": "Llama-3-8B KV reuse batch: 32 layers, 32q/8kv x 128, bf16, theta 5e5; "
+                    "requests of 8192/16384/24576/32768 tokens with 10/15/20/30% recompute "
+                    "(chunk-constant deltas in [-4096, 4096]); shared pool of 8192 blocks of 16",
+        "requests": len(reqs),
+        "rows": batch.num_rows,
+        "pairs": pairs,
+        "steps": steps,
+        "scatter_rope": {"ms": round(sr_ms, 4), "bytes": moved,
+                         "gbps": round(moved / (sr_ms * 1e-3) / 1e9, 1),
+                         "frac_of_peak": round(moved / (sr_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "attention": {"ms": round(at_ms, 4), "flops": flops,
+                      "tflops": round(flops / (at_ms * 1e-3) / 1e12, 2),
+                      "frac_of_peak": round(flops / (at_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                      "mfma_kernel_ms": round(mfma_ms / max(steps, 1), 4)},
+        "ms_per_step": round(sr_ms + at_ms, 4),
+    }
+    if cpu:
+        # Oracle on layer 0 of the largest request: 64 recompute rows and 512 reuse pairs.
+        from oracle import ref_cpu as ref
+
+        r = reqs[-1]
+        g = torch.Generator("cpu").manual_seed(6)
+        rows = torch.randperm(r.compute_positions.shape[0], generator=g)[:64].sort().values
+        pos = r.compute_positions.cpu()[rows]
+        kv = caches[0].cpu()
+        bt = r.block_table.cpu()
+        a0 = batch.row_offsets[len(reqs) - 1]
+        qs = q[a0:a0 + r.compute_positions.shape[0]].cpu()[rows]
+        t0 = time.perf_counter()
+        ref.partial_attention_paged(qs, kv, bt, pos)
+        dt_a = time.perf_counter() - t0
+        sel = torch.randperm(r.donor_positions.shape[0], generator=g)[:512]
+        dk = r.donor_kvs[0].cpu()
+        t0 = time.perf_counter()
+        ref.rope_correct_scatter_paged(kv, dk, bt, r.donor_positions.cpu()[sel],
+                                       r.target_positions.cpu()[sel], rope_base=theta)
+        dt_s = time.perf_counter() - t0
+        res["cpu_baseline"] = {
+            "attention_tflops": 4.0 * d * hq * float((pos.double() + 1).sum()) / dt_a / 1e12,
+            "scatter_rope_gbps": 512 * 2 * hkv * d * 2 * 2 / dt_s / 1e9,
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"layer 0, largest request: 64 recompute rows ({dt_a:.2f} s) and 512 "
+                      f"reuse pairs ({dt_s:.2f} s); rates, not whole-batch times"}
+    del caches, reqs, batch
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
 def capture(fn) -> "torch.cuda.CUDAGraph":
     """One launch sequence of fn captured as a HIP graph (after an eager run on the capture
     stream, so that every cached device table already exists)."""
@@ -257,6 +349,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-llama-batch", action="store_true",
+                    help="skip the Llama-3-8B multi-request batch section")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -414,6 +508,16 @@ def main() -> int:
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle on host cores)")
         result["cpu_baseline"] = cpu_baseline(inp)
+    if not args.no_llama_batch:
+        log("Llama-3-8B batch section")
+        del inp, graphs
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        result["llama3_8b_batch"] = llama_batch_section(dev, 3, not args.no_cpu_baseline)
+        lb = result["llama3_8b_batch"]
+        log(f"llama batch: scatter+rope {lb['scatter_rope']['ms']:.2f} ms "
+            f"({lb['scatter_rope']['gbps']:.0f} GB/s), attention {lb['attention']['ms']:.2f} ms "
+            f"({lb['attention']['tflops']:.1f} TFLOP/s)")
     print(json.dumps(result), flush=True)
     return 0
 
