@@ -56,6 +56,9 @@ enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3 };
 #ifndef SB_SCATTER_LPG
 #define SB_SCATTER_LPG 2
 #endif
+#ifndef SB_ROPE_SCATTER_LPG
+#define SB_ROPE_SCATTER_LPG 8
+#endif
 constexpr int kThreads = SB_MOVE_THREADS;
 constexpr int kBatch = SB_MOVE_BATCH;      // pair movers: rows loaded before the first store
 constexpr int kRopeBatch = SB_ROPE_BATCH;  // row-centric RoPE: the same
@@ -573,10 +576,13 @@ RowSide side_index(void* base, int64_t num_heads, int64_t head_dim, int64_t es, 
   return s;
 }
 
-int layers_per_group_for(int64_t num_layers, int64_t num_pairs) {
+int layers_per_group_for(int64_t num_layers, int64_t num_pairs, bool rope) {
   // Enough grid.y slices to fill the chip when there are few pairs; otherwise walk several
-  // layers per thread so cos/sin and index work are amortised.
-  if (num_pairs >= 8192) return static_cast<int>(num_layers < SB_SCATTER_LPG ? num_layers : SB_SCATTER_LPG);
+  // layers per thread so index work (and, when rotating, the fp64 cos/sin) is amortised.
+  // Plain copies stay at short groups (more independent slices in flight); the rotating
+  // path computes cos/sin once per group, so longer groups pay for themselves there.
+  const int64_t lpg = rope ? SB_ROPE_SCATTER_LPG : SB_SCATTER_LPG;
+  if (num_pairs >= 8192) return static_cast<int>(num_layers < lpg ? num_layers : lpg);
   return 1;
 }
 
@@ -615,7 +621,7 @@ extern "C" int sb_scatter_donor_kv(void* target, const void* donor, const int32_
   a.num_pairs = num_pairs;
   a.num_heads = static_cast<int>(num_heads);
   a.num_layers = static_cast<int>(num_layers);
-  a.layers_per_group = layers_per_group_for(num_layers, num_pairs);
+  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, false);
   a.kv_first = 0;
   a.num_kv = 2;
   const int groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
@@ -666,7 +672,7 @@ static int paged_scatter_impl(const char* fn, void* kv_base, const uint64_t* kv_
   a.num_pairs = num_pairs;
   a.num_heads = static_cast<int>(num_heads);
   a.num_layers = static_cast<int>(num_layers);
-  a.layers_per_group = layers_per_group_for(num_layers, num_pairs);
+  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, rope);
   a.kv_first = 0;
   a.num_kv = 2;
   const int groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
