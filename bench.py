@@ -21,7 +21,9 @@ overhead stays out of the phase times; every phase is timed with HIP events on t
 its kernels run on and ``ms_per_step`` is the sum of the three phase times. A separate eager
 pass brackets each library kernel launch with HIP events inside the library (``kernels``);
 ``roofline`` prices the MFMA attention kernel's average launch against the bf16 peak.
-``phases.copy_ceiling`` is a plain 1 GiB device copy, the achievable HBM rate. The CPU
+``phases.copy_ceiling`` is a plain 1 GiB device copy, the achievable HBM rate.
+``rope_scatter`` times the scatter workload again with K rotated on the way (one donor, and
+a composite from four donors). The CPU
 baseline times the oracle (a restatement of the reference's CPU path, with its per-pair
 loops) on the whole workload on the host's cores.
 
@@ -328,6 +330,57 @@ def llama_batch_section(dev: torch.device, steps: int, cpu: bool) -> dict:
     return res
 
 
+def rope_scatter_section(dev: torch.device, inp, steps: int) -> dict:
+    """Fused RoPE scatter of the 28-layer scatter workload (same 13926 pairs and bytes), from
+    one donor (``rope_correct_scatter_paged_layers``) and as a composite from four donors
+    (each 256-token target chunk owned by a random one of four 16384-token donors,
+    ``composite_scatter_paged_layers``), K rotated by a per-chunk delta. Graph replays timed
+    with HIP events."""
+    from semblend_amd import rope_correction as rc
+    from semblend_amd.multi_donor import composite_scatter_paged_layers
+
+    g = torch.Generator("cpu").manual_seed(3)
+    gd = torch.Generator(dev).manual_seed(3)
+    n_donors = 4
+    donors = [inp["donors"]] + [
+        [torch.randn((2, HKV, CTX, D), generator=gd, device=dev, dtype=torch.bfloat16)
+         for _ in range(L)] for _ in range(n_donors - 1)]
+    owner = torch.randint(0, n_donors, (CTX // CHUNK,), generator=g)
+    didx = owner[inp["sc_t"].cpu().long() // CHUNK].to(torch.int32).to(dev)
+    n_pairs = inp["sc_d"].shape[0]
+    nbytes = float(n_pairs) * L * 2 * HKV * D * 2 * 2
+
+    def one_donor():
+        rc.rope_correct_scatter_paged_layers(inp["caches"], inp["donors"], inp["block_table"],
+                                             inp["sc_d"], inp["sc_t"], rope_base=ROPE_BASE)
+
+    def four_donors():
+        composite_scatter_paged_layers(inp["caches"], donors, inp["block_table"], didx,
+                                       inp["sc_d"], inp["sc_t"], rope=True, rope_base=ROPE_BASE)
+
+    out = {"pairs": int(n_pairs), "bytes": nbytes}
+    for name, fn in (("one_donor", one_donor), ("four_donors", four_donors)):
+        gr = capture(fn)
+        gr.replay()
+        torch.cuda.synchronize()
+        evs = []
+        for _ in range(steps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            gr.replay()
+            e1.record()
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        t = [a.elapsed_time(b) for a, b in evs]
+        avg = sum(t) / len(t)
+        out[name] = {"ms": round(avg, 4), "ms_median": round(sorted(t)[len(t) // 2], 4),
+                     "gbps": round(nbytes / (avg * 1e-3) / 1e9, 1),
+                     "frac_of_peak": round(nbytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del gr
+    return out
+
+
 def capture(fn) -> "torch.cuda.CUDAGraph":
     """One launch sequence of fn captured as a HIP graph (after an eager run on the capture
     stream, so that every cached device table already exists)."""
@@ -505,6 +558,11 @@ def main() -> int:
         },
         "kernels": kernels,
     }
+    log("fused RoPE scatter: one donor and four-donor composite")
+    result["rope_scatter"] = rope_scatter_section(dev, inp, args.steps)
+    rs = result["rope_scatter"]
+    log(f"rope scatter: one donor {rs['one_donor']['ms']:.3f} ms ({rs['one_donor']['gbps']:.0f} GB/s), "
+        f"four donors {rs['four_donors']['ms']:.3f} ms ({rs['four_donors']['gbps']:.0f} GB/s)")
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle on host cores)")
         result["cpu_baseline"] = cpu_baseline(inp)

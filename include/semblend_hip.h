@@ -112,6 +112,30 @@ int sb_rope_correct_scatter_paged_layers(const uint64_t* kv_layer_ptrs,
                                          int64_t num_blocks_per_seq, const int64_t* kv_strides,
                                          const int64_t* d_strides, int32_t dtype, void* stream);
 
+/* Composite (multi-donor) scatter over many layers in one pass: pair i moves the rows of
+ * donor donor_index[i] at position donor_pos[i] (K and V, every layer and head) to
+ * target_pos[i] of the paged caches, rotating K by (target_pos - donor_pos) when inv_freq
+ * is not NULL (plain copy when it is).
+ *   donor_layer_ptrs  device [num_donors * num_layers] base addresses (donor-major), each a
+ *                     [2, H, S_k, D] tensor, 16-byte aligned
+ *   donor_strides     host [num_donors * 4]: kv, head and sequence strides of donor k in
+ *                     elements, then its sequence length S_k
+ * Pairs whose donor index, donor position or target slot is out of range are skipped.
+ * Target positions must be distinct across all pairs (a composite plan gives each target
+ * position one donor); duplicates race. Donors are moved in launches of at most 16.
+ * No reference counterpart: the reference carries the per-position donor map
+ * (semblend_core/partial_attention.py:306-435, multi_donor_types.py:50-78) but loads and
+ * scatters one donor at a time (synapse_kv_connector/semblend_connector.py:1508-1701). */
+int sb_composite_scatter_paged_layers(const uint64_t* kv_layer_ptrs, int64_t num_layers,
+                                      const uint64_t* donor_layer_ptrs, int64_t num_donors,
+                                      const int64_t* donor_strides, const int32_t* donor_index,
+                                      const int32_t* donor_pos, const int32_t* target_pos,
+                                      const float* inv_freq, int64_t num_pairs,
+                                      int64_t num_heads, int64_t block_size, int64_t head_dim,
+                                      const int32_t* block_table, int64_t num_blocks_total,
+                                      int64_t num_blocks_per_seq, const int64_t* kv_strides,
+                                      int32_t dtype, void* stream);
+
 /* Flat RoPE correction over k [L, H, S, D] (k_strides[4]; pass L = 1 for [H, S, D]):
  * for each pair i in order, the row at donor position d_i is rotated by (t_i - d_i) and
  * rounded to dtype; rows hit by several pairs are rotated once per pair, in pair order.

@@ -33,6 +33,7 @@ import torch
 
 __all__ = [
     "apply_rope_delta_inplace",
+    "composite_scatter_paged",
     "gather_paged_kv",
     "inv_freq",
     "masked_qkv_projection",
@@ -136,6 +137,29 @@ def rope_correct_scatter_paged(kv_cache, donor_kv, block_table, donor_positions,
         kv_cache[pb, 1, :, off, :] = donor_kv[1, :, d, :]
         k = rotate_interleaved(donor_kv[0, :, d, :], torch.cos(theta), torch.sin(theta))
         kv_cache[pb, 0, :, off, :] = k.to(kv_cache.dtype)
+    return kv_cache
+
+
+def composite_scatter_paged(kv_cache, donor_kvs, block_table, donor_index, donor_positions,
+                            target_positions, rope=True, rope_base=10000.0):
+    """Multi-donor scatter as the reference composes it: the pairs are split by donor
+    (``MultiDonorPositionMapping.for_donor``, semblend_core/multi_donor_types.py:70-78) and
+    each donor's subset goes through the single-donor path, RoPE-corrected
+    (rope_correction.py:296-328) or a plain copy (triton_kernels.py:338-354), donor by donor
+    in index order. Pairs naming no donor in range are skipped."""
+    donor_index = torch.as_tensor(donor_index)
+    donor_positions = torch.as_tensor(donor_positions)
+    target_positions = torch.as_tensor(target_positions)
+    for k, donor_kv in enumerate(donor_kvs):
+        sel = donor_index == k
+        if not bool(sel.any()):
+            continue
+        if rope:
+            rope_correct_scatter_paged(kv_cache, donor_kv, block_table, donor_positions[sel],
+                                       target_positions[sel], rope_base=rope_base)
+        else:
+            scatter_donor_kv_paged(kv_cache, donor_kv, block_table, donor_positions[sel],
+                                   target_positions[sel])
     return kv_cache
 
 

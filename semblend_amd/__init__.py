@@ -8,6 +8,9 @@ Drop-in modules (same call surface as SemBlend's ``semblend_core`` modules):
 * :mod:`semblend_amd.partial_attention` — plan types and mask / pair builders;
 * :mod:`semblend_amd.pipeline`         — ``PositionMapping``.
 
+Extensions: :mod:`semblend_amd.batch` (several requests over one paged pool) and
+:mod:`semblend_amd.multi_donor` (composite scatter from several donors in one pass).
+
 The compute runs in hand-written HIP kernels (``libsemblend_hip.so``, C ABI in
 ``include/semblend_hip.h``) on torch's current stream. ``semblend_amd.compat.install()``
 aliases the modules under the ``semblend_core`` / ``synapse_kv_connector`` import paths.

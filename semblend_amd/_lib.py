@@ -42,6 +42,9 @@ SIGNATURES: dict[str, list] = {
     "sb_rope_correct_scatter_paged_layers": [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
                                              _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i32,
                                              _vp],
+    "sb_composite_scatter_paged_layers": [_vp, _i64, _vp, _i64, _i64p, _vp, _vp, _vp, _vp,
+                                          _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64p, _i32,
+                                          _vp],
     "sb_rope_correct_k": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p,
                           _i64p, _i32, _vp],
     "sb_apply_rope_delta_inplace": [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,

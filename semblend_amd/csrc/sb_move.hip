@@ -19,11 +19,13 @@
 // compiled with -ffp-contract=off so each product and sum rounds exactly like torch's CPU
 // elementwise ops.
 
+#include <algorithm>
+
 #include "sb_common.h"
 
 namespace sb {
 
-enum RowMode : int { ROW_FLAT_POS = 0, ROW_PAGED_POS = 1, ROW_INDEX = 2 };
+enum RowMode : int { ROW_FLAT_POS = 0, ROW_PAGED_POS = 1, ROW_INDEX = 2, ROW_DONOR_POS = 3 };
 enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3 };
 
 // Launch shape and access hints, tuned on MI355X for the 7B-shape workloads (28 layers x
@@ -74,8 +76,25 @@ struct RowSide {
   int64_t bound;           // FLAT_POS: sequence length
 };
 
+// Composite (multi-donor) sources: each pair names a donor; donor k's layer l starts at
+// layers[k * num_layers + l] and its rows are [2, H, S_k, D] under its own strides. The
+// strides of the launch's donors travel in the kernel arguments (at most kMaxDonors per
+// launch; the host launches once per group of donors).
+constexpr int kMaxDonors = 16;
+struct DonorSet {
+  const uint64_t* layers;  // device [num_donors, num_layers] table of base addresses
+  const int32_t* index;    // per-pair donor index
+  int first;               // donors [first, first + count) are moved by this launch
+  int count;
+  int64_t s_kv[kMaxDonors];    // byte strides of each donor of the launch
+  int64_t s_head[kMaxDonors];
+  int64_t s_seq[kMaxDonors];
+  int64_t bound[kMaxDonors];   // donor sequence length
+};
+
 struct MoveArgs {
   RowSide src, dst;
+  DonorSet donors;         // ROW_DONOR_POS sources only
   const int32_t* src_pos;  // per-pair source positions (FLAT_POS / PAGED_POS sources)
   const int32_t* dst_pos;  // per-pair destination positions
   const int32_t* repeat;   // ROT_CONST: rotations to apply per pair (nullptr = 1)
@@ -251,8 +270,19 @@ __global__ __launch_bounds__(kThreads) void move_rows_kernel(MoveArgs a) {
   const int l0 = static_cast<int>(blockIdx.y / a.num_kv) * a.layers_per_group;
   const int l1 = min(l0 + a.layers_per_group, a.num_layers);
 
+  RowSide src = a.src;
+  if (SRCM == ROW_DONOR_POS) {
+    const int dn = a.donors.index[i] - a.donors.first;
+    if (dn < 0 || dn >= a.donors.count) return;  // another launch's donor, or invalid
+    src.layers = a.donors.layers + static_cast<int64_t>(a.donors.first + dn) * a.num_layers;
+    src.s_kv = a.donors.s_kv[dn];
+    src.s_head = a.donors.s_head[dn];
+    src.s_row = a.donors.s_seq[dn];
+    src.bound = a.donors.bound[dn];
+  }
+  constexpr int SRC_RESOLVE = SRCM == ROW_DONOR_POS ? ROW_FLAT_POS : SRCM;
   int64_t src_off, dst_off;
-  if (!resolve_row<SRCM>(a, a.src, a.src_pos, i, &src_off)) return;
+  if (!resolve_row<SRC_RESOLVE>(a, src, a.src_pos, i, &src_off)) return;
   if (!resolve_row<DSTM>(a, a.dst, a.dst_pos, i, &dst_off)) return;
   if (SRCM == ROW_INDEX && a.src_index_check) {
     int64_t unused;
@@ -292,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void move_rows_kernel(MoveArgs a) {
 #pragma unroll
       for (int b = 0; b < kBatch; ++b)
         if (r0 + b < nrows)
-          load_vec<VB, SB_MOVE_NT_LOAD>(row_of(a.src, r0 + b) + src_off + vofs, w[b]);
+          load_vec<VB, SB_MOVE_NT_LOAD>(row_of(src, r0 + b) + src_off + vofs, w[b]);
 #pragma unroll
       for (int b = 0; b < kBatch; ++b) {
         if (r0 + b >= nrows) continue;
@@ -749,6 +779,84 @@ extern "C" int sb_rope_correct_scatter_paged_layers(
                             target_pos, inv_freq, num_pairs, num_heads, block_size, head_dim,
                             donor_seq_len, num_blocks_total, num_blocks_per_seq, kv_strides,
                             d_strides, dtype, true, stream);
+}
+
+// Composite (multi-donor) scatter over many layers: pair i moves donor
+// donor_index[i]'s rows at donor_pos[i] to target_pos[i] of every layer's paged cache,
+// rotating K by (target - donor) when inv_freq is given.
+extern "C" int sb_composite_scatter_paged_layers(
+    const uint64_t* kv_layer_ptrs, int64_t num_layers, const uint64_t* donor_layer_ptrs,
+    int64_t num_donors, const int64_t* donor_strides, const int32_t* donor_index,
+    const int32_t* donor_pos, const int32_t* target_pos, const float* inv_freq,
+    int64_t num_pairs, int64_t num_heads, int64_t block_size, int64_t head_dim,
+    const int32_t* block_table, int64_t num_blocks_total, int64_t num_blocks_per_seq,
+    const int64_t* kv_strides, int32_t dtype, void* stream) {
+  const char* fn = "sb_composite_scatter_paged_layers";
+  clear_error();
+  if (num_pairs == 0 || num_layers == 0 || num_heads == 0 || head_dim == 0 || num_donors == 0)
+    return SB_OK;
+  if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
+  if (!kv_layer_ptrs || !donor_layer_ptrs || !donor_strides || !donor_index || !donor_pos ||
+      !target_pos || !block_table || !kv_strides)
+    return fail(fn, "null pointer argument");
+  const bool rope = inv_freq != nullptr;
+  if (rope && (head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
+  if (block_size <= 0) return fail(fn, "block_size must be positive");
+  if (kv_strides[4] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
+  if (num_donors > 0x7fffffff || num_layers > 0x7fffffff)
+    return fail(fn, "too many donors or layers");
+  const int64_t es = elem_size(dtype);
+  // The donors' strides bound the vector width like the cache's do (layer tables are
+  // checked for 16-byte alignment by the caller).
+  int64_t donor_vb = 16;
+  for (int64_t k = 0; k < num_donors; ++k) {
+    const int64_t* d = donor_strides + 4 * k;
+    if (d[3] < 0) return fail(fn, "negative donor sequence length");
+    for (int t = 0; t < 3; ++t)
+      while (donor_vb > 1 && (d[t] * es) % donor_vb != 0) donor_vb >>= 1;
+  }
+  Geometry g;
+  if (!make_geometry(head_dim, es,
+                     {16, donor_vb, kv_strides[0] * es, kv_strides[1] * es, kv_strides[2] * es,
+                      kv_strides[3] * es},
+                     rope, &g))
+    return fail(fn, "rows are not aligned for vector access");
+  MoveArgs a{};
+  a.dst = side_paged(nullptr, kv_layer_ptrs, kv_strides, es);
+  a.donors.layers = donor_layer_ptrs;
+  a.donors.index = donor_index;
+  a.src_pos = donor_pos;
+  a.dst_pos = target_pos;
+  a.block_table = block_table;
+  a.block_size = block_size;
+  a.nb_total = num_blocks_total;
+  a.nb_per_seq = num_blocks_per_seq;
+  a.inv_freq = inv_freq;
+  a.num_pairs = num_pairs;
+  a.num_heads = static_cast<int>(num_heads);
+  a.num_layers = static_cast<int>(num_layers);
+  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, rope);
+  a.kv_first = 0;
+  a.num_kv = 2;
+  const int groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  for (int64_t first = 0; first < num_donors; first += kMaxDonors) {
+    const int count = static_cast<int>(std::min<int64_t>(kMaxDonors, num_donors - first));
+    a.donors.first = static_cast<int>(first);
+    a.donors.count = count;
+    for (int k = 0; k < count; ++k) {
+      const int64_t* d = donor_strides + 4 * (first + k);
+      a.donors.s_kv[k] = d[0] * es;
+      a.donors.s_head[k] = d[1] * es;
+      a.donors.s_seq[k] = d[2] * es;
+      a.donors.bound[k] = d[3];
+    }
+    const int rc =
+        rope ? launch_move<ROT_DELTA, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, 2 * groups, st)
+             : launch_move<ROT_NONE, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, 2 * groups, st);
+    if (rc) return rc;
+  }
+  return SB_OK;
 }
 
 extern "C" int sb_rope_correct_k(void* out, const void* k, const int32_t* donor_pos,

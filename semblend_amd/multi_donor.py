@@ -1,0 +1,208 @@
+"""Multi-donor (composite) KV scatter on MI355X.
+
+A composite plan fills one target sequence from several donors: every reused target position
+names the donor that owns its KV and the position inside that donor
+(``MultiDonorPositionMapping``, semblend_core/multi_donor_types.py:50-78; the per-position
+``donor_map`` of ``build_multi_donor_attention_plan``, semblend_core/partial_attention.py:
+306-435). The reference loads and scatters one donor at a time
+(synapse_kv_connector/semblend_connector.py:1508-1701). Here one pass moves every pair of
+every donor, all layers and heads, through a per-pair donor index and a per-donor table of
+layer base addresses and strides (``sb_composite_scatter_paged_layers``), rotating K by
+``target - donor`` as ``rope_correct_scatter_paged`` does.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Mapping, Sequence
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from .partial_attention import PartialAttentionPlan, compute_donor_kv_indices
+from .rope_correction import inv_freq_table
+
+__all__ = [
+    "MultiDonorPositionMapping",
+    "composite_pairs",
+    "composite_pairs_from_plan",
+    "composite_scatter_paged",
+    "composite_scatter_paged_layers",
+]
+
+
+@dataclass(frozen=True)
+class MultiDonorPositionMapping:
+    """Donor-aware position mapping (semblend_core/multi_donor_types.py:50-78): entry i maps
+    target position ``target_positions[i]`` to ``donor_positions[i]`` of donor
+    ``donor_ids[i]``; RoPE correction rotates by ``target - donor`` per entry."""
+
+    donor_ids: tuple[str, ...] = ()
+    donor_positions: tuple[int, ...] = ()
+    target_positions: tuple[int, ...] = ()
+
+    @property
+    def num_pairs(self) -> int:
+        return len(self.target_positions)
+
+    @property
+    def needs_correction(self) -> bool:
+        return any(d != t for d, t in zip(self.donor_positions, self.target_positions))
+
+    def for_donor(self, donor_id: str) -> "MultiDonorPositionMapping":
+        """The entries of one donor, in their original order."""
+        keep = [i for i, did in enumerate(self.donor_ids) if did == donor_id]
+        return MultiDonorPositionMapping(
+            donor_ids=tuple(self.donor_ids[i] for i in keep),
+            donor_positions=tuple(self.donor_positions[i] for i in keep),
+            target_positions=tuple(self.target_positions[i] for i in keep),
+        )
+
+
+def composite_pairs(mapping: MultiDonorPositionMapping,
+                    donor_order: Sequence[str] | None = None):
+    """Flatten a mapping into the arrays the composite scatter takes.
+
+    Returns ``(donor_order, donor_index, donor_positions, target_positions)``: the donors in
+    the order their KV tensors must be passed (first appearance, unless ``donor_order`` is
+    given) and int32 arrays with ``donor_index[i]`` indexing that order. Target positions
+    must be distinct (each target has one owner); duplicates raise ``ValueError``, as do ids
+    missing from ``donor_order``.
+    """
+    n = mapping.num_pairs
+    if len(mapping.donor_ids) != n or len(mapping.donor_positions) != n:
+        raise ValueError("donor_ids, donor_positions and target_positions differ in length")
+    if donor_order is None:
+        donor_order = tuple(dict.fromkeys(mapping.donor_ids))
+    slot = {did: k for k, did in enumerate(donor_order)}
+    missing = set(mapping.donor_ids) - slot.keys()
+    if missing:
+        raise ValueError(f"donor ids not in donor_order: {sorted(missing)}")
+    tpos = np.asarray(mapping.target_positions, dtype=np.int64)
+    if np.unique(tpos).size != tpos.size:
+        raise ValueError("target positions must be distinct across donors")
+    didx = np.fromiter((slot[d] for d in mapping.donor_ids), dtype=np.int32, count=n)
+    return (tuple(donor_order), didx, np.asarray(mapping.donor_positions, dtype=np.int32),
+            tpos.astype(np.int32))
+
+
+def composite_pairs_from_plan(plan: PartialAttentionPlan, layer_idx: int = 0):
+    """The reuse pairs of one layer of a multi-donor plan with each pair's owner taken from
+    ``plan.donor_map`` (positions absent from it belong to ``plan.donor_id``, the primary
+    donor; partial_attention.py:405-413)."""
+    owner = dict(plan.donor_map)
+    pairs = compute_donor_kv_indices(plan, layer_idx)
+    return MultiDonorPositionMapping(
+        donor_ids=tuple(owner.get(t, plan.donor_id) for _, t in pairs),
+        donor_positions=tuple(d for d, _ in pairs),
+        target_positions=tuple(t for _, t in pairs),
+    )
+
+
+def composite_scatter_paged_layers(
+    kv_caches: list[torch.Tensor],
+    donor_kvs: Sequence[Sequence[torch.Tensor]],
+    block_table: torch.Tensor,
+    donor_index,
+    donor_positions,
+    target_positions,
+    rope: bool = True,
+    rope_base: float = 10000.0,
+) -> list[torch.Tensor]:
+    """Scatter pairs from several donors into every layer's paged cache in one pass.
+
+    kv_caches: per layer ``[num_blocks, 2, H, block_size, D]``, one shape/stride/dtype.
+    donor_kvs: per donor, per layer ``[2, H, S_k, D]`` (``donor_kvs[k][l]``); a donor's
+        layers share shape and strides, donors may differ in length ``S_k`` and strides.
+    donor_index / donor_positions / target_positions: per pair (int32 tensors or sequences).
+    Pair i moves donor ``donor_index[i]``'s K and V at ``donor_positions[i]`` to
+    ``target_positions[i]``; K is rotated by ``target - donor`` when ``rope``. Pairs whose
+    donor index, donor position or target slot is out of range are skipped. Target positions
+    must be distinct (the kernel does not order writes to one slot).
+    """
+    num_pairs = len(target_positions)
+    if num_pairs == 0 or not kv_caches or not donor_kvs:
+        return kv_caches
+    num_layers = len(kv_caches)
+    ref = kv_caches[0]
+    nb_total, _, num_heads, block_size, head_dim = ref.shape
+    dev = _lib.require_device(*kv_caches, *(t for per in donor_kvs for t in per))
+    _check_same(kv_caches, "kv_caches")
+    strides = []
+    for k, per_layer in enumerate(donor_kvs):
+        if len(per_layer) != num_layers:
+            raise ValueError(f"donor {k} has {len(per_layer)} layers, the cache {num_layers}")
+        _check_same(per_layer, f"donor {k} layers")
+        d0 = per_layer[0]
+        if d0.dim() != 4 or d0.shape[0] != 2 or d0.shape[1] != num_heads or d0.shape[3] != head_dim:
+            raise ValueError(f"donor {k} must be [2, {num_heads}, S, {head_dim}]")
+        if d0.dtype != ref.dtype:
+            raise TypeError("donors and caches must share a dtype")
+        if d0.stride(3) != 1:
+            raise ValueError("donor head_dim must be contiguous (stride 1)")
+        strides += [d0.stride(0), d0.stride(1), d0.stride(2), d0.shape[2]]
+    if rope and head_dim % 2:
+        raise ValueError("head_dim must be even for RoPE")
+    kv_tab = _lib.address_table(kv_caches, dev)
+    d_tab = _lib.address_table([t for per in donor_kvs for t in per], dev)
+    bt = _lib.as_index(block_table, dev)
+    didx = _lib.as_index(_as_tensor(donor_index), dev)
+    dpos = _lib.as_index(_as_tensor(donor_positions), dev)
+    tpos = _lib.as_index(_as_tensor(target_positions), dev)
+    if not (didx.shape[0] == dpos.shape[0] == tpos.shape[0]):
+        raise ValueError("donor_index, donor_positions and target_positions differ in length")
+    inv_freq = inv_freq_table(rope_base, head_dim, dev) if rope else None
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_composite_scatter_paged_layers",
+            kv_tab.data_ptr(), num_layers, d_tab.data_ptr(), len(donor_kvs),
+            _lib.i64_array(strides), didx.data_ptr(), dpos.data_ptr(), tpos.data_ptr(),
+            inv_freq.data_ptr() if inv_freq is not None else None, num_pairs, num_heads,
+            block_size, head_dim, bt.data_ptr(), nb_total, bt.shape[0], _lib.strides(ref),
+            _lib.dtype_code(ref), _lib.stream_handle(dev),
+        )
+    return kv_caches
+
+
+def composite_scatter_paged(
+    kv_cache: torch.Tensor,
+    donor_kvs: Mapping[str, torch.Tensor] | Sequence[torch.Tensor],
+    block_table: torch.Tensor,
+    mapping: MultiDonorPositionMapping,
+    rope_base: float = 10000.0,
+    rope: bool | None = None,
+) -> torch.Tensor:
+    """One layer from a ``MultiDonorPositionMapping``: ``donor_kvs`` maps donor id to its
+    ``[2, H, S, D]`` KV (or is a sequence in the mapping's first-appearance order). RoPE is
+    applied when ``rope`` is True, or, by default, when the mapping needs correction."""
+    if mapping.num_pairs == 0:
+        return kv_cache
+    if isinstance(donor_kvs, Mapping):
+        order, didx, dpos, tpos = composite_pairs(mapping, tuple(donor_kvs.keys()))
+        tensors = [donor_kvs[d] for d in order]
+    else:
+        order, didx, dpos, tpos = composite_pairs(mapping)
+        if len(donor_kvs) != len(order):
+            raise ValueError(f"{len(order)} donors in the mapping, {len(donor_kvs)} tensors")
+        tensors = list(donor_kvs)
+    if rope is None:
+        rope = mapping.needs_correction
+    composite_scatter_paged_layers([kv_cache], [[t] for t in tensors], block_table, didx, dpos,
+                                   tpos, rope=rope, rope_base=rope_base)
+    return kv_cache
+
+
+def _as_tensor(x) -> torch.Tensor:
+    if isinstance(x, torch.Tensor):
+        return x
+    return torch.as_tensor(np.asarray(x, dtype=np.int32))
+
+
+def _check_same(ts: Sequence[torch.Tensor], name: str) -> None:
+    t0 = ts[0]
+    for t in ts:
+        if t.shape != t0.shape or t.stride() != t0.stride() or t.dtype != t0.dtype:
+            raise ValueError(f"all {name} must share shape, strides and dtype")
+        if t.data_ptr() % 16:
+            raise ValueError(f"{name} base addresses must be 16-byte aligned")

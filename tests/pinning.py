@@ -397,6 +397,66 @@ def check_projection_and_prefill(impl) -> None:
     assert torch.all(out[~cm] == 0)
 
 
+
+# ------------------------------------------------------------------------------------------
+# Multi-donor (composite) scatter: concatenation identities
+# ------------------------------------------------------------------------------------------
+
+def _composite_case(dtype, lens, seed, n_pairs=40):
+    """Donors of the given lengths, distinct targets over a permuted block table, pairs
+    spread over the donors plus pairs that must be skipped (unknown donor ids, donor
+    positions past their donor's end)."""
+    bs, nb, h, d = 4, 16, 2, 16
+    g = _gen(seed)
+    donors = [_randn((2, h, n, d), seed + 1 + k, dtype) for k, n in enumerate(lens)]
+    tpos = torch.randperm(nb * bs, generator=g)[:n_pairs]
+    didx = torch.randint(0, len(lens), (n_pairs,), generator=g)
+    dpos = torch.tensor([int(torch.randint(0, lens[k], (1,), generator=g)) for k in didx])
+    bad = torch.randperm(nb * bs, generator=g)
+    bad = bad[~torch.isin(bad, tpos)][:3]
+    bad_idx = torch.tensor([len(lens), -1, 0])
+    bad_pos = torch.tensor([0, 0, lens[0]])
+    bt = torch.randperm(nb + 5, generator=g)[:nb].to(torch.int32)
+    cache = _randn((nb + 5, 2, h, bs, d), seed + 20, dtype)
+    return (donors, bt, cache, didx, dpos, tpos, torch.cat([didx, bad_idx]),
+            torch.cat([dpos, bad_pos]), torch.cat([tpos, bad]))
+
+
+def check_composite_concatenation(impl) -> None:
+    """Plain copies: a composite scatter from donors A, B, C equals one single-donor scatter
+    from cat(A, B, C) along the sequence, each pair's donor position shifted by its donor's
+    offset in the concatenation (ragged donor lengths; skipped pairs left out)."""
+    for dtype in (torch.float32, torch.bfloat16):
+        lens = [64, 20, 12]
+        donors, bt, cache, didx, dpos, tpos, cidx, cdpos, ctpos = _composite_case(dtype, lens, 50)
+        offs = torch.tensor([0, 64, 84])
+        want = impl.scatter_donor_kv_paged(cache.clone(), torch.cat(donors, dim=2), bt,
+                                           dpos + offs[didx], tpos)
+        got = impl.composite_scatter_paged(cache.clone(), donors, bt, cidx, cdpos, ctpos,
+                                           rope=False)
+        assert torch.equal(got, want)
+
+
+def check_composite_rope_concatenation(impl) -> None:
+    """RoPE: the same identity with targets shifted as well, so every delta t - d is kept;
+    the block table is repeated once per donor and every donor but the last spans exactly
+    one table (64 positions), so a shifted target names the same physical slot."""
+    for dtype in (torch.float32, torch.bfloat16):
+        lens = [64, 64, 12]
+        donors, bt, cache, didx, dpos, tpos, cidx, cdpos, ctpos = _composite_case(dtype, lens, 60)
+        offs = torch.tensor([0, 64, 128])
+        want = impl.rope_correct_scatter_paged(cache.clone(), torch.cat(donors, dim=2),
+                                               bt.repeat(3), dpos + offs[didx],
+                                               tpos + offs[didx], rope_base=500.0)
+        got = impl.composite_scatter_paged(cache.clone(), donors, bt, cidx, cdpos, ctpos,
+                                           rope=True, rope_base=500.0)
+        assert torch.equal(got, want)
+        # and the rotation is not a copy: K differs from the plain composite somewhere
+        plain = impl.composite_scatter_paged(cache.clone(), donors, bt, cidx, cdpos, ctpos,
+                                             rope=False)
+        assert torch.equal(got[:, 1], plain[:, 1]) and not torch.equal(got[:, 0], plain[:, 0])
+
+
 ALL_CHECKS = [
     check_rope_reference_cases,
     check_rope_paged_reference_cases,
@@ -411,4 +471,6 @@ ALL_CHECKS = [
     check_attention_golden,
     check_gqa_matches_dense,
     check_projection_and_prefill,
+    check_composite_concatenation,
+    check_composite_rope_concatenation,
 ]

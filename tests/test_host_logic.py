@@ -104,6 +104,56 @@ def test_multi_donor_plan():
     assert empty.donor_id == "" and empty.computation_ratio == 1.0
 
 
+def test_multi_donor_position_mapping():
+    # the reference suite's cases (tests/core/test_multi_donor_types.py:69-123), restated
+    from semblend_amd.multi_donor import MultiDonorPositionMapping as M
+    m = M(donor_ids=("d1", "d2"), donor_positions=(0, 256), target_positions=(0, 256))
+    with pytest.raises(AttributeError):
+        m.donor_ids = ()  # type: ignore[misc]
+    assert M(("d1", "d1", "d2"), (0, 1, 100), (0, 1, 200)).num_pairs == 3
+    assert not M(("d1",), (5,), (5,)).needs_correction
+    assert M(("d1",), (5,), (10,)).needs_correction
+    d1 = M(("d1", "d2", "d1", "d2"), (0, 100, 1, 101), (0, 200, 1, 201)).for_donor("d1")
+    assert (d1.num_pairs, d1.donor_ids, d1.donor_positions, d1.target_positions) == \
+        (2, ("d1", "d1"), (0, 1), (0, 1))
+    assert M().num_pairs == 0 and not M().needs_correction
+
+
+def test_composite_pairs():
+    from semblend_amd.multi_donor import MultiDonorPositionMapping as M, composite_pairs
+    m = M(("b", "a", "b", "c"), (7, 3, 8, 0), (10, 11, 12, 13))
+    order, didx, dpos, tpos = composite_pairs(m)
+    assert order == ("b", "a", "c")
+    np.testing.assert_array_equal(didx, [0, 1, 0, 2])
+    np.testing.assert_array_equal(dpos, [7, 3, 8, 0])
+    np.testing.assert_array_equal(tpos, [10, 11, 12, 13])
+    assert didx.dtype == np.int32 and dpos.dtype == np.int32 and tpos.dtype == np.int32
+    order, didx, _, _ = composite_pairs(m, ("c", "b", "a"))
+    np.testing.assert_array_equal(didx, [1, 2, 1, 0])
+    with pytest.raises(ValueError, match="not in donor_order"):
+        composite_pairs(m, ("a", "b"))
+    with pytest.raises(ValueError, match="distinct"):
+        composite_pairs(M(("a", "b"), (0, 1), (5, 5)))
+    with pytest.raises(ValueError, match="length"):
+        composite_pairs(M(("a",), (0, 1), (5, 6)))
+
+
+def test_composite_pairs_from_plan():
+    from semblend_amd.multi_donor import composite_pairs_from_plan
+    acts = [{"action": COPY, "targetPos": 0, "donorPos": 4, "donorId": "a"},
+            {"action": COPY, "targetPos": 1, "donorPos": 9, "donorId": "b"},
+            {"action": COPY, "targetPos": 2, "donorPos": 5},
+            {"action": "recompute", "targetPos": 3}]
+    plan = pa.build_multi_donor_attention_plan(4, acts, num_layers=2)
+    m = composite_pairs_from_plan(plan, 1)
+    # position 2 has no donorId: it belongs to the plan's primary donor ("a": tie -> first)
+    assert m.donor_ids == ("a", "b", plan.donor_id)
+    assert m.donor_positions == (4, 9, 5) and m.target_positions == (0, 1, 2)
+    full = pa.build_multi_donor_attention_plan(
+        4, acts, layer_hints=[{"recomputeAll": True}], num_layers=2)
+    assert composite_pairs_from_plan(full, 0).num_pairs == 0
+
+
 def test_plan_types_frozen_and_enum_values():
     m = pa.PositionMask(target_pos=0, mode=pa.AttentionMode.REUSE, donor_pos=3)
     assert m.donor_pos == 3

@@ -19,7 +19,7 @@ from oracle import ref_cpu as ref
 from tests import pinning
 
 API = [
-    "apply_rope_delta_inplace", "masked_qkv_projection", "nope_permute_paged_kv",
+    "apply_rope_delta_inplace", "composite_scatter_paged", "masked_qkv_projection", "nope_permute_paged_kv",
     "partial_attention_paged", "partial_prefill", "partial_prefill_attention",
     "permute_paged_kv_with_rope", "rope_correct_k", "rope_correct_scatter_paged",
     "scatter_donor_kv", "scatter_donor_kv_paged",
@@ -138,6 +138,27 @@ def _nope_snapshot_v(kv_cache, block_table, permutation, rope_base=10000.0):
         kv_cache[int(block_table[t // bs]), 1, :, t % bs] = v
 
 
+
+def _composite_donor_ignored(kv_cache, donor_kvs, block_table, didx, dpos, tpos, rope=True,
+                             rope_base=10000.0):
+    # every pair read from the first donor
+    valid = (torch.as_tensor(didx) >= 0) & (torch.as_tensor(didx) < len(donor_kvs))
+    return ref.composite_scatter_paged(kv_cache, donor_kvs[:1], block_table,
+                                       torch.where(valid, 0, -1), dpos, tpos, rope, rope_base)
+
+
+def _composite_last_donor_dropped(kv_cache, donor_kvs, block_table, didx, dpos, tpos,
+                                  rope=True, rope_base=10000.0):
+    return ref.composite_scatter_paged(kv_cache, donor_kvs[:-1], block_table, didx, dpos, tpos,
+                                       rope, rope_base)
+
+
+def _composite_rope_dropped(kv_cache, donor_kvs, block_table, didx, dpos, tpos, rope=True,
+                            rope_base=10000.0):
+    return ref.composite_scatter_paged(kv_cache, donor_kvs, block_table, didx, dpos, tpos, False,
+                                       rope_base)
+
+
 FUNCTION_MUTANTS = {
     "rope_delta_reversed": {"rope_correct_k": _rope_k_delta_reversed},
     "attention_causal_off_by_one": {"partial_prefill_attention": _attn_off_by_one},
@@ -146,6 +167,9 @@ FUNCTION_MUTANTS = {
     "paged_scatter_ignores_block_table": {"scatter_donor_kv_paged": _paged_scatter_ignores_table},
     "scatter_pair_roles_swapped": {"scatter_donor_kv": _scatter_swapped},
     "nope_v_snapshot_instead_of_sequential": {"nope_permute_paged_kv": _nope_snapshot_v},
+    "composite_donor_index_ignored": {"composite_scatter_paged": _composite_donor_ignored},
+    "composite_last_donor_dropped": {"composite_scatter_paged": _composite_last_donor_dropped},
+    "composite_rope_dropped": {"composite_scatter_paged": _composite_rope_dropped},
 }
 
 
