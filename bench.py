@@ -23,7 +23,8 @@ pass brackets each library kernel launch with HIP events inside the library (``k
 ``roofline`` prices the MFMA attention kernel's average launch against the bf16 peak.
 ``phases.copy_ceiling`` is a plain 1 GiB device copy, the achievable HBM rate.
 ``rope_scatter`` times the scatter workload again with K rotated on the way (one donor, and
-a composite from four donors). The CPU
+a composite from four donors); ``chunk_load`` streams the same donor from pinned host memory
+in 256-token chunks with the RoPE scatter overlapped. The CPU
 baseline times the oracle (a restatement of the reference's CPU path, with its per-pair
 loops) on the whole workload on the host's cores.
 
@@ -381,6 +382,71 @@ def rope_scatter_section(dev: torch.device, inp, steps: int) -> dict:
     return out
 
 
+def chunk_load_section(dev: torch.device, inp, steps: int) -> dict:
+    """The donor of the scatter workload (16384 tokens x 28 layers, 939.5 MB) held in host
+    memory as 64 LMCache chunks [2, 28, 256, 512] (pinned), loaded into the paged caches
+    with RoPE on the way (13926 pairs, per-chunk delta). Three schedules, each timed with
+    HIP events on the current stream: the copies alone (the PCIe ceiling), copy-then-scatter
+    on one stream (no overlap), and ChunkedKVLoader (8 staging slots; scatters on their own
+    stream, overlapped with the copies)."""
+    from semblend_amd.loader import ChunkedKVLoader, group_pairs_by_chunk
+    from semblend_amd.multi_donor import composite_scatter_paged_layers
+
+    T = CHUNK
+    n_chunks = CTX // T
+    chunks = []
+    for c in range(n_chunks):
+        x = torch.stack([dn[:, :, c * T:(c + 1) * T].permute(0, 2, 1, 3) for dn in inp["donors"]],
+                        dim=1).reshape(2, L, T, HKV * D)
+        h = torch.empty(x.shape, dtype=x.dtype, pin_memory=True)
+        h.copy_(x)
+        chunks.append(h)
+    host_bytes = float(sum(h.numel() * h.element_size() for h in chunks))
+    dpos = inp["sc_d"].cpu().numpy()
+    tpos = inp["sc_t"].cpu().numpy()
+    loader = ChunkedKVLoader(inp["caches"], inp["block_table"], chunk_tokens=T, slots=8,
+                             rope_base=ROPE_BASE)
+    arr, offs = group_pairs_by_chunk(dpos, tpos, T, n_chunks)
+    pairs = torch.from_numpy(arr).to(dev)
+    staging = torch.empty((2, L, T, HKV, D), dtype=torch.bfloat16, device=dev)
+
+    def copies_only():
+        for h in chunks:
+            staging.copy_(h.view(2, L, T, HKV, D), non_blocking=True)
+
+    def serial():
+        for c, h in enumerate(chunks):
+            staging.copy_(h.view(2, L, T, HKV, D), non_blocking=True)
+            lo, hi = int(offs[c]), int(offs[c + 1])
+            composite_scatter_paged_layers(
+                inp["caches"], [[staging[:, l].permute(0, 2, 1, 3) for l in range(L)]],
+                inp["block_table"], pairs[2, lo:hi], pairs[0, lo:hi], pairs[1, lo:hi],
+                rope=True, rope_base=ROPE_BASE, donor_first_positions=[c * T])
+
+    def streamed():
+        loader.load(chunks, dpos, tpos, rope=True)
+
+    out = {"chunks": n_chunks, "chunk_shape": [2, L, T, HKV * D], "host_bytes": host_bytes,
+           "pairs": int(len(dpos))}
+    for name, fn in (("copies_only", copies_only), ("serial", serial), ("streamed", streamed)):
+        fn()
+        torch.cuda.synchronize()
+        t = []
+        for _ in range(steps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            t.append(e0.elapsed_time(e1))
+        avg = sum(t) / len(t)
+        out[name] = {"ms": round(avg, 3), "host_gbps": round(host_bytes / (avg * 1e-3) / 1e9, 1)}
+    out["overlap_efficiency"] = round(out["copies_only"]["ms"] / out["streamed"]["ms"], 4)
+    del loader, chunks
+    return out
+
+
 def capture(fn) -> "torch.cuda.CUDAGraph":
     """One launch sequence of fn captured as a HIP graph (after an eager run on the capture
     stream, so that every cached device table already exists)."""
@@ -563,6 +629,12 @@ def main() -> int:
     rs = result["rope_scatter"]
     log(f"rope scatter: one donor {rs['one_donor']['ms']:.3f} ms ({rs['one_donor']['gbps']:.0f} GB/s), "
         f"four donors {rs['four_donors']['ms']:.3f} ms ({rs['four_donors']['gbps']:.0f} GB/s)")
+    log("chunked host-to-device donor load with RoPE on the way")
+    result["chunk_load"] = chunk_load_section(dev, inp, 5)
+    cl = result["chunk_load"]
+    log(f"chunk load: copies only {cl['copies_only']['ms']:.2f} ms "
+        f"({cl['copies_only']['host_gbps']:.1f} GB/s), serial {cl['serial']['ms']:.2f} ms, "
+        f"streamed {cl['streamed']['ms']:.2f} ms (overlap {cl['overlap_efficiency']:.3f})")
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle on host cores)")
         result["cpu_baseline"] = cpu_baseline(inp)

@@ -118,8 +118,11 @@ int sb_rope_correct_scatter_paged_layers(const uint64_t* kv_layer_ptrs,
  * is not NULL (plain copy when it is).
  *   donor_layer_ptrs  device [num_donors * num_layers] base addresses (donor-major), each a
  *                     [2, H, S_k, D] tensor, 16-byte aligned
- *   donor_strides     host [num_donors * 4]: kv, head and sequence strides of donor k in
- *                     elements, then its sequence length S_k
+ *   donor_strides     host [num_donors * 5]: kv, head and sequence strides of donor k in
+ *                     elements, the rows S_k its tensor holds, and the sequence position of
+ *                     its row 0 (0 for a whole donor; c * T for a staged chunk c): the pair
+ *                     reads row donor_pos[i] - first, and K is still rotated by
+ *                     target_pos[i] - donor_pos[i]
  * Pairs whose donor index, donor position or target slot is out of range are skipped.
  * Target positions must be distinct across all pairs (a composite plan gives each target
  * position one donor); duplicates race. Donors are moved in launches of at most 16.

@@ -89,7 +89,8 @@ struct DonorSet {
   int64_t s_kv[kMaxDonors];    // byte strides of each donor of the launch
   int64_t s_head[kMaxDonors];
   int64_t s_seq[kMaxDonors];
-  int64_t bound[kMaxDonors];   // donor sequence length
+  int64_t bound[kMaxDonors];   // rows held by each donor tensor
+  int64_t first_pos[kMaxDonors];  // sequence position of each donor tensor's row 0
 };
 
 struct MoveArgs {
@@ -271,18 +272,21 @@ __global__ __launch_bounds__(kThreads) void move_rows_kernel(MoveArgs a) {
   const int l1 = min(l0 + a.layers_per_group, a.num_layers);
 
   RowSide src = a.src;
+  int64_t src_off, dst_off;
   if (SRCM == ROW_DONOR_POS) {
     const int dn = a.donors.index[i] - a.donors.first;
     if (dn < 0 || dn >= a.donors.count) return;  // another launch's donor, or invalid
     src.layers = a.donors.layers + static_cast<int64_t>(a.donors.first + dn) * a.num_layers;
     src.s_kv = a.donors.s_kv[dn];
     src.s_head = a.donors.s_head[dn];
-    src.s_row = a.donors.s_seq[dn];
-    src.bound = a.donors.bound[dn];
+    // Rows are addressed relative to the donor tensor's first position; the rotation below
+    // still uses the pair's sequence positions.
+    const int64_t p = static_cast<int64_t>(a.src_pos[i]) - a.donors.first_pos[dn];
+    if (p < 0 || p >= a.donors.bound[dn]) return;
+    src_off = p * a.donors.s_seq[dn];
+  } else if (!resolve_row<SRCM>(a, src, a.src_pos, i, &src_off)) {
+    return;
   }
-  constexpr int SRC_RESOLVE = SRCM == ROW_DONOR_POS ? ROW_FLAT_POS : SRCM;
-  int64_t src_off, dst_off;
-  if (!resolve_row<SRC_RESOLVE>(a, src, a.src_pos, i, &src_off)) return;
   if (!resolve_row<DSTM>(a, a.dst, a.dst_pos, i, &dst_off)) return;
   if (SRCM == ROW_INDEX && a.src_index_check) {
     int64_t unused;
@@ -810,7 +814,7 @@ extern "C" int sb_composite_scatter_paged_layers(
   // checked for 16-byte alignment by the caller).
   int64_t donor_vb = 16;
   for (int64_t k = 0; k < num_donors; ++k) {
-    const int64_t* d = donor_strides + 4 * k;
+    const int64_t* d = donor_strides + 5 * k;
     if (d[3] < 0) return fail(fn, "negative donor sequence length");
     for (int t = 0; t < 3; ++t)
       while (donor_vb > 1 && (d[t] * es) % donor_vb != 0) donor_vb >>= 1;
@@ -845,11 +849,12 @@ extern "C" int sb_composite_scatter_paged_layers(
     a.donors.first = static_cast<int>(first);
     a.donors.count = count;
     for (int k = 0; k < count; ++k) {
-      const int64_t* d = donor_strides + 4 * (first + k);
+      const int64_t* d = donor_strides + 5 * (first + k);
       a.donors.s_kv[k] = d[0] * es;
       a.donors.s_head[k] = d[1] * es;
       a.donors.s_seq[k] = d[2] * es;
       a.donors.bound[k] = d[3];
+      a.donors.first_pos[k] = d[4];
     }
     const int rc =
         rope ? launch_move<ROT_DELTA, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, 2 * groups, st)

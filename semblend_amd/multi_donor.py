@@ -109,6 +109,7 @@ def composite_scatter_paged_layers(
     target_positions,
     rope: bool = True,
     rope_base: float = 10000.0,
+    donor_first_positions: Sequence[int] | None = None,
 ) -> list[torch.Tensor]:
     """Scatter pairs from several donors into every layer's paged cache in one pass.
 
@@ -120,6 +121,9 @@ def composite_scatter_paged_layers(
     ``target_positions[i]``; K is rotated by ``target - donor`` when ``rope``. Pairs whose
     donor index, donor position or target slot is out of range are skipped. Target positions
     must be distinct (the kernel does not order writes to one slot).
+    donor_first_positions: per donor, the sequence position its tensors' row 0 holds
+        (default 0): a tensor holding only a window ``[f, f + S_k)`` of a donor (one staged
+        chunk) is read at ``donor_positions[i] - f`` and rotated by the true delta.
     """
     num_pairs = len(target_positions)
     if num_pairs == 0 or not kv_caches or not donor_kvs:
@@ -129,6 +133,10 @@ def composite_scatter_paged_layers(
     nb_total, _, num_heads, block_size, head_dim = ref.shape
     dev = _lib.require_device(*kv_caches, *(t for per in donor_kvs for t in per))
     _check_same(kv_caches, "kv_caches")
+    if donor_first_positions is None:
+        donor_first_positions = [0] * len(donor_kvs)
+    if len(donor_first_positions) != len(donor_kvs):
+        raise ValueError("one first position per donor")
     strides = []
     for k, per_layer in enumerate(donor_kvs):
         if len(per_layer) != num_layers:
@@ -141,7 +149,8 @@ def composite_scatter_paged_layers(
             raise TypeError("donors and caches must share a dtype")
         if d0.stride(3) != 1:
             raise ValueError("donor head_dim must be contiguous (stride 1)")
-        strides += [d0.stride(0), d0.stride(1), d0.stride(2), d0.shape[2]]
+        strides += [d0.stride(0), d0.stride(1), d0.stride(2), d0.shape[2],
+                    int(donor_first_positions[k])]
     if rope and head_dim % 2:
         raise ValueError("head_dim must be even for RoPE")
     kv_tab = _lib.address_table(kv_caches, dev)

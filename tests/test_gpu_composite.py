@@ -112,6 +112,37 @@ def test_composite_single_donor_equals_layers_entries(dev):
             assert torch.equal(x.view(torch.int16), y.view(torch.int16))
 
 
+def test_composite_donor_windows(dev):
+    """Donor tensors that hold only a window [f, f + S) of their donor (first positions
+    given) give the same bits as the whole donors: rows are read at d - f, K is rotated by
+    the true t - d; pairs outside a window are skipped."""
+    layers, h, bs, d, dtype = 2, 4, 16, 128, torch.bfloat16
+    lens = [600, 900]
+    donors = [[randn((2, h, n, d), dtype, 300 + 10 * k + l).to(dev) for l in range(layers)]
+              for k, n in enumerate(lens)]
+    windows = [(128, 300), (512, 256)]      # (first, rows)
+    g = gen(301)
+    tpos = torch.randperm(64 * bs, generator=g)[:400].to(torch.int32)
+    didx = torch.randint(0, 2, (400,), generator=g).to(torch.int32)
+    first = torch.tensor([w[0] for w in windows])[didx.long()]
+    rows = torch.tensor([w[1] for w in windows])[didx.long()]
+    inside = first + (torch.rand(400, generator=g) * rows).long()
+    dpos = inside.to(torch.int32)
+    dpos[:5] = first[:5].to(torch.int32) - 1                 # just before a window: skipped
+    bt = torch.randperm(80, generator=gen(302))[:64].to(torch.int32).to(dev)
+    base = [randn((80, 2, h, bs, d), dtype, 303 + l).to(dev) for l in range(layers)]
+    got = [c.clone() for c in base]
+    composite_scatter_paged_layers(
+        got, [[t[:, :, f:f + n] for t in per] for per, (f, n) in zip(donors, windows)], bt,
+        didx, dpos, tpos, rope=True, rope_base=1e4,
+        donor_first_positions=[f for f, _ in windows])
+    want = [c.clone() for c in base]
+    composite_scatter_paged_layers(want, donors, bt, didx[5:], dpos[5:], tpos[5:], rope=True,
+                                   rope_base=1e4)
+    for a, b in zip(got, want):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 def test_composite_many_donors_two_launches(dev):
     # 20 donors: two launches of at most 16 donors each
     layers, h, bs, d, dtype = 2, 2, 16, 64, torch.bfloat16

@@ -154,6 +154,32 @@ def test_composite_pairs_from_plan():
     assert composite_pairs_from_plan(full, 0).num_pairs == 0
 
 
+def test_group_pairs_by_chunk():
+    from semblend_amd.loader import group_pairs_by_chunk
+    d = [700, 5, 256, 300, -1, 1024, 10, 511, 512]
+    t = [0, 1, 2, 3, 4, 5, 6, 7, 8]
+    arr, off = group_pairs_by_chunk(d, t, 256, 3)
+    # chunk 0: d 5, 10 (pair order kept); chunk 1: 256, 300, 511; chunk 2: 700, 512;
+    # d = -1 and d = 1024 (chunk 4 of 3) dropped
+    np.testing.assert_array_equal(arr[0], [5, 10, 256, 300, 511, 700, 512])
+    np.testing.assert_array_equal(arr[1], [1, 6, 2, 3, 7, 0, 8])
+    np.testing.assert_array_equal(arr[2], 0)
+    np.testing.assert_array_equal(off, [0, 2, 5, 7])
+    assert arr.dtype == np.int32
+    # brute force on random input: every kept pair in its chunk's run, runs in pair order
+    rng = np.random.default_rng(3)
+    d = rng.integers(-50, 3000, 500)
+    t = rng.permutation(500)
+    arr, off = group_pairs_by_chunk(d, t, 128, 20)
+    kept = [(int(a), int(b)) for a, b in zip(d, t) if 0 <= a < 128 * 20]
+    for c in range(20):
+        want = [p for p in kept if p[0] // 128 == c]
+        got = list(zip(arr[0, off[c]:off[c + 1]].tolist(), arr[1, off[c]:off[c + 1]].tolist()))
+        assert got == want
+    with pytest.raises(ValueError):
+        group_pairs_by_chunk([1, 2], [3], 256, 1)
+
+
 def test_plan_types_frozen_and_enum_values():
     m = pa.PositionMask(target_pos=0, mode=pa.AttentionMode.REUSE, donor_pos=3)
     assert m.donor_pos == 3
