@@ -52,6 +52,7 @@ POOL_BLOCKS = 2048
 
 # Library kernels whose launches are timed with HIP events over the timed region.
 KERNELS = ("attn_mfma", "attn_merge", "move_rows", "rope_rows", "rope_index", "fill_i32")
+# (the projection section times its own kernel, qkv_mfma)
 
 # HBM bytes per launch on this workload, from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
 # this script, scaled by what the same counters read for the 1 GiB copy of copy_ceiling()
@@ -447,6 +448,75 @@ def chunk_load_section(dev: torch.device, inp, steps: int) -> dict:
     return out
 
 
+QWEN7B_HIDDEN = 3584
+
+
+def projection_section(dev: torch.device, inp, steps: int) -> dict:
+    """Compacted QKV projection of the attention workload's recompute rows (Qwen2.5-7B:
+    hidden 3584 -> 28 q + 2 x 4 KV heads x 128 = 4608 features, QKV bias), RoPE theta 1e6 at
+    the new positions, K/V written into the paged cache: ``qkv_projection_paged`` (one MFMA
+    kernel) timed as graph replays and per launch. For comparison, torch on the same rows:
+    gather + addmm (hipBLASLt), without RoPE and without the K/V write."""
+    from semblend_amd import _lib
+    from semblend_amd import triton_kernels as tk
+
+    hidden = QWEN7B_HIDDEN
+    feats = (HQ + 2 * HKV) * D
+    gd = torch.Generator(dev).manual_seed(5)
+    x = torch.randn((CTX, hidden), generator=gd, device=dev, dtype=torch.bfloat16)
+    w = (torch.randn((feats, hidden), generator=gd, device=dev) * hidden ** -0.5).to(torch.bfloat16)
+    b = torch.randn((feats,), generator=gd, device=dev, dtype=torch.bfloat16)
+    pos = inp["attn_pos"]
+    rows = int(pos.shape[0])
+    q = torch.empty((rows, HQ, D), dtype=torch.bfloat16, device=dev)
+    flops = 2.0 * rows * hidden * feats
+
+    def fused():
+        tk.qkv_projection_paged(x, w, pos, inp["attn_kv"], inp["block_table"], HQ, HKV, D,
+                                qkv_bias=b, rope_base=ROPE_BASE, out=q)
+
+    pos_l = pos.long()
+
+    def library():
+        torch.addmm(b, x[pos_l], w.t())
+
+    def timed(fn, graph: bool):
+        fn()
+        torch.cuda.synchronize()
+        gr = capture(fn) if graph else None
+        evs = []
+        for _ in range(steps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            gr.replay() if graph else fn()
+            e1.record()
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        t = [a.elapsed_time(c) for a, c in evs]
+        return sum(t) / len(t)
+
+    ms_fused = timed(fused, True)
+    _lib.kernel_timing(True)
+    for _ in range(steps):
+        fused()
+    torch.cuda.synchronize()
+    _lib.kernel_timing(False)
+    total, n = _lib.kernel_time("qkv_mfma")
+    kern_us = 1e3 * total / n
+    ms_lib = timed(library, False)
+    return {
+        "rows": rows, "hidden": hidden, "features": feats, "flops": flops,
+        "fused": {"ms": round(ms_fused, 4), "tflops": round(flops / (ms_fused * 1e-3) / 1e12, 1)},
+        "kernel": {"avg_us": round(kern_us, 2),
+                   "tflops": round(flops / (kern_us * 1e-6) / 1e12, 1),
+                   "frac_of_peak": round(flops / (kern_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)},
+        "torch_gather_addmm": {"ms": round(ms_lib, 4),
+                               "tflops": round(flops / (ms_lib * 1e-3) / 1e12, 1),
+                               "what": "x[pos] @ W^T + b via torch (hipBLASLt), no RoPE, no K/V write"},
+    }
+
+
 def capture(fn) -> "torch.cuda.CUDAGraph":
     """One launch sequence of fn captured as a HIP graph (after an eager run on the capture
     stream, so that every cached device table already exists)."""
@@ -629,6 +699,12 @@ def main() -> int:
     rs = result["rope_scatter"]
     log(f"rope scatter: one donor {rs['one_donor']['ms']:.3f} ms ({rs['one_donor']['gbps']:.0f} GB/s), "
         f"four donors {rs['four_donors']['ms']:.3f} ms ({rs['four_donors']['gbps']:.0f} GB/s)")
+    log("compacted QKV projection with the K/V write")
+    result["projection"] = projection_section(dev, inp, args.steps)
+    pj = result["projection"]
+    log(f"projection: fused {pj['fused']['ms']:.4f} ms ({pj['fused']['tflops']} TFLOP/s), kernel "
+        f"{pj['kernel']['avg_us']} us ({pj['kernel']['tflops']} TFLOP/s), torch gather+addmm "
+        f"{pj['torch_gather_addmm']['ms']:.4f} ms ({pj['torch_gather_addmm']['tflops']} TFLOP/s)")
     log("chunked host-to-device donor load with RoPE on the way")
     result["chunk_load"] = chunk_load_section(dev, inp, 5)
     cl = result["chunk_load"]

@@ -82,6 +82,48 @@ int sb_scatter_donor_kv_paged_layers(const uint64_t* kv_layer_ptrs,
                                      const int64_t* d_strides, int32_t dtype, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * QKV projection (bf16 / fp16 on the matrix cores, fp32 accumulation, one rounding)
+ * ---------------------------------------------------------------------------------------- */
+
+/* Masked QKV projection as a compacted GEMM:
+ *   out[s, :] = hidden[s, :] W^T + bias   where compute_mask[s] != 0, 0 elsewhere.
+ * hidden [seq_len, hidden_dim] (row stride hidden_stride), W [out_features, hidden_dim]
+ * (row stride weight_stride), bias [out_features] in the same dtype or NULL, out
+ * [seq_len, out_features] (row stride out_stride); strides in elements. The mask is
+ * compacted on the device into `workspace` (sb_masked_qkv_projection_workspace_size bytes),
+ * and only the computed rows are multiplied. hidden_dim must be a multiple of 64,
+ * out_features of 8, all rows 16-byte aligned.
+ * Replaces semblend_core/triton_kernels.py:451-522 for bf16 / fp16. */
+int64_t sb_masked_qkv_projection_workspace_size(int64_t seq_len);
+int sb_masked_qkv_projection(void* out, const void* hidden, const void* weight, const void* bias,
+                             const uint8_t* compute_mask, void* workspace,
+                             int64_t workspace_bytes, int64_t seq_len, int64_t hidden_dim,
+                             int64_t out_features, int64_t hidden_stride, int64_t weight_stride,
+                             int64_t out_stride, int32_t dtype, void* stream);
+
+/* Compacted GQA QKV projection fused with the new K/V write: for each row n the hidden row
+ * p = positions[n] is projected with W [(Hq + 2 Hkv) * D, hidden_dim] (+ bias), features
+ * laid out Q | K | V. With inv_freq (device fp32 [D/2]), Q and K are rotated by p with the
+ * interleaved RoPE (angle p * inv_freq[i]) before the rounding. Q goes to q_out[n]
+ * ([num_rows, Hq * D], row stride q_stride); K and V go to the paged cache slot of p
+ * (kv_strides[5] = block, kv, head, pos, dim in elements), skipped when the slot is out of
+ * range. A row whose position is outside [0, seq_len) gets a zero Q row and writes no K/V.
+ * head_dim must be a multiple of 8 and every row (hidden, W, q_out, cache) 16-byte aligned.
+ * With RoPE, `workspace` (16-byte aligned, sb_qkv_projection_paged_workspace_size bytes)
+ * holds the per-row cos/sin table; without, it may be NULL.
+ * No reference counterpart: it fuses masked_qkv_projection (triton_kernels.py:451-522) with
+ * the K/V write of partial_prefill (:904-909) into the paged layout, for GQA models. */
+int64_t sb_qkv_projection_paged_workspace_size(int64_t num_rows, int64_t head_dim, int32_t rope);
+int sb_qkv_projection_paged(void* q_out, const void* hidden, const void* weight,
+                            const void* bias, const int32_t* positions, int64_t num_rows,
+                            int64_t seq_len, int64_t hidden_dim, int64_t num_q_heads,
+                            int64_t num_kv_heads, int64_t head_dim, const float* inv_freq,
+                            void* workspace, int64_t workspace_bytes, void* kv_cache, const int32_t* block_table, int64_t block_size,
+                            int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                            int64_t hidden_stride, int64_t weight_stride, int64_t q_stride,
+                            const int64_t* kv_strides, int32_t dtype, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * RoPE delta correction (interleaved pairs (2i, 2i+1); inv_freq is a device fp32 array of
  * head_dim/2 entries, 1 / base^(2i/head_dim))
  * ---------------------------------------------------------------------------------------- */

@@ -42,6 +42,7 @@ __all__ = [
     "partial_prefill",
     "partial_prefill_attention",
     "permute_paged_kv_with_rope",
+    "qkv_project_paged",
     "rope_correct_k",
     "rope_correct_scatter_paged",
     "rotate_interleaved",
@@ -331,6 +332,48 @@ def masked_qkv_projection(hidden_states, qkv_weight, compute_mask, qkv_bias=None
         hidden_states.float(), qkv_weight.float(),
         qkv_bias.float() if qkv_bias is not None else None)
     return (projected * compute_mask.unsqueeze(1).float()).to(hidden_states.dtype)
+
+
+def qkv_project_paged(hidden_states, qkv_weight, positions, kv_cache, block_table, num_heads,
+                      num_kv_heads, head_dim, qkv_bias=None, rope_base=None):
+    """Compacted, GQA form of the masked projection (triton_kernels.py:511-520: fp32 linear,
+    one rounding to the input dtype) restricted to the rows at ``positions``, with the new
+    K/V written into the paged cache at those positions.
+
+    Features are laid out Q [Hq*D] | K [Hkv*D] | V [Hkv*D]. With ``rope_base``, Q and K of
+    the row at position p are rotated in fp32 by p with the path's interleaved RoPE
+    (rope_correction.py:163-178, angle ``float(p) * inv_freq``) before the rounding. K/V rows
+    whose paged slot is out of range are not written; rows whose position lies outside the
+    hidden states give zero Q and write nothing. Returns Q [R, Hq, D] in the input dtype.
+    """
+    seq_len = hidden_states.shape[0]
+    pos = torch.as_tensor(positions).long()
+    n = pos.shape[0]
+    valid = (pos >= 0) & (pos < seq_len)
+    x = torch.zeros((n, hidden_states.shape[1]), dtype=torch.float32)
+    x[valid] = hidden_states[pos[valid]].float()
+    proj = torch.nn.functional.linear(x, qkv_weight.float(),
+                                      qkv_bias.float() if qkv_bias is not None else None)
+    qf, kf = num_heads * head_dim, num_kv_heads * head_dim
+    q = proj[:, :qf].reshape(n, num_heads, head_dim)
+    k = proj[:, qf:qf + kf].reshape(n, num_kv_heads, head_dim)
+    v = proj[:, qf + kf:qf + 2 * kf].reshape(n, num_kv_heads, head_dim)
+    if rope_base is not None:
+        theta = pos.to(torch.float32)[:, None] * inv_freq(rope_base, head_dim)[None, :]
+        c, s = torch.cos(theta)[:, None, :], torch.sin(theta)[:, None, :]
+        q = rotate_interleaved(q, c, s)
+        k = rotate_interleaved(k, c, s)
+    q[~valid] = 0.0
+    num_blocks_total, _, _, block_size, _ = kv_cache.shape
+    for r in range(n):
+        if not bool(valid[r]):
+            continue
+        slot = _paged_slot(block_table, int(pos[r]), block_size, num_blocks_total)
+        if slot is None:
+            continue
+        kv_cache[slot[0], 0, :, slot[1], :] = k[r].to(kv_cache.dtype)
+        kv_cache[slot[0], 1, :, slot[1], :] = v[r].to(kv_cache.dtype)
+    return q.to(hidden_states.dtype)
 
 
 def partial_prefill(hidden_states, donor_kv, qkv_weight, output_projection, donor_positions,

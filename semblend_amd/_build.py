@@ -42,6 +42,7 @@ COMMON_FLAGS = [
 # multiply-add), so contraction is off there.
 FILE_FLAGS = {
     "sb_move.hip": ["-ffp-contract=off"],
+    "sb_qkv.hip": ["-ffp-contract=off"],
 }
 
 

@@ -877,57 +877,6 @@ __global__ __launch_bounds__(64) void attn_valu_kernel(AttnArgs a) {
   }
 }
 
-// ---------------------------------------------------------------------------------------
-// Dense drop-in helpers: compact a bool mask into ascending positions (+ count), and write
-// zeros into the output rows whose mask entry is 0.
-// ---------------------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void mask_compact_kernel(const uint8_t* mask, int64_t n,
-                                                            int32_t* pos_out,
-                                                            int32_t* count_out) {
-  __shared__ int wsum[16];
-  __shared__ int base;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid == 0) base = 0;
-  __syncthreads();
-  for (int64_t c0 = 0; c0 < n; c0 += 1024) {
-    const int64_t i = c0 + tid;
-    const bool f = i < n && mask[i] != 0;
-    const uint64_t b = __ballot(f);
-    const int pre = __popcll(b & ((uint64_t{1} << lane) - 1));
-    if (lane == 0) wsum[wave] = __popcll(b);
-    __syncthreads();
-    int off = base;
-    for (int w = 0; w < wave; ++w) off += wsum[w];
-    if (f) pos_out[off + pre] = static_cast<int32_t>(i);
-    __syncthreads();
-    if (tid == 0) {
-      int t = 0;
-      for (int w = 0; w < 16; ++w) t += wsum[w];
-      base += t;
-    }
-    __syncthreads();
-  }
-  if (tid == 0) *count_out = base;
-}
-
-template <int VB>
-__global__ void zero_rows_kernel(char* out, const uint8_t* mask, int64_t num_heads,
-                                 int64_t seq_len, int64_t s_head, int64_t s_seq, int vpr) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t total = num_heads * seq_len * vpr;
-  if (idx >= total) return;
-  const int64_t j = idx % vpr;
-  const int64_t row = idx / vpr;
-  const int64_t s = row % seq_len;
-  const int64_t h = row / seq_len;
-  if (mask[s]) return;
-  char* p = out + h * s_head + s * s_seq + j * VB;
-  if (VB == 16) *reinterpret_cast<uint4*>(p) = make_uint4(0, 0, 0, 0);
-  else if (VB == 8) *reinterpret_cast<uint2*>(p) = make_uint2(0, 0);
-  else if (VB == 4) *reinterpret_cast<uint32_t*>(p) = 0u;
-  else *reinterpret_cast<uint16_t*>(p) = 0;
-}
-
 namespace {
 
 // Resident workgroups of the MFMA kernel on 256 CUs (one 4-wave workgroup per CU with two
@@ -1230,7 +1179,7 @@ extern "C" int sb_partial_prefill_attention(void* out, const void* q, const void
     else if (vb == 4) SB_LAUNCH("zero_rows", zero_rows_kernel<4>, grid, dim3(256), st, o, compute_mask, num_heads, seq_len, sh, ss, vpr);
     else SB_LAUNCH("zero_rows", zero_rows_kernel<2>, grid, dim3(256), st, o, compute_mask, num_heads, seq_len, sh, ss, vpr);
   }
-  SB_LAUNCH("mask_compact", mask_compact_kernel, dim3(1), dim3(1024), st, compute_mask, seq_len,
+  SB_LAUNCH("mask_compact", mask_compact_kernel<0>, dim3(1), dim3(1024), st, compute_mask, seq_len,
             pos, pos + seq_len);
   int rc = check_launch(fn);
   if (rc) return rc;

@@ -157,4 +157,68 @@ template <> struct ByteVec<4> { using T = uint32_t; };
 template <> struct ByteVec<2> { using T = uint16_t; };
 template <> struct ByteVec<1> { using T = uint8_t; };
 
+// fp32 sin/cos rounded correctly: evaluated in fp64 and rounded once to fp32. These are the
+// values a correctly rounded libm returns, which torch's CPU kernels also produce for all but
+// rare arguments. Matching them matters where e*c - o*s cancels: for an output of ~1e-6 from
+// O(1) inputs, a one-ulp difference in cos or sin is several bf16 ulps of the result.
+__device__ __forceinline__ void sincos_rn(float x, float* s, float* c) {
+  double sd, cd;
+  sincos(static_cast<double>(x), &sd, &cd);
+  *s = static_cast<float>(sd);
+  *c = static_cast<float>(cd);
+}
+
+// ---------------------------------------------------------------------------------------
+// Dense drop-in helpers shared by the attention and projection entries: compact a bool mask
+// into ascending positions (+ count) in one workgroup, and write zeros into the output rows
+// whose mask entry is 0 (rows of [heads, seq, ...] under byte strides).
+// ---------------------------------------------------------------------------------------
+template <int kUnused = 0>
+__global__ __launch_bounds__(1024) void mask_compact_kernel(const uint8_t* mask, int64_t n,
+                                                            int32_t* pos_out,
+                                                            int32_t* count_out) {
+  __shared__ int wsum[16];
+  __shared__ int base;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) base = 0;
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < n; c0 += 1024) {
+    const int64_t i = c0 + tid;
+    const bool f = i < n && mask[i] != 0;
+    const uint64_t b = __ballot(f);
+    const int pre = __popcll(b & ((uint64_t{1} << lane) - 1));
+    if (lane == 0) wsum[wave] = __popcll(b);
+    __syncthreads();
+    int off = base;
+    for (int w = 0; w < wave; ++w) off += wsum[w];
+    if (f) pos_out[off + pre] = static_cast<int32_t>(i);
+    __syncthreads();
+    if (tid == 0) {
+      int t = 0;
+      for (int w = 0; w < 16; ++w) t += wsum[w];
+      base += t;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) *count_out = base;
+}
+
+template <int VB>
+__global__ void zero_rows_kernel(char* out, const uint8_t* mask, int64_t num_heads,
+                                 int64_t seq_len, int64_t s_head, int64_t s_seq, int vpr) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = num_heads * seq_len * vpr;
+  if (idx >= total) return;
+  const int64_t j = idx % vpr;
+  const int64_t row = idx / vpr;
+  const int64_t s = row % seq_len;
+  const int64_t h = row / seq_len;
+  if (mask[s]) return;
+  char* p = out + h * s_head + s * s_seq + j * VB;
+  if (VB == 16) *reinterpret_cast<uint4*>(p) = make_uint4(0, 0, 0, 0);
+  else if (VB == 8) *reinterpret_cast<uint2*>(p) = make_uint2(0, 0);
+  else if (VB == 4) *reinterpret_cast<uint32_t*>(p) = 0u;
+  else *reinterpret_cast<uint16_t*>(p) = 0;
+}
+
 }  // namespace sb

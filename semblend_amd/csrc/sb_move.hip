@@ -218,17 +218,6 @@ __device__ __forceinline__ void store_vec(char* p, const uint32_t* w) {
   }
 }
 
-// fp32 sin/cos rounded correctly: evaluated in fp64 and rounded once to fp32. These are the
-// values a correctly rounded libm returns, which torch's CPU kernels also produce for all but
-// rare arguments. Matching them matters where e*c - o*s cancels: for an output of ~1e-6 from
-// O(1) inputs, a one-ulp difference in cos or sin is several bf16 ulps of the result.
-__device__ __forceinline__ void sincos_rn(float x, float* s, float* c) {
-  double sd, cd;
-  sincos(static_cast<double>(x), &sd, &cd);
-  *s = static_cast<float>(sd);
-  *c = static_cast<float>(cd);
-}
-
 // In-register rotation of E/2 interleaved pairs: e' = e*c - o*s, o' = e*s + o*c.
 template <int NP>
 __device__ __forceinline__ void rotate_pairs(float* f, const float* c, const float* s) {

@@ -1,0 +1,565 @@
+// Compacted QKV projection for gfx950, fused with the new K/V write into the paged cache.
+//
+// The reference projects every row of the sequence and zeroes the reuse rows afterwards
+// (semblend_core/triton_kernels.py:451-522; fp32 linear, one rounding to the input dtype).
+// Here only the computed rows are multiplied: row n of the product is hidden row positions[n],
+// gathered while the tile is loaded. The product is taken transposed,
+//     out^T[feature, row] = W[feature, :] . hidden[positions[row], :],
+// on v_mfma_f32_32x32x16 (bf16 / fp16 in, fp32 accumulate). In that accumulator layout each
+// lane owns one row (token) and four consecutive features per 4-register group, so the
+// interleaved RoPE pairs (2i, 2i+1) of a head sit in one lane and the epilogue rotates them
+// in registers before the single rounding to the output dtype.
+//
+// Tiles: 256 features x 256 rows per workgroup of 4 waves (each wave 128 x 128 = 4 x 4 MFMA
+// blocks, 256 fp32 accumulators), one workgroup per CU; 128 x 128 (two per CU) when the row
+// count is too small to give half the CUs a big tile. 32 hidden elements per k-step in a
+// 4-stage LDS ring (loads three steps ahead, one barrier per step). Both operands are read with their hidden
+// dimension contiguous (W row-major [F, hidden], hidden [S, hidden]), moved global -> LDS
+// with global_load_lds_dwordx4, 16-byte chunks of each tile row XOR-swizzled so that the
+// ds_read_b128 fragment reads of 16 consecutive rows fall on distinct banks. Tiles are
+// ordered XCD by XCD in bands of row tiles (qkv_tile) for L2 reuse.
+//
+// Epilogue (feature layout Q [Hq*D] | K [Hkv*D] | V [Hkv*D]):
+//   split mode  Q -> q_out[row] (compact), K / V -> paged cache slot of positions[row];
+//   dense mode  all features -> out[positions[row]] (the [S, F] drop-in layout).
+// Bias (input dtype) is added in fp32; with RoPE, Q and K are rotated by the row's position
+// (angle = float(p) * inv_freq[i]) with cos/sin from a per-(row, pair) table that a small
+// kernel fills first (fp64 sincos rounded once to fp32, as in the RoPE kernels).
+
+#include <algorithm>
+#include <type_traits>
+
+#include "sb_common.h"
+
+namespace sb {
+namespace {
+
+typedef __bf16 qbf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 qf16x8_t __attribute__((ext_vector_type(8)));
+typedef float qf32x16_t __attribute__((ext_vector_type(16)));
+
+#ifndef SB_QKV_GROUP
+#define SB_QKV_GROUP 8
+#endif
+constexpr int kQThreads = 256;
+constexpr int kTK = 32;        // hidden elements per k-step (64-byte tile rows)
+constexpr int kStages = 4;     // LDS ring depth: loads run three k-steps ahead
+constexpr int kTileChunks = kTK / 8;  // 16-byte chunks per tile row
+constexpr int kGroup = SB_QKV_GROUP;  // row tiles per band of the tile order
+constexpr int kXcds = 8;       // MI355X: workgroups go round-robin to 8 XCDs
+
+enum QkvMode : int { QKV_SPLIT = 0, QKV_DENSE = 1 };
+
+struct QkvArgs {
+  const char* hidden;         // [S, hidden] rows
+  int64_t h_s_row;            // bytes
+  const char* weight;         // [F, hidden] rows
+  int64_t w_s_row;            // bytes
+  const char* bias;           // [F] in the input dtype, or nullptr
+  const int32_t* positions;   // [R] hidden row (= sequence position) of each computed row
+  const int32_t* count;       // device row count (overrides num_rows when smaller), or nullptr
+  int64_t num_rows;           // R (grid bound)
+  int64_t seq_len;            // hidden rows S
+  int64_t k_steps;            // hidden / kTK
+  int64_t num_features;       // F
+  int64_t q_features;         // Hq * D
+  int64_t kv_features;        // Hkv * D
+  int head_dim;
+  const float4* rope_cs;      // [R, D/4] of (cos, sin) pairs for pairs 2i, 2i+1, or nullptr
+  char* out;                  // split: q_out [R, Hq*D] rows; dense: [S, F] rows
+  int64_t o_s_row;            // bytes
+  char* kv;                   // split: paged cache [NB, 2, Hkv, bs, D] under byte strides
+  int64_t s_blk, s_kv, s_head, s_pos;
+  const int32_t* block_table;
+  int64_t block_size, nb_total, nb_per_seq;
+};
+
+// 16-byte chunk position of chunk c of a 64-byte tile row r. Rows share the 64 banks four
+// ways; the XOR with (r / 4) spreads 16 consecutive rows read at one chunk over distinct
+// bank groups, so the ds_read_b128 fragment reads are conflict-free.
+__device__ __forceinline__ int qswz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+
+// s_waitcnt vmcnt(N) (6-bit count, split over bits 3:0 and 15:14), other counters untouched.
+template <int N>
+__device__ __forceinline__ void qkv_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N >> 4) << 14));
+}
+
+// Tile of workgroup b. Workgroups are dispatched round-robin over the XCDs, so workgroup b
+// runs on XCD b % 8; each XCD is given a contiguous range of the tile order, and the order
+// walks bands of kGroup row tiles feature tile by feature tile, so the workgroups resident
+// on one XCD at a time cover a compact block of feature x row tiles and share their W and
+// hidden slices in that XCD's L2.
+__device__ __forceinline__ void qkv_tile(int64_t b, int64_t n_ft, int64_t n_rt, int64_t* ft,
+                                         int64_t* rt) {
+  const int64_t total = n_ft * n_rt;
+  const int64_t x = b % kXcds, i = b / kXcds;
+  const int64_t per = total / kXcds, extra = total % kXcds;
+  const int64_t q = x * per + min(x, extra) + i;
+  const int64_t band = q / (kGroup * n_ft);
+  const int64_t in_band = q - band * kGroup * n_ft;
+  const int64_t rows_in_band = min<int64_t>(kGroup, n_rt - band * kGroup);
+  *rt = band * kGroup + in_band % rows_in_band;
+  *ft = in_band / rows_in_band;
+}
+
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane i's chunk lands at
+// lds_wave + 16 i, lds_wave wave-uniform. Inline assembly so that the compiler does not order
+// every later LDS read behind it; the kernel waits (vmcnt) before the barrier that publishes
+// each stage.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void qkv_dma(const char* src, const uint16_t* lds_wave) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_wave)));
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off"
+      :
+      : "s"(m0), "v"(src)
+      : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int DT>
+__device__ __forceinline__ float qkv_elem(uint16_t h) {
+  return DT == SB_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+// Two floats rounded to the input dtype (round to nearest even, one instruction per pair);
+// a bf16 NaN becomes 0x7FC0 as in torch, so the bits equal f32_to_bf16's.
+template <int DT>
+__device__ __forceinline__ uint32_t qkv_pack2(float lo, float hi) {
+  if (DT == SB_DTYPE_BF16) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    uint32_t w = __builtin_bit_cast(uint32_t, v);
+    if (lo != lo) w = (w & 0xffff0000u) | 0x7fc0u;
+    if (hi != hi) w = (w & 0x0000ffffu) | 0x7fc00000u;
+    return w;
+  }
+  return static_cast<uint32_t>(f32_to_f16(lo)) | (static_cast<uint32_t>(f32_to_f16(hi)) << 16);
+}
+
+// cos / sin of every (computed row, rotary pair), correctly rounded to fp32 (fp64 sincos):
+// table[n * D/4 + i/2] = (cos, sin) of pair 2 * (i/2) and of the next pair, angle
+// float(p) * inv_freq[pair]. Rows without a valid position get the identity.
+__global__ void qkv_rope_table_kernel(const int32_t* positions, int64_t num_rows,
+                                      int64_t seq_len, const float* inv_freq, int half_d,
+                                      float4* table) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int quads = half_d / 2;
+  if (idx >= num_rows * quads) return;
+  const int64_t n = idx / quads;
+  const int k = static_cast<int>(idx - n * quads);
+  const int p = positions[n];
+  float4 v = make_float4(1.f, 0.f, 1.f, 0.f);
+  if (p >= 0 && p < seq_len) {
+    sincos_rn(static_cast<float>(p) * inv_freq[2 * k], &v.y, &v.x);
+    sincos_rn(static_cast<float>(p) * inv_freq[2 * k + 1], &v.w, &v.z);
+  }
+  table[idx] = v;
+}
+
+// The projection. Workgroup tile: TM = 64 BI features x TN = 64 BJ rows, 4 waves as 2 x 2,
+// each wave BI x BJ MFMA blocks of 32 x 32 (BI = 4, BJ = 2..4: up to a 128 x 128 wave tile
+// and 256 accumulators, one workgroup per CU; BI = BJ = 2: 64 x 64, two per CU).
+template <int DT, int MODE, int BI, int BJ>
+__global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kernel(QkvArgs a) {
+  using vec8 = std::conditional_t<DT == SB_DTYPE_BF16, qbf16x8_t, qf16x8_t>;
+  constexpr int TM = 64 * BI, TN = 64 * BJ;
+  constexpr int LA = TM * kTileChunks / kQThreads;  // A loads per thread per stage (= BI)
+  constexpr int LB = TN * kTileChunks / kQThreads;  // B loads per thread per stage (= BJ)
+  constexpr int NKS = kTK / 16;                     // MFMA k-substeps per step
+  // The LDS ring (A stages, then B stages); after the k loop it holds the output tile.
+  __shared__ __align__(16) uint16_t smem[kStages * (TM + TN) * kTK];
+  static_assert(TM * TN <= kStages * (TM + TN) * kTK, "output tile fits in the ring");
+  auto As = [&](int stage) { return smem + stage * TM * kTK; };
+  auto Bs = [&](int stage) { return smem + kStages * TM * kTK + stage * TN * kTK; };
+  __shared__ int64_t brow[TN];   // byte offset of each tile row's hidden row
+  __shared__ int bpos[TN];       // its position (-1: no row)
+  __shared__ int64_t kvofs[TN];  // split: byte offset of its paged slot (-1: none)
+  __shared__ __align__(16) float bias_s[TM];  // the tile's bias (0 without bias / past F)
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, lq = lane & 31, lg = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int64_t n_ft = (a.num_features + TM - 1) / TM;
+  const int64_t n_rt = (a.num_rows + TN - 1) / TN;
+  int64_t ft, rt;
+  qkv_tile(blockIdx.x, n_ft, n_rt, &ft, &rt);
+  const int64_t m0 = ft * TM;
+  const int64_t n0 = rt * TN;
+  int64_t rows = a.num_rows;
+  if (a.count) rows = min(rows, static_cast<int64_t>(*a.count));
+  if (n0 >= rows) return;  // uniform
+
+  for (int t = tid; t < TN; t += kQThreads) {
+    const int64_t n = n0 + t;
+    int p = -1;
+    if (n < rows) {
+      p = a.positions[n];
+      if (p < 0 || p >= a.seq_len) p = -1;
+    }
+    bpos[t] = p;
+    brow[t] = static_cast<int64_t>(p < 0 ? 0 : p) * a.h_s_row;
+    int64_t off = -1;
+    if (MODE == QKV_SPLIT && p >= 0) {
+      const int64_t lb = p / a.block_size;
+      if (lb < a.nb_per_seq) {
+        const int64_t pb = a.block_table[lb];
+        if (pb >= 0 && pb < a.nb_total) off = pb * a.s_blk + (p - lb * a.block_size) * a.s_pos;
+      }
+    }
+    kvofs[t] = off;
+  }
+  for (int t = tid; t < TM; t += kQThreads) {
+    const int64_t f = m0 + t;
+    bias_s[t] = (a.bias && f < a.num_features)
+                    ? qkv_elem<DT>(reinterpret_cast<const uint16_t*>(a.bias)[f]) : 0.f;
+  }
+  __syncthreads();
+
+  // DMA sources: slot s = q * 256 + tid of a stage holds tile row s / 4 = 64 q + tid / 4 at
+  // position tid % 4, i.e. global chunk qswz(row, tid % 4), which does not depend on q.
+  const int chunk = qswz(tid / kTileChunks, tid % kTileChunks);
+  const char* asrc[LA];
+  const char* bsrc[LB];
+#pragma unroll
+  for (int q = 0; q < LA; ++q) {
+    const int64_t f = min(m0 + q * 64 + tid / kTileChunks, a.num_features - 1);
+    asrc[q] = a.weight + f * a.w_s_row + 16 * chunk;
+  }
+#pragma unroll
+  for (int q = 0; q < LB; ++q) bsrc[q] = a.hidden + brow[q * 64 + tid / kTileChunks] + 16 * chunk;
+  auto issue = [&](int stage, int64_t kt) {
+    const int64_t ko = kt * (kTK * 2);
+#pragma unroll
+    for (int q = 0; q < LA; ++q)
+      qkv_dma(asrc[q] + ko, As(stage) + (q * kQThreads + wave * 64) * 8);
+#pragma unroll
+    for (int q = 0; q < LB; ++q)
+      qkv_dma(bsrc[q] + ko, Bs(stage) + (q * kQThreads + wave * 64) * 8);
+  };
+
+  qf32x16_t acc[BI][BJ];
+#pragma unroll
+  for (int i = 0; i < BI; ++i)
+#pragma unroll
+    for (int j = 0; j < BJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Ring of kStages: step kt lives in stage kt % kStages; loads run kStages - 1 steps ahead.
+  // One barrier per step both publishes step kt and retires step kt - 1, whose stage the
+  // loads issued right after it refill.
+#pragma unroll
+  for (int s0 = 0; s0 < kStages - 1; ++s0)
+    if (s0 < a.k_steps) issue(s0, s0);
+  for (int64_t kt = 0; kt < a.k_steps; ++kt) {
+    const int st = static_cast<int>(kt % kStages);
+    const int64_t ahead = a.k_steps - 1 - kt;  // steps issued after this one (at most 2)
+    if (ahead >= 2) qkv_wait_vm<2 * (LA + LB)>();
+    else if (ahead == 1) qkv_wait_vm<LA + LB>();
+    else qkv_wait_vm<0>();
+    __syncthreads();
+    if (kt + kStages - 1 < a.k_steps)
+      issue(static_cast<int>((kt + kStages - 1) % kStages), kt + kStages - 1);
+    // Per k-substep: the wave's BI A and BJ B fragments, then BI x BJ MFMAs.
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int c = 2 * ks + lg;
+      vec8 af[BI], bf[BJ];
+#pragma unroll
+      for (int i = 0; i < BI; ++i) {
+        const int r = wm * (32 * BI) + i * 32 + lq;
+        af[i] = *reinterpret_cast<const vec8*>(As(st) + r * kTK + 8 * qswz(r, c));
+      }
+#pragma unroll
+      for (int j = 0; j < BJ; ++j) {
+        const int r = wn * (32 * BJ) + j * 32 + lq;
+        bf[j] = *reinterpret_cast<const vec8*>(Bs(st) + r * kTK + 8 * qswz(r, c));
+      }
+#pragma unroll
+      for (int i = 0; i < BI; ++i)
+#pragma unroll
+        for (int j = 0; j < BJ; ++j) {
+          if (DT == SB_DTYPE_BF16)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+  }
+
+  // Epilogue, phase 1: lane (lq, lg) of block (i, j) holds tile row wn*32*BJ + 32j + lq and,
+  // in register group g, tile features wm*32*BI + 32i + 8g + 4lg .. +3. Bias, RoPE and the
+  // rounding happen in registers; the rounded tile goes to LDS as [TN rows][TM features],
+  // 8-byte units of row r XOR-swizzled by 2 (r % 16) so that the 32 rows a wave writes at
+  // once spread over the banks (and 16-byte pairs of units stay adjacent for phase 2).
+  const int64_t kf0 = a.q_features, vf0 = a.q_features + a.kv_features;
+  const int quads = a.head_dim / 4;
+  __syncthreads();  // every wave is done with the last stage
+#pragma unroll
+  for (int j = 0; j < BJ; ++j) {
+    const int tr = wn * (32 * BJ) + j * 32 + lq;
+    const int64_t n = n0 + tr;
+    const bool rot = a.rope_cs && n < rows && bpos[tr] >= 0;
+    const int sw = 2 * (tr & 15);
+    // This row's cos / sin for every group it rotates, fetched together.
+    float4 cs[BI][4];
+#pragma unroll
+    for (int i = 0; i < BI; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t f0 = m0 + wm * (32 * BI) + i * 32 + 8 * g + 4 * lg;
+        cs[i][g] = make_float4(1.f, 0.f, 1.f, 0.f);
+        if (rot && f0 < vf0) {
+          const int64_t rf = f0 - (f0 < kf0 ? 0 : kf0);
+          cs[i][g] = a.rope_cs[n * quads + (rf % a.head_dim) / 4];
+        }
+      }
+#pragma unroll
+    for (int i = 0; i < BI; ++i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int fl = wm * (32 * BI) + i * 32 + 8 * g + 4 * lg;  // tile feature
+        const float4 b = *reinterpret_cast<const float4*>(&bias_s[fl]);
+        float v0 = acc[i][j][4 * g] + b.x, v1 = acc[i][j][4 * g + 1] + b.y;
+        float v2 = acc[i][j][4 * g + 2] + b.z, v3 = acc[i][j][4 * g + 3] + b.w;
+        if (rot) {  // the identity (1, 0) for features that are not rotated
+          const float4 c = cs[i][g];
+          float ev = v0, od = v1;
+          v0 = ev * c.x - od * c.y;
+          v1 = ev * c.y + od * c.x;
+          ev = v2;
+          od = v3;
+          v2 = ev * c.z - od * c.w;
+          v3 = ev * c.w + od * c.z;
+        }
+        uint2 w;
+        w.x = qkv_pack2<DT>(v0, v1);
+        w.y = qkv_pack2<DT>(v2, v3);
+        *reinterpret_cast<uint2*>(smem + tr * TM + 4 * ((fl / 4) ^ sw)) = w;
+      }
+    }
+  }
+  __syncthreads();
+
+  // Phase 2: 16-byte chunks (8 features) of each tile row to their destination, consecutive
+  // threads along a row: Q / dense rows and K / V head rows are contiguous, so the stores
+  // coalesce. Chunks never straddle a head (head_dim % 8 == 0).
+  constexpr int CPR = TM / 8;  // chunks per tile row
+  for (int k = tid; k < TN * CPR; k += kQThreads) {
+    const int tr = k / CPR, c = k % CPR;
+    const int64_t n = n0 + tr;
+    const int64_t f0 = m0 + 8 * c;
+    if (n >= rows || f0 >= a.num_features) continue;
+    const int p = bpos[tr];
+    uint4 w = *reinterpret_cast<const uint4*>(smem + tr * TM + 4 * ((2 * c) ^ (2 * (tr & 15))));
+    if (MODE == QKV_DENSE) {
+      if (p >= 0) *reinterpret_cast<uint4*>(a.out + p * a.o_s_row + 2 * f0) = w;
+    } else if (f0 < kf0) {
+      if (p < 0) w = make_uint4(0u, 0u, 0u, 0u);
+      *reinterpret_cast<uint4*>(a.out + n * a.o_s_row + 2 * f0) = w;
+    } else {
+      const int64_t slot = kvofs[tr];
+      if (slot < 0) continue;
+      const bool is_v = f0 >= vf0;
+      const int64_t rf = f0 - (is_v ? vf0 : kf0);
+      const int64_t h = rf / a.head_dim;
+      *reinterpret_cast<uint4*>(a.kv + slot + (is_v ? a.s_kv : 0) + h * a.s_head +
+                                2 * (rf - h * a.head_dim)) = w;
+    }
+  }
+}
+
+// Checks shared by both entries; fills the operand part of QkvArgs.
+int qkv_common(const char* fn, QkvArgs* a, const void* hidden, const void* weight,
+               const void* bias, int64_t seq_len, int64_t hidden_dim, int64_t num_features,
+               int64_t hidden_stride, int64_t weight_stride, int32_t dtype) {
+  if (dtype != SB_DTYPE_BF16 && dtype != SB_DTYPE_F16)
+    return fail(fn, "dtype must be bf16 or fp16 (the MFMA path)");
+  if (!hidden || !weight) return fail(fn, "null pointer argument");
+  // Rows without a valid position still load hidden row 0 (their results are not stored).
+  if (seq_len < 1) return fail(fn, "seq_len must be positive");
+  if (hidden_dim <= 0 || hidden_dim % 64 != 0)
+    return fail(fn, "hidden size must be a positive multiple of 64");
+  if (num_features <= 0 || num_features % 8 != 0)
+    return fail(fn, "output features must be a positive multiple of 8");
+  if (reinterpret_cast<uintptr_t>(hidden) % 16 || reinterpret_cast<uintptr_t>(weight) % 16 ||
+      (hidden_stride * 2) % 16 || (weight_stride * 2) % 16)
+    return fail(fn, "hidden and weight rows must be 16-byte aligned");
+  if (bias && reinterpret_cast<uintptr_t>(bias) % 8) return fail(fn, "bias must be 8-byte aligned");
+  a->hidden = static_cast<const char*>(hidden);
+  a->h_s_row = hidden_stride * 2;
+  a->weight = static_cast<const char*>(weight);
+  a->w_s_row = weight_stride * 2;
+  a->bias = static_cast<const char*>(bias);
+  a->seq_len = seq_len;
+  a->k_steps = hidden_dim / kTK;
+  a->num_features = num_features;
+  return SB_OK;
+}
+
+// Tile shape. 256 features x 64 BJ rows (one workgroup per CU) with BJ in {4, 3, 2} chosen to
+// minimise the work of the busiest CU, rounds x BJ (ties: larger tiles); 128 x 128 (two per
+// CU) when even BJ = 2 leaves more than half the CUs without a tile.
+constexpr int64_t kCus = 256;
+template <int MODE>
+int launch_qkv(const char* fn, const QkvArgs& a, int32_t dtype, hipStream_t st) {
+  const int64_t nft = (a.num_features + 255) / 256;
+  int bj = 0;
+  int64_t best = 0, tiles = 0;
+  for (int c = 4; c >= 2; --c) {
+    const int64_t t = nft * ((a.num_rows + 64 * c - 1) / (64 * c));
+    const int64_t cost = ((t + kCus - 1) / kCus) * c;
+    if (bj == 0 || cost < best) {
+      bj = c;
+      best = cost;
+      tiles = t;
+    }
+  }
+  if (tiles * 2 < kCus) {
+    bj = 0;  // small tiles
+    tiles = ((a.num_features + 127) / 128) * ((a.num_rows + 127) / 128);
+  }
+  if (tiles > 0x7fffffff) return fail(fn, "grid too large");
+  const dim3 grid(static_cast<unsigned>(tiles));
+#define SB_QKV_CASE(DT, BI, BJ)                                                              \
+  SB_LAUNCH("qkv_mfma", (qkv_mfma_kernel<DT, MODE, BI, BJ>), grid, dim3(kQThreads), st, a)
+#define SB_QKV_DT(DT)                   \
+  switch (bj) {                         \
+    case 4: SB_QKV_CASE(DT, 4, 4); break; \
+    case 3: SB_QKV_CASE(DT, 4, 3); break; \
+    case 2: SB_QKV_CASE(DT, 4, 2); break; \
+    default: SB_QKV_CASE(DT, 2, 2); break; \
+  }
+  if (dtype == SB_DTYPE_BF16) {
+    SB_QKV_DT(SB_DTYPE_BF16)
+  } else {
+    SB_QKV_DT(SB_DTYPE_F16)
+  }
+#undef SB_QKV_DT
+#undef SB_QKV_CASE
+  return check_launch(fn);
+}
+
+}  // namespace
+}  // namespace sb
+
+using namespace sb;
+
+extern "C" int64_t sb_qkv_projection_paged_workspace_size(int64_t num_rows, int64_t head_dim,
+                                                         int32_t rope) {
+  return rope ? num_rows * head_dim * static_cast<int64_t>(sizeof(float)) : 0;
+}
+
+extern "C" int sb_qkv_projection_paged(
+    void* q_out, const void* hidden, const void* weight, const void* bias,
+    const int32_t* positions, int64_t num_rows, int64_t seq_len, int64_t hidden_dim,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, const float* inv_freq,
+    void* workspace, int64_t workspace_bytes, void* kv_cache, const int32_t* block_table, int64_t block_size, int64_t num_blocks_total,
+    int64_t num_blocks_per_seq, int64_t hidden_stride, int64_t weight_stride, int64_t q_stride,
+    const int64_t* kv_strides, int32_t dtype, void* stream) {
+  const char* fn = "sb_qkv_projection_paged";
+  clear_error();
+  if (num_rows == 0) return SB_OK;
+  if (num_rows < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0)
+    return fail(fn, "invalid sizes");
+  if (head_dim % 8 != 0) return fail(fn, "head_dim must be a multiple of 8");
+  if (!q_out || !positions || !kv_cache || !block_table || !kv_strides)
+    return fail(fn, "null pointer argument");
+  if (block_size <= 0) return fail(fn, "block_size must be positive");
+  if (kv_strides[4] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
+  QkvArgs a{};
+  const int64_t qf = num_q_heads * head_dim, kvf = num_kv_heads * head_dim;
+  int rc = qkv_common(fn, &a, hidden, weight, bias, seq_len, hidden_dim, qf + 2 * kvf,
+                      hidden_stride, weight_stride, dtype);
+  if (rc) return rc;
+  if (reinterpret_cast<uintptr_t>(q_out) % 16 || (q_stride * 2) % 16 ||
+      reinterpret_cast<uintptr_t>(kv_cache) % 16 || (kv_strides[0] * 2) % 16 ||
+      (kv_strides[1] * 2) % 16 || (kv_strides[2] * 2) % 16 || (kv_strides[3] * 2) % 16)
+    return fail(fn, "q_out and cache rows must be 16-byte aligned");
+  a.positions = positions;
+  a.num_rows = num_rows;
+  a.q_features = qf;
+  a.kv_features = kvf;
+  a.head_dim = static_cast<int>(head_dim);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (inv_freq) {
+    if (!workspace || reinterpret_cast<uintptr_t>(workspace) % 16)
+      return fail(fn, "RoPE needs a 16-byte aligned workspace");
+    if (workspace_bytes < sb_qkv_projection_paged_workspace_size(num_rows, head_dim, 1))
+      return fail(fn, "workspace too small");
+    float4* table = static_cast<float4*>(workspace);
+    const int64_t n = num_rows * (head_dim / 4);
+    SB_LAUNCH("qkv_rope_table", qkv_rope_table_kernel,
+              dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), st, positions, num_rows,
+              seq_len, inv_freq, static_cast<int>(head_dim / 2), table);
+    rc = check_launch(fn);
+    if (rc) return rc;
+    a.rope_cs = table;
+  }
+  a.out = static_cast<char*>(q_out);
+  a.o_s_row = q_stride * 2;
+  a.kv = static_cast<char*>(kv_cache);
+  a.s_blk = kv_strides[0] * 2;
+  a.s_kv = kv_strides[1] * 2;
+  a.s_head = kv_strides[2] * 2;
+  a.s_pos = kv_strides[3] * 2;
+  a.block_table = block_table;
+  a.block_size = block_size;
+  a.nb_total = num_blocks_total;
+  a.nb_per_seq = num_blocks_per_seq;
+  return launch_qkv<QKV_SPLIT>(fn, a, dtype, st);
+}
+
+extern "C" int64_t sb_masked_qkv_projection_workspace_size(int64_t seq_len) {
+  return (seq_len + 1) * static_cast<int64_t>(sizeof(int32_t));
+}
+
+extern "C" int sb_masked_qkv_projection(void* out, const void* hidden, const void* weight,
+                                        const void* bias, const uint8_t* compute_mask,
+                                        void* workspace, int64_t workspace_bytes,
+                                        int64_t seq_len, int64_t hidden_dim,
+                                        int64_t out_features, int64_t hidden_stride,
+                                        int64_t weight_stride, int64_t out_stride,
+                                        int32_t dtype, void* stream) {
+  const char* fn = "sb_masked_qkv_projection";
+  clear_error();
+  if (seq_len == 0) return SB_OK;
+  if (seq_len < 0) return fail(fn, "invalid sizes");
+  if (!out || !compute_mask || !workspace) return fail(fn, "null pointer argument");
+  if (workspace_bytes < sb_masked_qkv_projection_workspace_size(seq_len))
+    return fail(fn, "workspace too small");
+  QkvArgs a{};
+  int rc = qkv_common(fn, &a, hidden, weight, bias, seq_len, hidden_dim, out_features,
+                      hidden_stride, weight_stride, dtype);
+  if (rc) return rc;
+  if (reinterpret_cast<uintptr_t>(out) % 16 || (out_stride * 2) % 16)
+    return fail(fn, "output rows must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int32_t* pos = static_cast<int32_t*>(workspace);
+  // Reuse rows are zero (the reference multiplies them by the mask); computed rows are
+  // written by the projection.
+  const int vpr = static_cast<int>(out_features * 2 / 8);
+  const int64_t total = seq_len * vpr;
+  SB_LAUNCH("zero_rows", zero_rows_kernel<8>, dim3(static_cast<unsigned>((total + 255) / 256)),
+            dim3(256), st, static_cast<char*>(out), compute_mask, int64_t{1}, seq_len,
+            int64_t{0}, out_stride * 2, vpr);
+  SB_LAUNCH("mask_compact", mask_compact_kernel<0>, dim3(1), dim3(1024), st, compute_mask,
+            seq_len, pos, pos + seq_len);
+  rc = check_launch(fn);
+  if (rc) return rc;
+  a.positions = pos;
+  a.count = pos + seq_len;
+  a.num_rows = seq_len;
+  a.q_features = out_features;  // every feature goes to the dense row; no RoPE
+  a.kv_features = 0;
+  a.head_dim = 8;
+  a.out = static_cast<char*>(out);
+  a.o_s_row = out_stride * 2;
+  return launch_qkv<QKV_DENSE>(fn, a, dtype, st);
+}

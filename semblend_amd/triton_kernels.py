@@ -5,14 +5,16 @@ The module keeps the reference's names, signatures, defaults and return conventi
 
 * ``scatter_donor_kv`` / ``scatter_donor_kv_paged`` — donor KV copied into the target cache,
   in place, bit-exact (HIP row mover, 16-byte vector loads);
-* ``masked_qkv_projection`` — projection for compute rows only, reuse rows zero;
+* ``masked_qkv_projection`` — projection for compute rows only, reuse rows zero (bf16/fp16:
+  a compacted MFMA GEMM over the computed rows only; fp32: torch's GEMM, as the reference);
 * ``partial_prefill_attention`` — causal attention for compute rows only, zero elsewhere
   (bf16/fp16 MFMA kernel with an fp32 online softmax; fp32 inputs take an fp32 kernel);
 * ``partial_prefill`` / ``PartialPrefillResult`` — the single-layer orchestrator.
 
 Extensions with no reference counterpart: ``scatter_donor_kv_paged_layers`` (many layers in
-one launch) and ``partial_prefill_attention_paged`` (GQA over a paged cache for a compact
-set of query rows). CPU tensors are rejected: the kernels exist only for HIP devices.
+one launch), ``partial_prefill_attention_paged`` (GQA over a paged cache for a compact set of
+query rows) and ``qkv_projection_paged`` (compacted GQA projection that writes the new K/V
+into the paged cache, optionally with RoPE at the new positions). CPU tensors are rejected: the kernels exist only for HIP devices.
 """
 
 from __future__ import annotations
@@ -37,6 +39,7 @@ __all__ = [
     "partial_prefill",
     "partial_prefill_attention",
     "partial_prefill_attention_paged",
+    "qkv_projection_paged",
     "scatter_donor_kv",
     "scatter_donor_kv_paged",
     "scatter_donor_kv_paged_layers",
@@ -180,6 +183,12 @@ def scatter_donor_kv_paged_layers(
 # Masked QKV projection
 # ------------------------------------------------------------------------------------------
 
+def _mfma_rows_ok(*ts: torch.Tensor) -> bool:
+    """Row-major 2-D operands the MFMA projection can stream (16-byte aligned rows)."""
+    return all(t.dim() == 2 and t.stride(1) == 1 and t.data_ptr() % 16 == 0
+               and (t.stride(0) * t.element_size()) % 16 == 0 for t in ts)
+
+
 def masked_qkv_projection(
     hidden_states: torch.Tensor,
     qkv_weight: torch.Tensor,
@@ -189,18 +198,114 @@ def masked_qkv_projection(
     """QKV projection whose reuse rows (compute_mask == False) are zero.
 
     hidden_states [seq_len, hidden]; qkv_weight [3 * H * D, hidden]; output
-    [seq_len, 3 * H * D] in the input dtype. The product is a plain GEMM, so it runs on
-    hipBLASLt through torch in fp32 (the reference's rounding, which projects in fp32 and casts
-    back, semblend_core/triton_kernels.py:511-520). Reference: :451-522.
+    [seq_len, 3 * H * D] in the input dtype, accumulated in fp32 and rounded once (the
+    reference projects in fp32 and casts back, semblend_core/triton_kernels.py:511-520).
+    bf16 / fp16 with a hidden size that is a multiple of 64 run ``sb_masked_qkv_projection``:
+    the mask is compacted on the device and only the computed rows are multiplied (MFMA);
+    other cases run torch's GEMM in fp32 on the device, as the reference's fallback does.
+    Reference: :451-522.
     """
-    _lib.require_device(hidden_states, qkv_weight)
+    dev = _lib.require_device(hidden_states, qkv_weight)
+    seq_len, hidden = hidden_states.shape
+    out_features = qkv_weight.shape[0]
+    dt = hidden_states.dtype
+    mask = compute_mask.to(device=dev)
+    if (dt in (torch.bfloat16, torch.float16) and qkv_weight.dtype == dt
+            and (qkv_bias is None or qkv_bias.dtype == dt) and hidden % 64 == 0
+            and out_features % 8 == 0 and seq_len > 0
+            and _mfma_rows_ok(hidden_states, qkv_weight)):
+        out = torch.empty((seq_len, out_features), dtype=dt, device=dev)
+        mask_u8 = (mask if mask.dtype == torch.bool else mask != 0).contiguous().view(torch.uint8)
+        bias = None if qkv_bias is None else qkv_bias.contiguous()
+        ws_bytes = _lib.size_query("sb_masked_qkv_projection_workspace_size", seq_len)
+        ws = torch.empty(ws_bytes // 4, dtype=torch.int32, device=dev)
+        with torch.cuda.device(dev):
+            _lib.call(
+                "sb_masked_qkv_projection",
+                out.data_ptr(), hidden_states.data_ptr(), qkv_weight.data_ptr(), _lib.ptr(bias),
+                mask_u8.data_ptr(), ws.data_ptr(), ws_bytes, seq_len, hidden, out_features,
+                hidden_states.stride(0), qkv_weight.stride(0), out.stride(0),
+                _lib.dtype_code(hidden_states), _lib.stream_handle(dev),
+            )
+        return out
     projected = torch.nn.functional.linear(
         hidden_states.float(),
         qkv_weight.float(),
         qkv_bias.float() if qkv_bias is not None else None,
     )
-    mask = compute_mask.to(device=hidden_states.device).unsqueeze(1).float()
-    return (projected * mask).to(hidden_states.dtype)
+    return (projected * mask.unsqueeze(1).float()).to(dt)
+
+
+def qkv_projection_paged(
+    hidden_states: torch.Tensor,
+    qkv_weight: torch.Tensor,
+    positions: torch.Tensor,
+    kv_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    num_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    qkv_bias: torch.Tensor | None = None,
+    rope_base: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Project only the rows at ``positions`` and write their new K/V into the paged cache.
+
+    hidden_states [S, hidden]; qkv_weight [(Hq + 2 * Hkv) * D, hidden] with features laid out
+    Q | K | V (+ qkv_bias of the same length); kv_cache [NB, 2, Hkv, bs, D] with its block
+    table. Returns Q [R, Hq, D] for the computed rows (``out`` may supply it). With
+    ``rope_base``, Q and K are rotated by their position with the interleaved RoPE of this
+    path before the single rounding. K/V slots out of the table are skipped; a position
+    outside the hidden states gives a zero Q row. bf16 / fp16, hidden a multiple of 64,
+    head_dim a multiple of 8.
+    Fuses the masked projection (semblend_core/triton_kernels.py:451-522) with the K/V write
+    of partial_prefill (:904-909), compacted and paged; no reference counterpart.
+    """
+    from .rope_correction import inv_freq_table
+
+    dev = _lib.require_device(hidden_states, qkv_weight, kv_cache)
+    dt = hidden_states.dtype
+    if dt not in (torch.bfloat16, torch.float16):
+        raise TypeError("qkv_projection_paged runs bf16 / fp16 (the MFMA path)")
+    if qkv_weight.dtype != dt or kv_cache.dtype != dt or (
+            qkv_bias is not None and qkv_bias.dtype != dt):
+        raise TypeError("hidden_states, qkv_weight, qkv_bias and kv_cache must share a dtype")
+    seq_len, hidden = hidden_states.shape
+    features = (num_heads + 2 * num_kv_heads) * head_dim
+    if qkv_weight.shape != (features, hidden):
+        raise ValueError(f"qkv_weight must be [{features}, {hidden}]")
+    if qkv_bias is not None and qkv_bias.shape != (features,):
+        raise ValueError(f"qkv_bias must be [{features}]")
+    nb, two, hkv, bs, d = kv_cache.shape
+    if two != 2 or hkv != num_kv_heads or d != head_dim:
+        raise ValueError("kv_cache must be [num_blocks, 2, num_kv_heads, block_size, head_dim]")
+    if not _mfma_rows_ok(hidden_states, qkv_weight):
+        raise ValueError("hidden_states and qkv_weight need unit-stride, 16-byte aligned rows")
+    pos = _lib.as_index(positions, dev)
+    bt = _lib.as_index(block_table, dev)
+    n = pos.shape[0]
+    if out is None:
+        out = torch.empty((n, num_heads, head_dim), dtype=dt, device=dev)
+    elif out.shape != (n, num_heads, head_dim) or out.dtype != dt or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [R, Hq, D] tensor of the input dtype")
+    if n == 0:
+        return out
+    bias = None if qkv_bias is None else qkv_bias.contiguous()
+    inv = inv_freq_table(rope_base, head_dim, dev) if rope_base is not None else None
+    ws_bytes = _lib.size_query("sb_qkv_projection_paged_workspace_size", n, head_dim,
+                               int(inv is not None))
+    ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "sb_qkv_projection_paged",
+            out.data_ptr(), hidden_states.data_ptr(), qkv_weight.data_ptr(), _lib.ptr(bias),
+            pos.data_ptr(), n, seq_len, hidden, num_heads, num_kv_heads, head_dim,
+            _lib.ptr(inv), ws.data_ptr(), ws_bytes, kv_cache.data_ptr(), bt.data_ptr(), bs, nb,
+            bt.shape[0],
+            hidden_states.stride(0), qkv_weight.stride(0), num_heads * head_dim,
+            _lib.strides(kv_cache), _lib.dtype_code(hidden_states), _lib.stream_handle(dev),
+        )
+    return out
 
 
 # ------------------------------------------------------------------------------------------

@@ -457,6 +457,103 @@ def check_composite_rope_concatenation(impl) -> None:
         assert torch.equal(got[:, 1], plain[:, 1]) and not torch.equal(got[:, 0], plain[:, 0])
 
 
+
+# ------------------------------------------------------------------------------------------
+# Compacted GQA projection with the K/V write (qkv_project_paged)
+# ------------------------------------------------------------------------------------------
+
+def _proj_case(seed, h, hkv, d, hidden, seq=40, nb=6, bs=8, dtype=torch.bfloat16):
+    g = _gen(seed)
+    x = _randn((seq, hidden), seed + 1, dtype)
+    pos = torch.randperm(seq, generator=g)[:17].sort().values.to(torch.int32)
+    bt = torch.randperm(nb + 2, generator=g)[:nb].to(torch.int32)
+    cache = _randn((nb + 2, 2, hkv, bs, d), seed + 2, dtype)
+    return x, pos, bt, cache
+
+
+def check_qkv_projection_mha(impl) -> None:
+    """MHA, no RoPE: the compacted projection equals the reference's masked projection on
+    the computed rows (Q, and the K/V now in the cache), bias included."""
+    h, d, hidden = 4, 8, 24
+    x, pos, bt, cache = _proj_case(70, h, h, d, hidden)
+    w = _randn((3 * h * d, hidden), 73, torch.bfloat16)
+    b = _randn((3 * h * d,), 74, torch.bfloat16)
+    mask = torch.zeros(x.shape[0], dtype=torch.bool)
+    mask[pos.long()] = True
+    dense = impl.masked_qkv_projection(x, w, mask, b)
+    kv = cache.clone()
+    q = impl.qkv_project_paged(x, w, pos, kv, bt, h, h, d, qkv_bias=b)
+    assert torch.equal(q.reshape(len(pos), -1), dense[pos.long(), :h * d])
+    for r, p in enumerate(pos.tolist()):
+        pb, off = int(bt[p // 8]), p % 8
+        assert torch.equal(kv[pb, 0, :, off].reshape(-1), dense[p, h * d:2 * h * d])
+        assert torch.equal(kv[pb, 1, :, off].reshape(-1), dense[p, 2 * h * d:])
+
+
+def check_qkv_projection_layout(impl) -> None:
+    """GQA feature layout and row gather, closed form: with selector weights (Q rows pick
+    -x[j], K rows x[j], V rows 2 x[j + 1]) every output is a copy of an input element, so
+    Q [R, Hq, D], K and V [Hkv, D] per position are fixed exactly; slots past the block
+    table are not written; a position past the hidden states gives a zero Q row."""
+    h, hkv, d, hidden = 4, 2, 8, 40
+    x, pos, bt, cache = _proj_case(80, h, hkv, d, hidden)
+    qf, kf = h * d, hkv * d
+    w = torch.zeros((qf + 2 * kf, hidden))
+    for j in range(qf):
+        w[j, j % hidden] = -1.0
+    for j in range(kf):
+        w[qf + j, j] = 1.0
+        w[qf + kf + j, j + 1] = 2.0
+    w = w.to(torch.bfloat16)
+    pos = torch.cat([pos, torch.tensor([47, x.shape[0]], dtype=torch.int32)])  # 47: past table
+    xx = torch.cat([x, _randn((8, hidden), 81, torch.bfloat16)])  # rows 40..47 exist
+    kv = cache.clone()
+    q = impl.qkv_project_paged(xx, w, pos, kv, bt, h, hkv, d)
+    for r, p in enumerate(pos.tolist()):
+        if p >= xx.shape[0]:
+            assert torch.all(q[r] == 0)
+            continue
+        want_q = torch.stack([-xx[p, j % hidden] for j in range(qf)]).reshape(h, d)
+        assert torch.equal(q[r], want_q)
+        if p // 8 >= bt.shape[0]:
+            continue
+        pb, off = int(bt[p // 8]), p % 8
+        assert torch.equal(kv[pb, 0, :, off], xx[p, :kf].reshape(hkv, d))
+        assert torch.equal(kv[pb, 1, :, off], 2 * xx[p, 1:kf + 1].reshape(hkv, d))
+    # untouched elsewhere: only slots of computed, in-table positions changed
+    written = {(int(bt[p // 8]), p % 8) for p in pos.tolist() if p // 8 < bt.shape[0]}
+    for pb in range(cache.shape[0]):
+        for off in range(8):
+            if (pb, off) not in written:
+                assert torch.equal(kv[pb, :, :, off], cache[pb, :, :, off])
+
+
+def check_qkv_projection_rope(impl) -> None:
+    """RoPE at the new positions: Q and K equal the reference suite's own test rotation
+    (apply_rope_from_scratch, fp32) applied to the unrotated fp32 projection, then rounded;
+    V is not rotated."""
+    h, hkv, d, hidden = 4, 2, 16, 32
+    x, pos, bt, cache = _proj_case(90, h, hkv, d, hidden, seq=60, nb=8)
+    w = _randn((h * d + 2 * hkv * d, hidden), 91, torch.bfloat16)
+    plain_kv = cache.clone()
+    plain = impl.qkv_project_paged(x, w, pos, plain_kv, bt, h, hkv, d)
+    rope_kv = cache.clone()
+    q = impl.qkv_project_paged(x, w, pos, rope_kv, bt, h, hkv, d, rope_base=500.0)
+    xf = x[pos.long()].float()
+    proj = torch.nn.functional.linear(xf, w.float())
+    qf, kf = h * d, hkv * d
+    q32 = proj[:, :qf].reshape(-1, h, d).permute(1, 0, 2)      # [H, R, D]: row i = pos[i]
+    k32 = proj[:, qf:qf + kf].reshape(-1, hkv, d).permute(1, 0, 2)
+    want_q = apply_rope_from_scratch(q32, pos.tolist(), d, 500.0).permute(1, 0, 2)
+    want_k = apply_rope_from_scratch(k32, pos.tolist(), d, 500.0).permute(1, 0, 2)
+    assert torch.equal(q, want_q.to(torch.bfloat16))
+    for r, p in enumerate(pos.tolist()):
+        pb, off = int(bt[p // 8]), p % 8
+        assert torch.equal(rope_kv[pb, 0, :, off], want_k[r].to(torch.bfloat16))
+        assert torch.equal(rope_kv[pb, 1, :, off], plain_kv[pb, 1, :, off])
+    assert not torch.equal(q, plain)
+
+
 ALL_CHECKS = [
     check_rope_reference_cases,
     check_rope_paged_reference_cases,
@@ -473,4 +570,7 @@ ALL_CHECKS = [
     check_projection_and_prefill,
     check_composite_concatenation,
     check_composite_rope_concatenation,
+    check_qkv_projection_mha,
+    check_qkv_projection_layout,
+    check_qkv_projection_rope,
 ]

@@ -21,7 +21,8 @@ from tests import pinning
 API = [
     "apply_rope_delta_inplace", "composite_scatter_paged", "masked_qkv_projection", "nope_permute_paged_kv",
     "partial_attention_paged", "partial_prefill", "partial_prefill_attention",
-    "permute_paged_kv_with_rope", "rope_correct_k", "rope_correct_scatter_paged",
+    "permute_paged_kv_with_rope", "qkv_project_paged", "rope_correct_k",
+    "rope_correct_scatter_paged",
     "scatter_donor_kv", "scatter_donor_kv_paged",
 ]
 
@@ -159,6 +160,47 @@ def _composite_rope_dropped(kv_cache, donor_kvs, block_table, didx, dpos, tpos, 
                                        rope_base)
 
 
+
+def _proj_kv_swapped(hs, w, pos, kv_cache, bt, h, hkv, d, qkv_bias=None, rope_base=None):
+    qf, kf = h * d, hkv * d
+    w2 = torch.cat([w[:qf], w[qf + kf:], w[qf:qf + kf]])
+    b2 = None if qkv_bias is None else torch.cat(
+        [qkv_bias[:qf], qkv_bias[qf + kf:], qkv_bias[qf:qf + kf]])
+    return ref.qkv_project_paged(hs, w2, pos, kv_cache, bt, h, hkv, d, b2, rope_base)
+
+
+def _proj_kv_interleaved_per_head(hs, w, pos, kv_cache, bt, h, hkv, d, qkv_bias=None,
+                                  rope_base=None):
+    # reads the K/V rows as [K0 V0 K1 V1 ...] instead of [K0 K1 ... V0 V1 ...]
+    qf, kf = h * d, hkv * d
+    kv_rows = w[qf:qf + 2 * kf].reshape(hkv, 2, d, -1)
+    w2 = torch.cat([w[:qf], kv_rows[:, 0].reshape(kf, -1), kv_rows[:, 1].reshape(kf, -1)])
+    b2 = qkv_bias
+    if qkv_bias is not None:
+        kb = qkv_bias[qf:qf + 2 * kf].reshape(hkv, 2, d)
+        b2 = torch.cat([qkv_bias[:qf], kb[:, 0].reshape(-1), kb[:, 1].reshape(-1)])
+    return ref.qkv_project_paged(hs, w2, pos, kv_cache, bt, h, hkv, d, b2, rope_base)
+
+
+def _proj_rope_on_v(hs, w, pos, kv_cache, bt, h, hkv, d, qkv_bias=None, rope_base=None):
+    q = ref.qkv_project_paged(hs, w, pos, kv_cache, bt, h, hkv, d, qkv_bias, rope_base)
+    if rope_base is not None:
+        bs = kv_cache.shape[3]
+        f = ref.inv_freq(rope_base, d)
+        for p in torch.as_tensor(pos).tolist():
+            if 0 <= p // bs < bt.shape[0]:
+                pb, off = int(bt[p // bs]), p % bs
+                th = float(p) * f
+                kv_cache[pb, 1, :, off] = ref.rotate_interleaved(
+                    kv_cache[pb, 1, :, off], torch.cos(th), torch.sin(th)).to(kv_cache.dtype)
+    return q
+
+
+def _proj_rope_q_skipped(hs, w, pos, kv_cache, bt, h, hkv, d, qkv_bias=None, rope_base=None):
+    ref.qkv_project_paged(hs, w, pos, kv_cache, bt, h, hkv, d, qkv_bias, rope_base)
+    return ref.qkv_project_paged(hs, w, pos, kv_cache.clone(), bt, h, hkv, d, qkv_bias, None)
+
+
 FUNCTION_MUTANTS = {
     "rope_delta_reversed": {"rope_correct_k": _rope_k_delta_reversed},
     "attention_causal_off_by_one": {"partial_prefill_attention": _attn_off_by_one},
@@ -170,6 +212,10 @@ FUNCTION_MUTANTS = {
     "composite_donor_index_ignored": {"composite_scatter_paged": _composite_donor_ignored},
     "composite_last_donor_dropped": {"composite_scatter_paged": _composite_last_donor_dropped},
     "composite_rope_dropped": {"composite_scatter_paged": _composite_rope_dropped},
+    "projection_k_v_swapped": {"qkv_project_paged": _proj_kv_swapped},
+    "projection_kv_interleaved_per_head": {"qkv_project_paged": _proj_kv_interleaved_per_head},
+    "projection_rope_on_v": {"qkv_project_paged": _proj_rope_on_v},
+    "projection_rope_q_skipped": {"qkv_project_paged": _proj_rope_q_skipped},
 }
 
 
