@@ -505,6 +505,14 @@ def projection_section(dev: torch.device, inp, steps: int) -> dict:
     total, n = _lib.kernel_time("qkv_mfma")
     kern_us = 1e3 * total / n
     ms_lib = timed(library, False)
+    wo = (torch.randn((hidden, HQ * D), generator=gd, device=dev) * (HQ * D) ** -0.5).to(
+        torch.bfloat16)
+
+    def layer():
+        tk.partial_prefill_layer_paged(x, w, wo, pos, inp["attn_kv"], inp["block_table"], HQ,
+                                       HKV, D, qkv_bias=b, rope_base=ROPE_BASE)
+
+    ms_layer = timed(layer, False)
     return {
         "rows": rows, "hidden": hidden, "features": feats, "flops": flops,
         "fused": {"ms": round(ms_fused, 4), "tflops": round(flops / (ms_fused * 1e-3) / 1e12, 1)},
@@ -514,6 +522,9 @@ def projection_section(dev: torch.device, inp, steps: int) -> dict:
         "torch_gather_addmm": {"ms": round(ms_lib, 4),
                                "tflops": round(flops / (ms_lib * 1e-3) / 1e12, 1),
                                "what": "x[pos] @ W^T + b via torch (hipBLASLt), no RoPE, no K/V write"},
+        "layer": {"ms": round(ms_layer, 4),
+                  "what": "partial_prefill_layer_paged: projection + K/V write + RoPE, paged "
+                          "GQA attention, output projection (3584 x 3584) of the 2458 rows"},
     }
 
 
@@ -704,7 +715,8 @@ def main() -> int:
     pj = result["projection"]
     log(f"projection: fused {pj['fused']['ms']:.4f} ms ({pj['fused']['tflops']} TFLOP/s), kernel "
         f"{pj['kernel']['avg_us']} us ({pj['kernel']['tflops']} TFLOP/s), torch gather+addmm "
-        f"{pj['torch_gather_addmm']['ms']:.4f} ms ({pj['torch_gather_addmm']['tflops']} TFLOP/s)")
+        f"{pj['torch_gather_addmm']['ms']:.4f} ms ({pj['torch_gather_addmm']['tflops']} TFLOP/s); "
+        f"whole layer {pj['layer']['ms']:.3f} ms")
     log("chunked host-to-device donor load with RoPE on the way")
     result["chunk_load"] = chunk_load_section(dev, inp, 5)
     cl = result["chunk_load"]

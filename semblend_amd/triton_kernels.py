@@ -14,7 +14,9 @@ The module keeps the reference's names, signatures, defaults and return conventi
 Extensions with no reference counterpart: ``scatter_donor_kv_paged_layers`` (many layers in
 one launch), ``partial_prefill_attention_paged`` (GQA over a paged cache for a compact set of
 query rows) and ``qkv_projection_paged`` (compacted GQA projection that writes the new K/V
-into the paged cache, optionally with RoPE at the new positions). CPU tensors are rejected: the kernels exist only for HIP devices.
+into the paged cache, optionally with RoPE at the new positions), and
+``partial_prefill_layer_paged``, one attention layer of partial prefill over a paged cache
+built from those pieces. CPU tensors are rejected: the kernels exist only for HIP devices.
 """
 
 from __future__ import annotations
@@ -39,6 +41,8 @@ __all__ = [
     "partial_prefill",
     "partial_prefill_attention",
     "partial_prefill_attention_paged",
+    "partial_prefill_layer_paged",
+    "PagedLayerResult",
     "qkv_projection_paged",
     "scatter_donor_kv",
     "scatter_donor_kv_paged",
@@ -494,6 +498,54 @@ def partial_prefill_attention_paged_varlen(
 # ------------------------------------------------------------------------------------------
 # Orchestrator
 # ------------------------------------------------------------------------------------------
+
+@dataclass
+class PagedLayerResult:
+    """Result of :func:`partial_prefill_layer_paged`: output [R, out_features] of the computed
+    rows, their query [R, Hq, D] (rotated when RoPE was applied) and attention [R, Hq, D]."""
+
+    output: torch.Tensor
+    query: torch.Tensor
+    attention: torch.Tensor
+
+
+def partial_prefill_layer_paged(
+    hidden_states: torch.Tensor,
+    qkv_weight: torch.Tensor,
+    output_projection: torch.Tensor,
+    compute_positions: torch.Tensor,
+    kv_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    num_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    qkv_bias: torch.Tensor | None = None,
+    output_bias: torch.Tensor | None = None,
+    rope_base: float | None = None,
+    scale: float | None = None,
+) -> PagedLayerResult:
+    """One attention layer of partial prefill, on the paged cache of that layer.
+
+    The reference's single-layer orchestrator (semblend_core/triton_kernels.py:769-923)
+    projects every row, runs MHA attention over a contiguous cache assembled per call and
+    writes the new K/V into every layer. Here, per layer and for the computed rows only:
+    (1) ``qkv_projection_paged`` — Q of the computed rows, their new K/V (RoPE at their
+    positions when ``rope_base`` is given) written into this layer's paged cache, whose other
+    slots already hold the scattered, RoPE-corrected donor K/V; (2) GQA attention of those
+    rows over the cache (``partial_prefill_attention_paged``); (3) the output projection of
+    the attention rows (torch's GEMM, fp32 accumulation, rounded to the input dtype). A model
+    runs this once per layer with that layer's weights and cache.
+    """
+    dev = _lib.require_device(hidden_states, qkv_weight, output_projection, kv_cache)
+    q = qkv_projection_paged(hidden_states, qkv_weight, compute_positions, kv_cache,
+                             block_table, num_heads, num_kv_heads, head_dim, qkv_bias=qkv_bias,
+                             rope_base=rope_base)
+    pos = _lib.as_index(compute_positions, dev)
+    attn = partial_prefill_attention_paged(q, kv_cache, block_table, pos, scale=scale)
+    flat = attn.reshape(attn.shape[0], num_heads * head_dim)
+    out = torch.nn.functional.linear(flat, output_projection, output_bias)
+    return PagedLayerResult(output=out, query=q, attention=attn)
+
 
 @dataclass
 class PartialPrefillResult:

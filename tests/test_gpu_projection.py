@@ -178,3 +178,41 @@ def test_projection_paged_rejects(dev):
         tk.qkv_projection_paged(x.float(), w.float(), pos, cache.float(), bt, 2, 2, 16)
     with pytest.raises(ValueError):
         tk.qkv_projection_paged(x, w[:-16], pos, cache, bt, 2, 2, 16)
+
+
+def test_partial_prefill_layers_paged(dev):
+    """Two layers of partial prefill over their own paged caches (Qwen2.5-0.5B attention
+    shape, bias, RoPE theta 1e6), each stage against the oracle: the projection to its bar,
+    the attention over the oracle-written cache to the attention bar (2e-2), and the output
+    projection within 2e-2 * sum_k |Wo[j, k]| + 1 ulp (the attention bar carried through the
+    linear map)."""
+    hq, hkv, d, hidden, seq = 14, 2, 64, 896, 400
+    x = randn((seq, hidden), torch.bfloat16, 60)
+    pos = torch.randperm(seq, generator=gen(61))[:90].sort().values.to(torch.int32)
+    nbs = (seq + 15) // 16
+    bt = torch.randperm(nbs + 3, generator=gen(62))[:nbs].to(torch.int32)
+    for layer in range(2):
+        s0 = 70 + 10 * layer
+        f = (hq + 2 * hkv) * d
+        w = (randn((f, hidden), torch.float32, s0) * hidden ** -0.5).to(torch.bfloat16)
+        b = randn((f,), torch.bfloat16, s0 + 1)
+        wo = (randn((hidden, hq * d), torch.float32, s0 + 2) * (hq * d) ** -0.5).to(
+            torch.bfloat16)
+        bo = randn((hidden,), torch.bfloat16, s0 + 3)
+        cache = randn((nbs + 3, 2, hkv, 16, d), torch.bfloat16, s0 + 4)  # donor K/V stand-in
+        kv_dev = cache.to(dev)
+        res = tk.partial_prefill_layer_paged(
+            x.to(dev), w.to(dev), wo.to(dev), pos.to(dev), kv_dev, bt.to(dev), hq, hkv, d,
+            qkv_bias=b.to(dev), output_bias=bo.to(dev), rope_base=1e6)
+        want_kv = cache.clone()
+        want_q = ref.qkv_project_paged(x, w, pos, want_kv, bt, hq, hkv, d, qkv_bias=b,
+                                       rope_base=1e6)
+        ad = _pair_sum(_absdot(x[pos.long()], w)[:, :hq * d]).reshape(want_q.shape)
+        _assert_proj_close(res.query, want_q, ad, f"layer {layer} Q")
+        want_attn = ref.partial_attention_paged(want_q, want_kv, bt, pos)
+        assert float((res.attention.cpu().float() - want_attn).abs().max()) <= 2e-2
+        want_out = torch.nn.functional.linear(want_attn.reshape(len(pos), -1).to(
+            torch.bfloat16).float(), wo.float(), bo.float())
+        bound = 2e-2 * wo.float().abs().sum(dim=1) + _ulp16(want_out.abs(), torch.bfloat16)
+        diff = (res.output.cpu().float() - want_out).abs()
+        assert bool((diff <= bound).all()), float((diff - bound).max())
