@@ -210,3 +210,20 @@ def test_composite_rejects_bad_inputs(dev):
     with pytest.raises(ValueError):   # duplicate targets in a mapping
         composite_scatter_paged(cache[0], [donor[0][0]], bt,
                                 MultiDonorPositionMapping(("a", "a"), (0, 1), (3, 3)))
+
+
+def test_composite_empty_inputs(dev):
+    """No pairs, or pairs that all name no donor, leave the caches untouched."""
+    h, d, dtype = 2, 64, torch.bfloat16
+    base = [randn((8, 2, h, 16, d), dtype, 400 + l).to(dev) for l in range(2)]
+    caches = [c.clone() for c in base]
+    donors = [[randn((2, h, 32, d), dtype, 410 + l).to(dev) for l in range(2)]]
+    bt = torch.arange(8, dtype=torch.int32, device=dev)
+    empty = torch.zeros(0, dtype=torch.int32, device=dev)
+    composite_scatter_paged_layers(caches, donors, bt, empty, empty, empty)
+    bad = torch.tensor([1, 5, -1], dtype=torch.int32, device=dev)     # no such donors
+    pos = torch.tensor([0, 1, 2], dtype=torch.int32, device=dev)
+    composite_scatter_paged_layers(caches, donors, bt, bad, pos, pos)
+    composite_scatter_paged(caches[0], [donors[0][0]], bt, MultiDonorPositionMapping())
+    for a, b in zip(caches, base):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))

@@ -126,3 +126,25 @@ def test_loader_rejects_bad_chunks(dev):
         loader.load([torch.zeros((2, 3, 16, 512), dtype=torch.bfloat16).pin_memory()], d, d)
     with pytest.raises(TypeError):
         loader.load([torch.zeros((2, 2, 16, 512), dtype=torch.float16).pin_memory()], d, d)
+
+
+def test_loader_no_pairs_and_unread_chunks(dev):
+    """A load whose pairs all lie outside the chunks changes nothing; chunks no pair reads
+    are skipped (only the read chunk's rows land)."""
+    donors, caches, bt = _setup(torch.bfloat16, layers=2, donor_len=600)
+    kv = [c.to(dev) for c in caches]
+    loader = ChunkedKVLoader(kv, bt.to(dev), chunk_tokens=256, slots=2)
+    chunks = _host_chunks(donors, 256)
+    loader.load(chunks, torch.tensor([700, -3], dtype=torch.int32),
+                torch.tensor([1, 2], dtype=torch.int32))
+    loader.load(chunks, torch.zeros(0, dtype=torch.int32), torch.zeros(0, dtype=torch.int32))
+    for a, b in zip(kv, caches):
+        assert torch.equal(a.cpu().view(torch.int16), b.view(torch.int16))
+    d = torch.arange(300, 310, dtype=torch.int32)          # chunk 1 only
+    t = torch.arange(40, 50, dtype=torch.int32)
+    loader.load(chunks, d, t)
+    want = [c.to(dev) for c in caches]
+    rc.rope_correct_scatter_paged_layers(want, [x.to(dev) for x in donors], bt.to(dev),
+                                         d.to(dev), t.to(dev), rope_base=10000.0)
+    for a, b in zip(kv, want):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))

@@ -216,3 +216,13 @@ def test_partial_prefill_layers_paged(dev):
         bound = 2e-2 * wo.float().abs().sum(dim=1) + _ulp16(want_out.abs(), torch.bfloat16)
         diff = (res.output.cpu().float() - want_out).abs()
         assert bool((diff <= bound).all()), float((diff - bound).max())
+
+
+def test_projection_zero_rows(dev):
+    x = randn((32, 128), torch.bfloat16, 90).to(dev)
+    w = randn(((4 + 2 * 2) * 32, 128), torch.bfloat16, 91).to(dev)
+    cache = torch.zeros((4, 2, 2, 16, 32), dtype=torch.bfloat16, device=dev)
+    bt = torch.arange(2, dtype=torch.int32, device=dev)
+    q = tk.qkv_projection_paged(x, w, torch.zeros(0, dtype=torch.int32, device=dev), cache, bt,
+                                4, 2, 32, rope_base=1e4)
+    assert q.shape == (0, 4, 32) and torch.all(cache == 0)
