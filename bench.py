@@ -184,6 +184,25 @@ def copy_ceiling(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> fl
     return gbps
 
 
+def gemm_ceiling(dev: torch.device, n: int = 8192, reps: int = 10) -> float:
+    """Achievable dense bf16 matrix-core rate of a large square library GEMM (torch matmul,
+    hipBLASLt), TFLOP/s: the practical ceiling next to the 2516.6 TFLOP/s spec figure."""
+    g = torch.Generator(dev).manual_seed(9)
+    a = torch.randn((n, n), generator=g, device=dev, dtype=torch.bfloat16)
+    b = torch.randn((n, n), generator=g, device=dev, dtype=torch.bfloat16)
+    c = torch.matmul(a, b)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        torch.matmul(a, b, out=c)
+    e1.record()
+    torch.cuda.synchronize()
+    tflops = 2.0 * n ** 3 * reps / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    del a, b, c
+    return tflops
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -635,6 +654,7 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall0
     copy_gbps = copy_ceiling(dev)
+    gemm_tflops = gemm_ceiling(dev)
     log("kernels (avg us): " + ", ".join(f"{k} {v['avg_us']}" for k, v in kernels.items())
         + f"; copy ceiling {copy_gbps:.0f} GB/s")
     ms = {name: [a.elapsed_time(b) for a, b in pairs] for name, pairs in ev.items()}
@@ -699,6 +719,9 @@ def main() -> int:
                      "kernel_gbps": round(rope_bytes / (kernels["rope_rows"]["avg_us"] * 1e-6) / 1e9, 1),
                      "traffic_bytes": MEASURED_TRAFFIC_BYTES["rope_rows"],
                      "frac_of_peak": round(rope_gbps / HBM_PEAK_GBS, 4)},
+            "gemm_ceiling": {"tflops": round(gemm_tflops, 1),
+                             "frac_of_peak": round(gemm_tflops / BF16_PEAK_TFLOPS, 4),
+                             "what": "8192^3 bf16 torch matmul (hipBLASLt), 10 repeats"},
             "copy_ceiling": {"gbps": round(copy_gbps, 1),
                              "frac_of_peak": round(copy_gbps / HBM_PEAK_GBS, 4),
                              "what": "1 GiB device-to-device copy (torch copy_), 10 repeats"},
