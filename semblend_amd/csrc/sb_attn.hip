@@ -722,7 +722,7 @@ attn_mfma_kernel(const AttnBatch batch) {
 //   M = max_c m_c,  O = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.
 // One workgroup per (32 rows of a row tile, KV head); 8 threads per row, each owning D / 8
 // output elements, so the partial reads of a row are spread over 8 lanes.
-template <int DT>
+template <int DT, int D>
 __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnBatch batch) {
   __shared__ int red[4];
   AttnArgs a = batch.a;
@@ -763,42 +763,46 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnBatch batch) 
   if (p < 0) return;
   if (p >= a.kv_len) p = static_cast<int>(a.kv_len - 1);
   const int64_t qrow = a.q_by_position ? p : pi;
-  const int D = a.head_dim;
-  const int dpt = D / 8;
-  const int d_begin = (tid % 8) * dpt;
+  constexpr int DPT = D / 8;  // values per lane (8 lanes per row)
+  const int d_begin = (tid % 8) * DPT;
   const int64_t base = (static_cast<int64_t>(kvh) * a.n_tiles + tile) * a.max_chunks;
   float mmax = -INFINITY;
   for (int ch = 0; ch < nchunks; ++ch)
     mmax = fmaxf(mmax, a.part_ml[((base + ch) * TR + row_in_tile) * 2]);
+  // Each chunk's DPT values are loaded together (one 16-byte load per four), then weighted.
+  float acc[DPT];
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) acc[e] = 0.f;
   float lsum = 0.f;
   for (int ch = 0; ch < nchunks; ++ch) {
-    const float2 ml =
-        *reinterpret_cast<const float2*>(a.part_ml + ((base + ch) * TR + row_in_tile) * 2);
-    if (ml.x != -INFINITY) lsum += __builtin_amdgcn_exp2f(ml.x - mmax) * ml.y;
+    const int64_t slot = (base + ch) * TR + row_in_tile;
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + slot * 2);
+    if (ml.x == -INFINITY) continue;
+    const float w = __builtin_amdgcn_exp2f(ml.x - mmax);
+    lsum += w * ml.y;
+    float4 v[DPT / 4];
+#pragma unroll
+    for (int q = 0; q < DPT / 4; ++q)
+      v[q] = *reinterpret_cast<const float4*>(a.part_o + slot * D + d_begin + 4 * q);
+#pragma unroll
+    for (int q = 0; q < DPT / 4; ++q) {
+      acc[4 * q] += w * v[q].x;
+      acc[4 * q + 1] += w * v[q].y;
+      acc[4 * q + 2] += w * v[q].z;
+      acc[4 * q + 3] += w * v[q].w;
+    }
   }
   const float inv = 1.f / lsum;
   char* op = a.o + qrow * a.o_s_row + qh * a.o_s_head;
-  for (int d = d_begin; d < d_begin + dpt; d += 4) {
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int ch = 0; ch < nchunks; ++ch) {
-      const int64_t slot = (base + ch) * TR + row_in_tile;
-      const float m = a.part_ml[slot * 2];
-      if (m == -INFINITY) continue;
-      const float w = __builtin_amdgcn_exp2f(m - mmax);
-      const float4 v = *reinterpret_cast<const float4*>(a.part_o + slot * D + d);
-      acc.x += w * v.x; acc.y += w * v.y; acc.z += w * v.z; acc.w += w * v.w;
-    }
-    const uint32_t w0 = static_cast<uint32_t>(Mma<DT>::cvt1(acc.x * inv)) |
-                        (static_cast<uint32_t>(Mma<DT>::cvt1(acc.y * inv)) << 16);
-    const uint32_t w1 = static_cast<uint32_t>(Mma<DT>::cvt1(acc.z * inv)) |
-                        (static_cast<uint32_t>(Mma<DT>::cvt1(acc.w * inv)) << 16);
-    *reinterpret_cast<uint2*>(op + d * 2) = make_uint2(w0, w1);
+#pragma unroll
+  for (int q = 0; q < DPT / 4; ++q) {
+    const uint32_t w0 = static_cast<uint32_t>(Mma<DT>::cvt1(acc[4 * q] * inv)) |
+                        (static_cast<uint32_t>(Mma<DT>::cvt1(acc[4 * q + 1] * inv)) << 16);
+    const uint32_t w1 = static_cast<uint32_t>(Mma<DT>::cvt1(acc[4 * q + 2] * inv)) |
+                        (static_cast<uint32_t>(Mma<DT>::cvt1(acc[4 * q + 3] * inv)) << 16);
+    *reinterpret_cast<uint2*>(op + (d_begin + 4 * q) * 2) = make_uint2(w0, w1);
   }
 }
-
-// ---------------------------------------------------------------------------------------
-// VALU path: any dtype, any head_dim. One wave per (row, q-head).
-// ---------------------------------------------------------------------------------------
 template <int DT>
 __device__ __forceinline__ float load_elem(const char* p, int64_t idx) {
   if (DT == SB_DTYPE_F32) return reinterpret_cast<const float*>(p)[idx];
@@ -957,7 +961,7 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
   if (dtype == DT && a.head_dim == D) {                                                 \
     SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(kThreads), st, one); \
     if (pl.max_chunks > 1)                                                              \
-      SB_LAUNCH("attn_merge", (attn_merge_kernel<DT>), mgrid, dim3(256), st, one);      \
+      SB_LAUNCH("attn_merge", (attn_merge_kernel<DT, D>), mgrid, dim3(256), st, one);   \
     return check_launch(fn);                                                            \
   }
     SB_ATT_CASE(SB_DTYPE_BF16, 128)
@@ -1098,7 +1102,7 @@ int launch_attention_varlen(const char* fn, AttnArgs a, int32_t dtype, int64_t n
 #define SB_ATT_VCASE(DT, D)                                                             \
   if (dtype == DT && a.head_dim == D) {                                                 \
     SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(kThreads), st, b); \
-    if (split) SB_LAUNCH("attn_merge", (attn_merge_kernel<DT>), mgrid, dim3(256), st, b); \
+    if (split) SB_LAUNCH("attn_merge", (attn_merge_kernel<DT, D>), mgrid, dim3(256), st, b); \
     const int rc = check_launch(fn);                                                    \
     if (rc) return rc;                                                                  \
     continue;                                                                           \
