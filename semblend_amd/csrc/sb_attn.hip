@@ -47,6 +47,16 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWaveRows = 32;   // flattened query rows per MFMA row group
+// Wave priority (s_setprio) raised around the PV MFMA burst, so that of the two waves on a
+// SIMD the one with MFMAs ready issues first while the other forms P on the VALUs (3% on the
+// 7B workload: 368 -> 357 us); raising it around the QK MFMA + softmax block instead was
+// slower. 0 turns either off.
+#ifndef SB_ATTN_PV_PRIO
+#define SB_ATTN_PV_PRIO 2
+#endif
+#ifndef SB_ATTN_QK_PRIO
+#define SB_ATTN_QK_PRIO 0
+#endif
 #ifndef SB_ATTN_ROW_GROUPS
 #define SB_ATTN_ROW_GROUPS 1
 #endif
@@ -594,6 +604,9 @@ attn_mfma_kernel(const AttnBatch batch) {
       fill_offsets(it % 3, t0 + 3 * kTileKeys, wave * (kTileKeys / kWaves) + lane);
     const bool live = t0 <= pmax_c;
     // ---- S(it+1) on the matrix cores while P(it) is formed on the vector ALUs ----
+#if SB_ATTN_QK_PRIO
+    __builtin_amdgcn_s_setprio(SB_ATTN_QK_PRIO);
+#endif
     if (NEXT) qk((it + 1) & 1, s_nxt);
     bool bad_any = false;
     bool bad[RG];
@@ -614,6 +627,9 @@ attn_mfma_kernel(const AttnBatch batch) {
         __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
       }
     }
+#if SB_ATTN_QK_PRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
     if (NEXT) mask(t0 + kTileKeys, s_nxt);
     // ---- rare: seed the reference with the first live tile's max, or move it up when a
     // tile would push P past kPMax; O and l are rescaled by 2^(m_old - m_new) and the
@@ -652,6 +668,9 @@ attn_mfma_kernel(const AttnBatch batch) {
     for (int g = 0; g < RG; ++g) l_run[g] += tsum[g];
     // ---- O^T += V^T P^T; V fragments stream through a 4-deep ring ----
     if (live) {
+#if SB_ATTN_PV_PRIO
+      __builtin_amdgcn_s_setprio(SB_ATTN_PV_PRIO);
+#endif
       constexpr int NV = 2 * kHalves * NDT;  // (half, step, d-tile) triples
       const int vb = it & 1;
       vec8 vring[4];
@@ -665,6 +684,9 @@ attn_mfma_kernel(const AttnBatch batch) {
 #pragma unroll
         for (int g = 0; g < RG; ++g) o[g][t] = M::mma(va, pb[g][j][st], o[g][t]);
       }
+#if SB_ATTN_PV_PRIO
+      __builtin_amdgcn_s_setprio(0);
+#endif
     }
     if (NEXT) {
 #pragma unroll
