@@ -54,6 +54,11 @@ constexpr int kWaveRows = 32;   // flattened query rows per MFMA row group
 #ifndef SB_ATTN_PV_PRIO
 #define SB_ATTN_PV_PRIO 2
 #endif
+// VALU instructions scheduled after each QK MFMA (and its fragment read) in the block that
+// forms P(it) under S(it+1) (3, 4, 6 and 8 measured within noise of 5).
+#ifndef SB_ATTN_IL_VALU
+#define SB_ATTN_IL_VALU 5
+#endif
 #ifndef SB_ATTN_QK_PRIO
 #define SB_ATTN_QK_PRIO 0
 #endif
@@ -624,7 +629,7 @@ attn_mfma_kernel(const AttnBatch batch) {
       for (int n = 0; n < kHalves * NKS; ++n) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, SB_ATTN_IL_VALU, 0);  // VALU
       }
     }
 #if SB_ATTN_QK_PRIO
