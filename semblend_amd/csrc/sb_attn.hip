@@ -358,7 +358,7 @@ attn_mfma_kernel(const AttnBatch batch) {
   __shared__ int red_max[kWaves];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
   const int lane = tid & 63;
   const int lq = lane & 31;
   const int lg = lane >> 5;
@@ -481,22 +481,23 @@ attn_mfma_kernel(const AttnBatch batch) {
   // instruction fills 1 KB of consecutive 16-byte slots; every lane fetches the chunk that
   // the swizzled layout puts in its slot). Loads are unconditional: every offset is a valid
   // row.
-  auto load_rows = [&](const char* base, const uint64_t* ofs, uint16_t* dst, bool is_k) {
+  // Slot q * kThreads + tid of a tile holds row q * (kThreads / CH) + tid / CH at position
+  // tid % CH; both swizzles depend on the row modulo 16 only, so the 16-byte chunk a lane
+  // fetches is the same for every q: one source pointer per lane for K and one for V.
+  static_assert((kThreads / CH) % 16 == 0, "swizzle independent of the load index");
+  const char* ksrc = kbase + 16 * kswz<CH>(tid / CH, tid % CH);
+  const char* vsrc = vbase + 16 * vswz<CH>(tid / CH, tid % CH);
+  auto load_rows = [&](const char* src, const uint64_t* ofs, uint16_t* dst) {
     // All row offsets first (back-to-back LDS reads, one wait), then the loads.
     uint64_t ro[NLD];
 #pragma unroll
     for (int q = 0; q < NLD; ++q) ro[q] = ofs[(q * kThreads + tid) / CH];
 #pragma unroll
-    for (int q = 0; q < NLD; ++q) {
-      const int sl = q * kThreads + tid;     // 16-byte slot within the tile
-      const int row = sl / CH;
-      const int pos = sl % CH;
-      const int chunk = is_k ? kswz<CH>(row, pos) : vswz<CH>(row, pos);
-      dma_row_chunk(base + ro[q] + 16 * chunk, dst + (q * kThreads + wave * 64) * 8);
-    }
+    for (int q = 0; q < NLD; ++q)
+      dma_row_chunk(src + ro[q], dst + (q * kThreads + wave * 64) * 8);
   };
-  auto load_k = [&](int slot, int stage) { load_rows(kbase, kofs[slot], Ks[stage], true); };
-  auto load_v = [&](int slot, int stage) { load_rows(vbase, vofs[slot], Vs[stage], false); };
+  auto load_k = [&](int slot, int stage) { load_rows(ksrc, kofs[slot], Ks[stage]); };
+  auto load_v = [&](int slot, int stage) { load_rows(vsrc, vofs[slot], Vs[stage]); };
 
   // K fragment of (half n % kHalves, k-step n / kHalves): key row 32 * half + lq, 16-byte
   // chunk 2 * kstep + lg.
