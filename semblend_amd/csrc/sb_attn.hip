@@ -115,6 +115,8 @@ struct AttnArgs {
   int64_t block_size, nb_total, nb_per_seq;
   int bs_log2;                // log2(block_size) when a power of two, else -1
   int64_t s_block, s_pos;     // paged byte strides (shared by K and V)
+  int narrow_ofs;             // power-of-two blocks, s_block < 2^32, s_pos and block_size
+                              // < 2^24: key offsets by one 32 x 32 -> 64-bit multiply-add
   int64_t kv_len;             // addressable keys
   int num_kv_heads;
   int group;                  // q heads per kv head
@@ -438,15 +440,25 @@ attn_mfma_kernel(const AttnBatch batch) {
   }
   const char* kbase = a.k + kvh * a.k_s_head;
   const char* vbase = a.v + kvh * a.v_s_head;
-  // Byte offsets of key `key` (clamped into [k0, k1)) relative to kbase / vbase.
+  // Byte offsets of key `key` (clamped into [k0, k1)) relative to kbase / vbase. Paged K
+  // and V rows share one offset, kept in kofs only.
   auto fill_offsets = [&](int slot, int t0, int i) {
     const int key = min(t0 + i, k1 - 1);
     if (a.paged) {
-      const int lb = a.bs_log2 >= 0 ? key >> a.bs_log2 : key / static_cast<int>(a.block_size);
-      const uint64_t off = static_cast<uint64_t>(bt_s[lb - lb0]) * a.s_block +
-                           static_cast<uint64_t>(key - lb * a.block_size) * a.s_pos;
+      uint64_t off;
+      if (a.narrow_ofs) {
+        const int lb = key >> a.bs_log2;
+        const uint32_t in_block =
+            static_cast<uint32_t>(key) & (static_cast<uint32_t>(a.block_size) - 1u);
+        off = static_cast<uint64_t>(static_cast<uint32_t>(bt_s[lb - lb0])) *
+                  static_cast<uint32_t>(a.s_block) +
+              __umul24(in_block, static_cast<uint32_t>(a.s_pos));
+      } else {
+        const int lb = a.bs_log2 >= 0 ? key >> a.bs_log2 : key / static_cast<int>(a.block_size);
+        off = static_cast<uint64_t>(bt_s[lb - lb0]) * a.s_block +
+              static_cast<uint64_t>(key - lb * a.block_size) * a.s_pos;
+      }
       kofs[slot][i] = off;
-      vofs[slot][i] = off;
     } else {
       kofs[slot][i] = static_cast<uint64_t>(key) * a.k_s_seq;
       vofs[slot][i] = static_cast<uint64_t>(key) * a.v_s_seq;
@@ -497,7 +509,9 @@ attn_mfma_kernel(const AttnBatch batch) {
       dma_row_chunk(src + ro[q], dst + (q * kThreads + wave * 64) * 8);
   };
   auto load_k = [&](int slot, int stage) { load_rows(ksrc, kofs[slot], Ks[stage]); };
-  auto load_v = [&](int slot, int stage) { load_rows(vsrc, vofs[slot], Vs[stage]); };
+  auto load_v = [&](int slot, int stage) {
+    load_rows(vsrc, a.paged ? kofs[slot] : vofs[slot], Vs[stage]);
+  };
 
   // K fragment of (half n % kHalves, k-step n / kHalves): key row 32 * half + lq, 16-byte
   // chunk 2 * kstep + lg.
@@ -1302,6 +1316,8 @@ int paged_args(const char* fn, AttnArgs* pa, bool* aligned16, void* out, const v
   a.nb_total = num_blocks_total;
   a.s_block = kvs[0] * es;
   a.s_pos = kvs[3] * es;
+  a.narrow_ofs = a.bs_log2 >= 0 && a.s_block >= 0 && a.s_block <= 0xFFFFFFFFll &&
+                 a.s_pos >= 0 && a.s_pos < (1ll << 24) && block_size < (1ll << 24);
   a.num_kv_heads = static_cast<int>(num_kv_heads);
   a.group = static_cast<int>(num_q_heads / num_kv_heads);
   a.head_dim = static_cast<int>(head_dim);

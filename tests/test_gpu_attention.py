@@ -104,6 +104,27 @@ def test_paged_gqa_mfma(dev, dtype, hq, hkv, d):
     assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
 
 
+@pytest.mark.parametrize("bs", [24, 32, 1])
+def test_paged_gqa_block_sizes(dev, bs):
+    """Block sizes other than 16. 24 is not a power of two, so the block of a key is found
+    by division and its offset with 64-bit products; 1 puts every key in its own block."""
+    q, kv, bt, pos = _paged_case(28, 4, 128, 1500, 200, torch.bfloat16, 80 + bs, bs=bs)
+    got = tk.partial_prefill_attention_paged(q.to(dev), kv.to(dev), bt.to(dev), pos.to(dev))
+    assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
+
+
+def test_paged_gqa_position_major_layout(dev):
+    """A cache stored [blocks, block_size, 2, kv_heads, head_dim] and viewed as
+    [blocks, 2, kv_heads, block_size, head_dim]: the position stride (2·H·D) exceeds the
+    head stride, and K and V of a position sit next to each other."""
+    q, kv, bt, pos = _paged_case(32, 8, 128, 1200, 150, torch.bfloat16, 90)
+    store = kv.permute(0, 3, 1, 2, 4).contiguous()        # [nb, bs, 2, H, D]
+    view = store.to(dev).permute(0, 2, 3, 1, 4)           # [nb, 2, H, bs, D]
+    assert not view.is_contiguous()
+    got = tk.partial_prefill_attention_paged(q.to(dev), view, bt.to(dev), pos.to(dev))
+    assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
+
+
 def test_paged_gqa_unsorted_positions(dev):
     q, kv, bt, pos = _paged_case(28, 4, 128, 1024, 200, torch.bfloat16, 60)
     perm = torch.randperm(pos.shape[0], generator=gen(61))
