@@ -111,6 +111,11 @@ struct MoveArgs {
   int layers_per_group;
   int kv_first;            // first kv plane (0 = K, 1 = V)
   int num_kv;              // 1 or 2 planes
+  // Rotating launches over both planes: grid.y slices [0, k_slices) rotate K in groups of
+  // layers_per_group layers, the rest copy V in groups of v_layers_per_group (0: one
+  // interleaved decode with layers_per_group for both planes).
+  int k_slices;
+  int v_layers_per_group;
   int src_index_check;     // ROW_INDEX source: also require src_pos to be a valid paged slot
   int vpr;                 // vectors per row
   int tpr_log2;            // log2(threads per row)
@@ -256,9 +261,19 @@ __global__ __launch_bounds__(kThreads) void move_rows_kernel(MoveArgs a) {
                     (threadIdx.x >> a.tpr_log2);
   if (i >= a.num_pairs) return;
 
-  const int kv = a.kv_first + static_cast<int>(blockIdx.y % a.num_kv);
-  const int l0 = static_cast<int>(blockIdx.y / a.num_kv) * a.layers_per_group;
-  const int l1 = min(l0 + a.layers_per_group, a.num_layers);
+  int kv, l0, lpg;
+  if (ROT != ROT_NONE && a.k_slices > 0) {
+    const int y = static_cast<int>(blockIdx.y);
+    const bool k_slice = y < a.k_slices;
+    kv = k_slice ? 0 : 1;
+    lpg = k_slice ? a.layers_per_group : a.v_layers_per_group;
+    l0 = (k_slice ? y : y - a.k_slices) * lpg;
+  } else {
+    kv = a.kv_first + static_cast<int>(blockIdx.y % a.num_kv);
+    lpg = a.layers_per_group;
+    l0 = static_cast<int>(blockIdx.y / a.num_kv) * lpg;
+  }
+  const int l1 = min(l0 + lpg, a.num_layers);
 
   RowSide src = a.src;
   int64_t src_off, dst_off;
@@ -599,6 +614,18 @@ RowSide side_index(void* base, int64_t num_heads, int64_t head_dim, int64_t es, 
   return s;
 }
 
+int layers_per_group_for(int64_t num_layers, int64_t num_pairs, bool rope);
+
+// Grid slices of a rotating launch over both planes: K in the rotating path's long layer
+// groups (cos/sin once per group), V in the plain copy's short ones (more slices in flight).
+int split_rope_planes(MoveArgs& a, int64_t num_layers, int64_t num_pairs) {
+  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, true);
+  a.v_layers_per_group = layers_per_group_for(num_layers, num_pairs, false);
+  a.k_slices = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
+  return a.k_slices +
+         static_cast<int>((num_layers + a.v_layers_per_group - 1) / a.v_layers_per_group);
+}
+
 int layers_per_group_for(int64_t num_layers, int64_t num_pairs, bool rope) {
   // Enough grid.y slices to fill the chip when there are few pairs; otherwise walk several
   // layers per thread so index work (and, when rotating, the fp64 cos/sin) is amortised.
@@ -701,7 +728,8 @@ static int paged_scatter_impl(const char* fn, void* kv_base, const uint64_t* kv_
   const int groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (rope)
-    return launch_move<ROT_DELTA, ROW_FLAT_POS, ROW_PAGED_POS>(fn, a, dtype, g, 2 * groups, st);
+    return launch_move<ROT_DELTA, ROW_FLAT_POS, ROW_PAGED_POS>(
+        fn, a, dtype, g, split_rope_planes(a, num_layers, num_pairs), st);
   return launch_move<ROT_NONE, ROW_FLAT_POS, ROW_PAGED_POS>(fn, a, dtype, g, 2 * groups, st);
 }
 
@@ -846,7 +874,8 @@ extern "C" int sb_composite_scatter_paged_layers(
       a.donors.first_pos[k] = d[4];
     }
     const int rc =
-        rope ? launch_move<ROT_DELTA, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, 2 * groups, st)
+        rope ? launch_move<ROT_DELTA, ROW_DONOR_POS, ROW_PAGED_POS>(
+                   fn, a, dtype, g, split_rope_planes(a, num_layers, num_pairs), st)
              : launch_move<ROT_NONE, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, 2 * groups, st);
     if (rc) return rc;
   }
