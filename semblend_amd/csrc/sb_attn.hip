@@ -503,7 +503,7 @@ attn_mfma_kernel(const AttnBatch batch) {
     // All row offsets first (back-to-back LDS reads, one wait), then the loads.
     uint64_t ro[NLD];
 #pragma unroll
-    for (int q = 0; q < NLD; ++q) ro[q] = ofs[(q * kThreads + tid) / CH];
+    for (int q = 0; q < NLD; ++q) ro[q] = ofs[q * (kThreads / CH) + tid / CH];
 #pragma unroll
     for (int q = 0; q < NLD; ++q)
       dma_row_chunk(src + ro[q], dst + (q * kThreads + wave * 64) * 8);
@@ -614,14 +614,17 @@ attn_mfma_kernel(const AttnBatch batch) {
   mask(k0, s_cur);
   __syncthreads();  // K stage 0 is refilled at the top of the first iteration
 
-  auto iteration = [&](int it, auto has_next) {
+  // slot = it mod 3 (offset-table ring), advanced once per tile.
+  auto iteration = [&](int it, int slot, auto has_next) {
     constexpr bool NEXT = decltype(has_next)::value;
     const int t0 = k0 + it * kTileKeys;
-    if (it + 2 < ntiles) load_k((it + 2) % 3, it & 1);
-    if (it + 1 < ntiles) load_v((it + 1) % 3, (it + 1) & 1);
+    const int slot1 = slot == 2 ? 0 : slot + 1;  // (it + 1) mod 3
+    const int slot2 = slot == 0 ? 2 : slot - 1;  // (it + 2) mod 3
+    if (it + 2 < ntiles) load_k(slot2, it & 1);
+    if (it + 1 < ntiles) load_v(slot1, (it + 1) & 1);
     // Offsets of tile it+3: kTileKeys / kWaves entries from each wave.
     if (it + 3 < ntiles && lane < kTileKeys / kWaves)
-      fill_offsets(it % 3, t0 + 3 * kTileKeys, wave * (kTileKeys / kWaves) + lane);
+      fill_offsets(slot, t0 + 3 * kTileKeys, wave * (kTileKeys / kWaves) + lane);
     const bool live = t0 <= pmax_c;
     // ---- S(it+1) on the matrix cores while P(it) is formed on the vector ALUs ----
 #if SB_ATTN_QK_PRIO
@@ -717,8 +720,12 @@ attn_mfma_kernel(const AttnBatch batch) {
     wait_vmem();
     __syncthreads();
   };
-  for (int it = 0; it + 1 < ntiles; ++it) iteration(it, std::true_type{});
-  iteration(ntiles - 1, std::false_type{});
+  int slot = 0;
+  for (int it = 0; it + 1 < ntiles; ++it) {
+    iteration(it, slot, std::true_type{});
+    slot = slot == 2 ? 0 : slot + 1;
+  }
+  iteration(ntiles - 1, slot, std::false_type{});
 
   // ---- finish: lane holds d = 32t + 8*(i/4) + 4*lg + (i%4) of each of its rows ----
 #pragma unroll
@@ -729,16 +736,18 @@ attn_mfma_kernel(const AttnBatch batch) {
     if (nchunks == 1) {
       const float inv = 1.f / l_tot;
       char* op = a.o + qrow[g] * a.o_s_row + qh[g] * a.o_s_head;
+      // Two groups of 4 consecutive d (8 apart) per hardware pack of 8 (round to nearest even).
 #pragma unroll
       for (int t = 0; t < NDT; ++t)
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const int d0 = 32 * t + 8 * qd + 4 * lg;
-          const uint32_t w0 = static_cast<uint32_t>(M::cvt1(o[g][t][4 * qd] * inv)) |
-                              (static_cast<uint32_t>(M::cvt1(o[g][t][4 * qd + 1] * inv)) << 16);
-          const uint32_t w1 = static_cast<uint32_t>(M::cvt1(o[g][t][4 * qd + 2] * inv)) |
-                              (static_cast<uint32_t>(M::cvt1(o[g][t][4 * qd + 3] * inv)) << 16);
-          *reinterpret_cast<uint2*>(op + d0 * 2) = make_uint2(w0, w1);
+        for (int qp = 0; qp < 2; ++qp) {
+          float f[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = o[g][t][8 * qp + e] * inv;
+          const u32x4_t w = __builtin_bit_cast(u32x4_t, M::cvt8(f));
+          const int d0 = 32 * t + 16 * qp + 4 * lg;
+          *reinterpret_cast<uint2*>(op + d0 * 2) = make_uint2(w.x, w.y);
+          *reinterpret_cast<uint2*>(op + (d0 + 8) * 2) = make_uint2(w.z, w.w);
         }
     } else {
       const int64_t slot =
