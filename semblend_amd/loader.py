@@ -144,6 +144,10 @@ class ChunkedKVLoader:
         cur = torch.cuda.current_stream(self.dev)
         side = self.scatter_stream
         side.wait_stream(cur)  # the caches' earlier users and the pair upload come first
+        # Device memory the scatters read on the side stream: marked there, so the caching
+        # allocator does not hand it out again before those reads have run.
+        for t in (pairs, self._kv_tab, self.block_table, self._inv_freq):
+            t.record_stream(side)
         base = pairs.data_ptr()
         # (kv, head, seq) strides of a slot's layer window in elements; then rows, first
         row = self.num_heads * self.head_dim
@@ -164,6 +168,8 @@ class ChunkedKVLoader:
             side.wait_event(self._loaded[s])
             tab = self._slot_tabs[s] if tc == self.chunk_tokens else self._layer_table(
                 self._slots[s], tc)
+            tab.record_stream(side)
+            self._slots[s].record_stream(side)
             strides[0] = self.num_layers * tc * row
             strides[3] = tc
             strides[4] = c * self.chunk_tokens
@@ -177,7 +183,6 @@ class ChunkedKVLoader:
                 raise RuntimeError("sb_composite_scatter_paged_layers failed: "
                                    + lib.sb_last_error_string().decode())
             self._free[s].record(side)
-        pairs.record_stream(side)
         cur.wait_stream(side)
 
     def _chunk_tokens_of(self, ch: torch.Tensor) -> int:
