@@ -381,7 +381,10 @@ def partial_prefill_attention_paged(
     block_table: [num_blocks_per_seq]. Query head h reads KV head
     ``h // (num_q_heads // num_kv_heads)``. Returns [R, num_q_heads, head_dim]:
     ``out[r, h] = softmax(scale * q[r, h] K[0..p_r]^T) V[0..p_r]``.
-    Ascending positions give the best schedule; any order is correct.
+    Ascending positions give the best schedule; any order is correct. Positions belong in
+    ``[0, len(block_table) * block_size)``: one at or past the end attends the whole table,
+    and a row with a negative position is left unwritten (no memory outside the inputs is
+    touched either way).
     Extension with no reference counterpart: the reference attention is MHA over contiguous
     K/V (semblend_core/triton_kernels.py:655-734), gathered from the cache by its callers.
     """

@@ -125,6 +125,29 @@ def test_paged_gqa_position_major_layout(dev):
     assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
 
 
+def test_paged_gqa_no_rows(dev):
+    q, kv, bt, _ = _paged_case(28, 4, 128, 256, 8, torch.bfloat16, 95)
+    got = tk.partial_prefill_attention_paged(q[:0].to(dev), kv.to(dev), bt.to(dev),
+                                             torch.zeros(0, dtype=torch.int32, device=dev))
+    assert got.shape == (0, 28, 128)
+
+
+def test_paged_gqa_long_context_many_chunks(dev):
+    """A 65536-token context with few rows: the planner splits the key range into 512-key
+    chunks to fill the GPU, so the last rows span 128 chunks that the merge combines. Rows
+    at the start, at chunk limits and at the last position, plus random ones."""
+    ctx, bs = 65536, 16
+    nblk = ctx // bs
+    kv = randn((nblk + 3, 2, 1, bs, 128), torch.bfloat16, 96)
+    bt = torch.randperm(nblk + 3, generator=gen(97))[:nblk].to(torch.int32)
+    pos = torch.cat([torch.tensor([0, 1, 16383, 16384, 32767, 49152, 65534, 65535]),
+                     torch.randint(0, ctx, (40,), generator=gen(98))]).unique()
+    pos = pos.sort().values.to(torch.int32)
+    q = randn((pos.shape[0], 8, 128), torch.bfloat16, 99)
+    got = tk.partial_prefill_attention_paged(q.to(dev), kv.to(dev), bt.to(dev), pos.to(dev))
+    assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
+
+
 def test_paged_gqa_unsorted_positions(dev):
     q, kv, bt, pos = _paged_case(28, 4, 128, 1024, 200, torch.bfloat16, 60)
     perm = torch.randperm(pos.shape[0], generator=gen(61))
