@@ -25,11 +25,8 @@ from typing import Sequence
 import torch
 
 from . import _lib
-from .rope_correction import rope_correct_scatter_paged_layers
-from .triton_kernels import (
-    partial_prefill_attention_paged_varlen,
-    scatter_donor_kv_paged_layers,
-)
+from .rope_correction import prepare_scatter_paged_layers
+from .triton_kernels import partial_prefill_attention_paged_varlen
 
 
 @dataclass
@@ -80,6 +77,7 @@ class KVReuseBatch:
                 [_lib.as_index(r.compute_positions, dev) for r in self.requests])
         else:
             self.compute_positions = torch.zeros(0, dtype=torch.int32, device=dev)
+        self._scatter_calls: dict[bool, list] = {}
         self.row_offsets = [0]
         for n in self.rows_per_request:
             self.row_offsets.append(self.row_offsets[-1] + n)
@@ -89,18 +87,20 @@ class KVReuseBatch:
         return self.row_offsets[-1]
 
     def scatter_rope(self, rope: bool = True) -> None:
-        """Donor K/V of every request into every layer's cache (K rotated when ``rope``)."""
-        for r in self.requests:
-            if r.donor_positions.shape[0] == 0:
-                continue
-            if rope:
-                rope_correct_scatter_paged_layers(self.kv_caches, list(r.donor_kvs),
-                                                  r.block_table, r.donor_positions,
-                                                  r.target_positions, rope_base=self.rope_base)
-            else:
-                scatter_donor_kv_paged_layers(self.kv_caches, list(r.donor_kvs),
-                                              r.block_table, r.donor_positions,
-                                              r.target_positions)
+        """Donor K/V of every request into every layer's cache (K rotated when ``rope``).
+
+        The per-request launches are validated and bound on first use (one
+        ``PreparedScatter`` each), so a repeated step costs one C call per request."""
+        calls = self._scatter_calls.get(rope)
+        if calls is None:
+            calls = [prepare_scatter_paged_layers(
+                         self.kv_caches, list(r.donor_kvs), r.block_table, r.donor_positions,
+                         r.target_positions, self.rope_base if rope else None)
+                     for r in self.requests]
+            calls = [c for c in calls if c is not None]
+            self._scatter_calls[rope] = calls
+        for call in calls:
+            call()
 
     def attention(self, layer: int, query: torch.Tensor, scale: float | None = None,
                   out: torch.Tensor | None = None) -> torch.Tensor:

@@ -126,14 +126,51 @@ def rope_correct_scatter_paged_layers(
     with no reference counterpart; it replaces a per-layer loop around
     ``rope_correct_scatter_paged`` (semblend/integration/trtllm/pytorch_backend.py:106-154).
     """
+    call = prepare_scatter_paged_layers(kv_caches, donor_kvs, block_table, donor_positions,
+                                        target_positions, rope_base)
+    if call is not None:
+        call()
+    return kv_caches
+
+
+class PreparedScatter:
+    """A validated multi-layer paged scatter bound to its tensors' addresses; calling it
+    enqueues the launch on torch's current stream. It holds the device tables and index
+    tensors it reads, so they live as long as it does."""
+
+    def __init__(self, entry: str, args: tuple, keep: tuple, device: torch.device):
+        self.entry, self.args, self.keep, self.device = entry, args, keep, device
+
+    def __call__(self) -> None:
+        with torch.cuda.device(self.device):
+            _lib.call(self.entry, *self.args, _lib.stream_handle(self.device))
+
+
+def prepare_scatter_paged_layers(
+    kv_caches: list[torch.Tensor],
+    donor_kvs: list[torch.Tensor],
+    block_table: torch.Tensor,
+    donor_positions: torch.Tensor,
+    target_positions: torch.Tensor,
+    rope_base: float | None = 10000.0,
+) -> PreparedScatter | None:
+    """Check the inputs of the multi-layer paged scatter once and bind them: K is rotated by
+    ``target - donor`` with RoPE base ``rope_base``, or copied unrotated (with V) when
+    ``rope_base`` is None. Returns None when there are no pairs. For callers that repeat the
+    same scatter every step: the host work of validation, address tables and index uploads
+    is done here, not per launch; the tensors must keep their storage afterwards."""
     if len(kv_caches) != len(donor_kvs):
         raise ValueError("kv_caches and donor_kvs must have the same length")
     num_pairs = donor_positions.shape[0]
     if num_pairs == 0 or not kv_caches:
-        return kv_caches
+        return None
+    if target_positions.shape[0] != num_pairs:
+        raise ValueError("donor_positions and target_positions differ in length")
     ref, dref = kv_caches[0], donor_kvs[0]
     nb_total, _, num_heads, block_size, head_dim = ref.shape
-    _check_head_dim(head_dim, head_dim, "rope_correct_scatter_paged_layers")
+    rope = rope_base is not None
+    if rope:
+        _check_head_dim(head_dim, head_dim, "rope_correct_scatter_paged_layers")
     dev = _lib.require_device(*kv_caches, *donor_kvs)
     _check_uniform(kv_caches, "kv_caches")
     _check_uniform(donor_kvs, "donor_kvs")
@@ -144,16 +181,17 @@ def rope_correct_scatter_paged_layers(
     bt = _lib.as_index(block_table, dev)
     dpos = _lib.as_index(donor_positions, dev)
     tpos = _lib.as_index(target_positions, dev)
-    inv_freq = inv_freq_table(rope_base, head_dim, dev)
-    with torch.cuda.device(dev):
-        _lib.call(
-            "sb_rope_correct_scatter_paged_layers",
-            kv_tab.data_ptr(), d_tab.data_ptr(), len(kv_caches), bt.data_ptr(),
-            dpos.data_ptr(), tpos.data_ptr(), inv_freq.data_ptr(), num_pairs, num_heads,
-            block_size, head_dim, dref.shape[2], nb_total, bt.shape[0], _lib.strides(ref),
-            _lib.strides(dref), _lib.dtype_code(ref), _lib.stream_handle(dev),
-        )
-    return kv_caches
+    tail = (num_pairs, num_heads, block_size, head_dim, dref.shape[2], nb_total, bt.shape[0],
+            _lib.strides(ref), _lib.strides(dref), _lib.dtype_code(ref))
+    head = (kv_tab.data_ptr(), d_tab.data_ptr(), len(kv_caches), bt.data_ptr(),
+            dpos.data_ptr(), tpos.data_ptr())
+    if rope:
+        inv_freq = inv_freq_table(float(rope_base), head_dim, dev)
+        return PreparedScatter("sb_rope_correct_scatter_paged_layers",
+                               head + (inv_freq.data_ptr(),) + tail,
+                               (kv_tab, d_tab, bt, dpos, tpos, inv_freq), dev)
+    return PreparedScatter("sb_scatter_donor_kv_paged_layers", head + tail,
+                           (kv_tab, d_tab, bt, dpos, tpos), dev)
 
 
 def _check_uniform(ts: list[torch.Tensor], name: str) -> None:

@@ -120,6 +120,20 @@ def test_kv_reuse_batch_llama_shape(dev):
         got = caches[layer].cpu()
         assert torch.equal(got[:, 1].view(torch.int16), want[:, 1].view(torch.int16))
         assert_rope_close(got[:, 0], want[:, 0])
+    # a repeated step reuses the prepared launches and lands the same bytes
+    again = [c.clone() for c in caches]
+    batch.scatter_rope()
+    for a_, b_ in zip(caches, again):
+        assert torch.equal(a_.view(torch.int16), b_.view(torch.int16))
+    # rope=False copies like the plain multi-layer scatter, request by request
+    got_plain = [c.to(dev) for c in before]
+    KVReuseBatch(got_plain, reqs, rope_base=theta).scatter_rope(rope=False)
+    want_plain = [c.to(dev) for c in before]
+    for r in reqs:
+        tk.scatter_donor_kv_paged_layers(want_plain, list(r.donor_kvs), r.block_table,
+                                         r.donor_positions, r.target_positions)
+    for a_, b_ in zip(got_plain, want_plain):
+        assert torch.equal(a_.view(torch.int16), b_.view(torch.int16))
     q = randn((batch.num_rows, 32, 128), torch.bfloat16, 150).to(dev)
     for layer in range(2):
         out = batch.attention(layer, q)
