@@ -12,12 +12,13 @@
 //
 // Tiles: 256 features x 256 rows per workgroup of 4 waves (each wave 128 x 128 = 4 x 4 MFMA
 // blocks, 256 fp32 accumulators), one workgroup per CU; 128 x 128 (two per CU) when the row
-// count is too small to give half the CUs a big tile. 32 hidden elements per k-step in a
-// 4-stage LDS ring (loads three steps ahead, one barrier per step). Both operands are read with their hidden
-// dimension contiguous (W row-major [F, hidden], hidden [S, hidden]), moved global -> LDS
-// with global_load_lds_dwordx4, 16-byte chunks of each tile row XOR-swizzled so that the
-// ds_read_b128 fragment reads of 16 consecutive rows fall on distinct banks. Tiles are
-// ordered XCD by XCD in bands of row tiles (qkv_tile) for L2 reuse.
+// count is too small to give half the CUs a big tile. 64 hidden elements per k-step (each
+// tile row one 128-byte line) in a 2-stage LDS ring (loads one step ahead, one barrier per
+// step; 32 elements in 4 stages, half lines, was 1.5-4% slower). Both operands are read
+// with their hidden dimension contiguous (W row-major [F, hidden], hidden [S, hidden]),
+// moved global -> LDS with global_load_lds_dwordx4, 16-byte chunks of each tile row
+// XOR-swizzled so that the ds_read_b128 fragment reads of 16 consecutive rows fall on
+// distinct banks. Tiles are ordered XCD by XCD in bands of row tiles (qkv_tile) for L2 reuse.
 //
 // Epilogue (feature layout Q [Hq*D] | K [Hkv*D] | V [Hkv*D]):
 //   split mode  Q -> q_out[row] (compact), K / V -> paged cache slot of positions[row];
@@ -42,9 +43,18 @@ typedef float qf32x16_t __attribute__((ext_vector_type(16)));
 #define SB_QKV_GROUP 8
 #endif
 constexpr int kQThreads = 256;
-constexpr int kTK = 32;        // hidden elements per k-step (64-byte tile rows)
-constexpr int kStages = 4;     // LDS ring depth: loads run three k-steps ahead
+#ifndef SB_QKV_TK
+#define SB_QKV_TK 64
+#endif
+#ifndef SB_QKV_STAGES
+#define SB_QKV_STAGES 2
+#endif
+constexpr int kTK = SB_QKV_TK;        // hidden elements per k-step (2 * kTK-byte tile rows)
+constexpr int kStages = SB_QKV_STAGES;  // LDS ring depth: loads run kStages - 1 steps ahead
 constexpr int kTileChunks = kTK / 8;  // 16-byte chunks per tile row
+constexpr int kLoadRows = kQThreads / kTileChunks;  // tile rows one load of every thread fills
+static_assert(kTK == 32 || kTK == 64, "tile rows of 64 or 128 bytes");
+static_assert(kStages >= 2 && kStages <= 4, "the step waits cover rings of 2 to 4 stages");
 constexpr int kGroup = SB_QKV_GROUP;  // row tiles per band of the tile order
 constexpr int kXcds = 8;       // MI355X: workgroups go round-robin to 8 XCDs
 
@@ -74,10 +84,14 @@ struct QkvArgs {
   int64_t block_size, nb_total, nb_per_seq;
 };
 
-// 16-byte chunk position of chunk c of a 64-byte tile row r. Rows share the 64 banks four
-// ways; the XOR with (r / 4) spreads 16 consecutive rows read at one chunk over distinct
-// bank groups, so the ds_read_b128 fragment reads are conflict-free.
-__device__ __forceinline__ int qswz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+// 16-byte chunk position of chunk c of tile row r. 256 bytes of banks hold 256 / (2 kTK)
+// rows (4 for 64-byte rows, 2 for 128-byte rows); the XOR with r divided by that count
+// spreads 16 consecutive rows read at one chunk over distinct bank groups, so the
+// ds_read_b128 fragment reads are conflict-free.
+__device__ __forceinline__ int qswz(int row, int chunk) {
+  constexpr int shift = kTK == 32 ? 2 : 1;
+  return chunk ^ ((row >> shift) & (kTileChunks - 1));
+}
 
 // s_waitcnt vmcnt(N) (6-bit count, split over bits 3:0 and 15:14), other counters untouched.
 template <int N>
@@ -221,18 +235,20 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
   }
   __syncthreads();
 
-  // DMA sources: slot s = q * 256 + tid of a stage holds tile row s / 4 = 64 q + tid / 4 at
-  // position tid % 4, i.e. global chunk qswz(row, tid % 4), which does not depend on q.
+  // DMA sources: slot s = q * 256 + tid of a stage holds tile row s / kTileChunks =
+  // q * kLoadRows + tid / kTileChunks at position tid % kTileChunks, i.e. global chunk
+  // qswz(row, tid % kTileChunks), which does not depend on q.
   const int chunk = qswz(tid / kTileChunks, tid % kTileChunks);
   const char* asrc[LA];
   const char* bsrc[LB];
 #pragma unroll
   for (int q = 0; q < LA; ++q) {
-    const int64_t f = min(m0 + q * 64 + tid / kTileChunks, a.num_features - 1);
+    const int64_t f = min(m0 + q * kLoadRows + tid / kTileChunks, a.num_features - 1);
     asrc[q] = a.weight + f * a.w_s_row + 16 * chunk;
   }
 #pragma unroll
-  for (int q = 0; q < LB; ++q) bsrc[q] = a.hidden + brow[q * 64 + tid / kTileChunks] + 16 * chunk;
+  for (int q = 0; q < LB; ++q)
+    bsrc[q] = a.hidden + brow[q * kLoadRows + tid / kTileChunks] + 16 * chunk;
   auto issue = [&](int stage, int64_t kt) {
     const int64_t ko = kt * (kTK * 2);
 #pragma unroll
@@ -259,9 +275,11 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
     if (s0 < a.k_steps) issue(s0, s0);
   for (int64_t kt = 0; kt < a.k_steps; ++kt) {
     const int st = static_cast<int>(kt % kStages);
-    const int64_t ahead = a.k_steps - 1 - kt;  // steps issued after this one (at most 2)
-    if (ahead >= 2) qkv_wait_vm<2 * (LA + LB)>();
-    else if (ahead == 1) qkv_wait_vm<LA + LB>();
+    // Steps issued after this one: at most kStages - 2, fewer near the end; they may stay
+    // in flight while step kt must have landed.
+    const int64_t ahead = a.k_steps - 1 - kt;
+    if (kStages >= 4 && ahead >= 2) qkv_wait_vm<2 * (LA + LB)>();
+    else if (kStages >= 3 && ahead >= 1) qkv_wait_vm<LA + LB>();
     else qkv_wait_vm<0>();
     __syncthreads();
     if (kt + kStages - 1 < a.k_steps)
