@@ -572,7 +572,7 @@ def main() -> int:
                     help="skip the Llama-3-8B multi-request batch section")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path "
+        print("bench.py measures one MI355X: the library has no multi-GPU path "
               "(each GPU would own its own layers or KV heads with no exchange). "
               "Run with --gpus 1.", file=sys.stderr)
         return 2

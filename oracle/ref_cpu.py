@@ -1,7 +1,7 @@
 """CPU oracle for SemBlend's KV-reuse path — TEST INFRASTRUCTURE ONLY.
 
 This module restates, on CPU tensors, the reference's own CPU semantics for every function on
-the path. It is the checker the HIP kernels are compared against, and the CPU baseline that
+the path. The HIP kernels are compared against it in the tests, and it is the CPU baseline that
 ``bench.py`` times. Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 cpu_baseline leg may import it; the ``semblend_amd`` package never does.
 
