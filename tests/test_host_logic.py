@@ -272,3 +272,21 @@ def test_cpu_tensors_are_rejected():
     for call in calls:
         with pytest.raises(RuntimeError, match="device tensors"):
             call()
+
+
+def test_prepare_scatter_paged_layers_host_checks():
+    """Checks made before any device work: layer counts, pair counts, and no launch for an
+    empty pair set; CPU caches are refused (no CPU fallback)."""
+    kv = [torch.zeros((4, 2, 2, 16, 64), dtype=torch.bfloat16) for _ in range(2)]
+    donors = [torch.zeros((2, 2, 32, 64), dtype=torch.bfloat16) for _ in range(2)]
+    bt = torch.arange(4, dtype=torch.int32)
+    d = torch.arange(5, dtype=torch.int32)
+    with pytest.raises(ValueError, match="same length"):
+        rc.prepare_scatter_paged_layers(kv, donors[:1], bt, d, d)
+    with pytest.raises(ValueError, match="differ in length"):
+        rc.prepare_scatter_paged_layers(kv, donors, bt, d, d[:3])
+    empty = torch.zeros(0, dtype=torch.int32)
+    assert rc.prepare_scatter_paged_layers(kv, donors, bt, empty, empty) is None
+    assert rc.rope_correct_scatter_paged_layers(kv, donors, bt, empty, empty) is kv
+    with pytest.raises((ValueError, RuntimeError)):
+        rc.prepare_scatter_paged_layers(kv, donors, bt, d, d)
