@@ -83,6 +83,62 @@ def recompute_positions(g: torch.Generator, ctx: int = CTX,
     return mask.nonzero().flatten().to(torch.int32)
 
 
+# Qwen2.5-0.5B one-layer pipeline (the reference's CPU-runnable case).
+QWEN05B = {"hq": 14, "hkv": 2, "d": 64, "theta": 1e6, "ctx": 1024, "pool_blocks": 128,
+           "max_delta": 64, "rows": 154}
+
+
+def qwen05b_pipeline_inputs(seed: int = 0) -> dict:
+    """Inputs of the one-layer KV-reuse pipeline at the Qwen2.5-0.5B shape (14 q heads, 2 KV
+    heads, head_dim 64, fp32, theta 1e6, 1024 tokens), drawn in this order from one CPU
+    generator: donor K/V [2, 2, 1024, 64] ~ N(0, 1); a block table of 64 entries from a random
+    permutation of the 128-block pool; one RoPE delta per token, uniform over the integers in
+    [-64, 64]; 154 recompute positions (15%) drawn uniformly without replacement (sorted);
+    their queries [154, 14, 64] ~ N(0, 1). The cache [128, 2, 2, 16, 64] starts zeroed and
+    donor row t goes to position t. CPU tensors."""
+    c = QWEN05B
+    g = torch.Generator("cpu").manual_seed(seed)
+    donor = torch.randn((2, c["hkv"], c["ctx"], c["d"]), generator=g)
+    bt = torch.randperm(c["pool_blocks"], generator=g)[:c["ctx"] // BS].to(torch.int32)
+    deltas = torch.randint(-c["max_delta"], c["max_delta"] + 1, (c["ctx"],), generator=g)
+    rows = torch.randperm(c["ctx"], generator=g)[:c["rows"]].sort().values.to(torch.int32)
+    q = torch.randn((c["rows"], c["hq"], c["d"]), generator=g)
+    return {"donor": donor, "block_table": bt, "deltas": deltas, "rows": rows, "q": q,
+            "cache": torch.zeros((c["pool_blocks"], 2, c["hkv"], BS, c["d"])),
+            "positions": torch.arange(c["ctx"], dtype=torch.int32)}
+
+
+def delta_groups(deltas: torch.Tensor) -> list[tuple[int, list[int]]]:
+    """(delta, positions) for every distinct nonzero per-token delta, in ascending delta
+    order: one in-place RoPE call per group."""
+    out = []
+    for dl in torch.unique(deltas).tolist():
+        if dl != 0:
+            out.append((int(dl), (deltas == dl).nonzero().flatten().tolist()))
+    return out
+
+
+def qwen05b_pipeline(mod_tk, mod_rc, inp: dict, device=None):
+    """The pipeline through the drop-in entry points (``mod_tk`` / ``mod_rc`` are the
+    triton_kernels / rope_correction modules, or the oracle for both): scatter the donor into
+    the paged cache, rotate every token's K in place by its delta (one
+    ``apply_rope_delta_inplace`` call per distinct delta), then causal GQA attention of the
+    recompute rows over that cache. Returns (cache, attention output)."""
+    c = QWEN05B
+    to = (lambda t: t.to(device)) if device is not None else (lambda t: t.clone())
+    kv = to(inp["cache"])
+    bt = to(inp["block_table"])
+    pos = to(inp["positions"])
+    mod_tk.scatter_donor_kv_paged(kv, to(inp["donor"]), bt, pos, pos)
+    for dl, where in delta_groups(inp["deltas"]):
+        mod_rc.apply_rope_delta_inplace(kv, bt, where, dl, rope_base=c["theta"])
+    if device is not None:
+        out = mod_tk.partial_prefill_attention_paged(to(inp["q"]), kv, bt, to(inp["rows"]))
+    else:
+        out = mod_tk.partial_attention_paged(inp["q"], kv, bt, inp["rows"])
+    return kv, out
+
+
 # Llama-3-8B batch (four requests sharing one paged pool, all layers).
 LLAMA = {"layers": 32, "hq": 32, "hkv": 8, "d": 128, "theta": 5e5,
          "ctx": (8192, 16384, 24576, 32768), "frac": (0.10, 0.15, 0.20, 0.30),
@@ -203,37 +259,65 @@ def gemm_ceiling(dev: torch.device, n: int = 8192, reps: int = 10) -> float:
     return tflops
 
 
-def cpu_model() -> str:
+def cpu_model() -> dict:
+    """Host CPU description: lscpu's model name, family/model/stepping, sockets and threads
+    per core (what /proc/cpuinfo says when lscpu is absent)."""
+    info = {}
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
+        import subprocess
+
+        res = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10)
+        for line in res.stdout.splitlines():
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key in ("Model name", "Vendor ID", "CPU family", "Model", "Stepping",
+                       "Socket(s)", "Thread(s) per core", "Core(s) per socket", "CPU(s)",
+                       "CPU max MHz"):
+                info[key] = val.strip()
+    except (OSError, ValueError):
         pass
-    return "unknown"
+    if "Model name" not in info:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        info["Model name"] = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            info["Model name"] = "unknown"
+    return info
+
+
+def median_time(fn, reps: int = 3) -> float:
+    """Median wall time of ``reps`` calls of fn (time.perf_counter), seconds."""
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
 
 
 def cpu_baseline(inp) -> dict:
-    """Oracle (reference CPU path restated) on the whole workload, on the host's cores."""
+    """Oracle (reference CPU path restated) on the whole workload, on the host's cores;
+    each leg's time is the median of three runs."""
     from oracle import ref_cpu as ref
 
-    torch.set_num_threads(max(1, torch.get_num_threads()))
+    torch.set_num_threads(max(1, os.cpu_count() or 1))
     cores = torch.get_num_threads()
     kv = inp["attn_kv"].cpu()
     bt = inp["block_table"].cpu()
     pos = inp["pos_cpu"]
     q = inp["attn_q"].cpu()
     flops = 4.0 * D * HQ * float((pos.double() + 1).sum())
-    t0 = time.perf_counter()
-    ref.partial_attention_paged(q, kv, bt, pos)
-    dt = time.perf_counter() - t0
+    dt = median_time(lambda: ref.partial_attention_paged(q, kv, bt, pos))
     out = {
         "value": flops / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
-        "host": {"cpu_count": os.cpu_count(), "torch_threads": cores, "model": cpu_model()},
+        "host": {"cpu_count": os.cpu_count(), "torch_threads": cores, "cpu": cpu_model()},
+        "timing": "median of 3 (time.perf_counter)",
         "sample": f"whole workload: partial attention, all {pos.shape[0]} recompute rows, "
                   f"28q/4kv x 128, 16384-token paged context, bf16 in / fp32 math {dt:.2f} s",
     }
@@ -242,21 +326,62 @@ def cpu_baseline(inp) -> dict:
     donors = [x.cpu() for x in inp["donors"]]
     caches = [torch.zeros((POOL_BLOCKS, 2, HKV, BS, D), dtype=torch.bfloat16)
               for _ in range(L)]
-    t0 = time.perf_counter()
-    for layer in range(L):
-        ref.scatter_donor_kv_paged(caches[layer], donors[layer], bt, d_pos, t_pos)
-    dt_s = time.perf_counter() - t0
+
+    def scatter_all():
+        for layer in range(L):
+            ref.scatter_donor_kv_paged(caches[layer], donors[layer], bt, d_pos, t_pos)
+
+    dt_s = median_time(scatter_all)
     out["scatter_gbps"] = float(d_pos.shape[0]) * L * 2 * HKV * D * 2 * 2 / dt_s / 1e9
     del caches, donors
     k = inp["rope_k"][0].cpu()
-    t0 = time.perf_counter()
-    ref.rope_correct_k(k, inp["rope_d"].cpu(), inp["rope_t"].cpu(), head_dim=D,
-                       rope_base=ROPE_BASE)
-    dt_r = time.perf_counter() - t0
+    dt_r = median_time(lambda: ref.rope_correct_k(k, inp["rope_d"].cpu(), inp["rope_t"].cpu(),
+                                                  head_dim=D, rope_base=ROPE_BASE))
     out["rope_gbps"] = k.numel() * 2 * 2 / dt_r / 1e9
     out["sample"] += (f"; scatter {d_pos.shape[0]} pairs x {L} layers {dt_s:.2f} s; "
                       f"rope {ROPE_TOKENS} tokens x {L} layers x {HKV} heads {dt_r:.2f} s")
     return out
+
+
+def qwen05b_section(dev: torch.device, steps: int, cpu: bool) -> dict:
+    """The one-layer Qwen2.5-0.5B pipeline (fp32, 1024 tokens): scatter, per-token RoPE in
+    place (one call per distinct delta), 154-row GQA attention. GPU: the drop-in calls as a
+    caller makes them, host work included (wall time around the synchronised pipeline,
+    median over ``steps``); CPU: the oracle, median of 3."""
+    from semblend_amd import rope_correction as rc
+    from semblend_amd import triton_kernels as tk
+
+    inp = qwen05b_pipeline_inputs(seed=0)
+    c = QWEN05B
+    rows = inp["rows"].double()
+    flops = 4.0 * c["d"] * c["hq"] * float((rows + 1).sum())
+    moved = float(c["ctx"]) * 2 * c["hkv"] * c["d"] * 4 * 2
+    qwen05b_pipeline(tk, rc, inp, device=dev)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(max(steps, 3)):
+        t0 = time.perf_counter()
+        qwen05b_pipeline(tk, rc, inp, device=dev)
+        torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t0)
+    gpu_ms = 1e3 * sorted(ts)[len(ts) // 2]
+    res = {
+        "workload": "Qwen2.5-0.5B one layer: 14q/2kv x 64, fp32, theta 1e6, 1024 tokens; "
+                    "scatter into [128, 2, 2, 16, 64] (permuted block table), per-token "
+                    "deltas in [-64, 64] applied in place (one call per distinct delta), "
+                    "154 recompute rows",
+        "rope_calls": len(delta_groups(inp["deltas"])),
+        "attention_flops": flops, "scatter_bytes": moved,
+        "gpu": {"ms": round(gpu_ms, 3), "what": "drop-in calls incl. host work, median"},
+    }
+    if cpu:
+        from oracle import ref_cpu as ref
+
+        cpu_s = median_time(lambda: qwen05b_pipeline(ref, ref, inp))
+        res["cpu_baseline"] = {"ms": round(1e3 * cpu_s, 1), "cores": torch.get_num_threads(),
+                               "kind": "port", "timing": "median of 3",
+                               "sample": "the whole pipeline (it is small)"}
+    return res
 
 
 def llama_batch_section(dev: torch.device, steps: int, cpu: bool) -> dict:
@@ -319,32 +444,51 @@ def llama_batch_section(dev: torch.device, steps: int, cpu: bool) -> dict:
         "ms_per_step": round(sr_ms + at_ms, 4),
     }
     if cpu:
-        # Oracle on layer 0 of the largest request: 64 recompute rows and 512 reuse pairs.
+        # Oracle on layer 0, extrapolated to 32 layers: the RoPE scatter of every pair of
+        # every request into layer 0, and attention for one in 16 recompute rows of every
+        # request (rows spread evenly over each request's positions) scaled by the FLOP
+        # share of the sample. Median of 3 each.
         from oracle import ref_cpu as ref
 
-        r = reqs[-1]
-        g = torch.Generator("cpu").manual_seed(6)
-        rows = torch.randperm(r.compute_positions.shape[0], generator=g)[:64].sort().values
-        pos = r.compute_positions.cpu()[rows]
-        kv = caches[0].cpu()
-        bt = r.block_table.cpu()
-        a0 = batch.row_offsets[len(reqs) - 1]
-        qs = q[a0:a0 + r.compute_positions.shape[0]].cpu()[rows]
-        t0 = time.perf_counter()
-        ref.partial_attention_paged(qs, kv, bt, pos)
-        dt_a = time.perf_counter() - t0
-        sel = torch.randperm(r.donor_positions.shape[0], generator=g)[:512]
-        dk = r.donor_kvs[0].cpu()
-        t0 = time.perf_counter()
-        ref.rope_correct_scatter_paged(kv, dk, bt, r.donor_positions.cpu()[sel],
-                                       r.target_positions.cpu()[sel], rope_base=theta)
-        dt_s = time.perf_counter() - t0
+        kv0 = caches[0].cpu()
+        donors0 = [r.donor_kvs[0].cpu() for r in reqs]
+        tables = [r.block_table.cpu() for r in reqs]
+        dps = [r.donor_positions.cpu() for r in reqs]
+        tps = [r.target_positions.cpu() for r in reqs]
+
+        def scatter_layer0():
+            for i in range(len(reqs)):
+                ref.rope_correct_scatter_paged(kv0, donors0[i], tables[i], dps[i], tps[i],
+                                               rope_base=theta)
+
+        dt_s = median_time(scatter_layer0)
+        qs, poss, sample_p1 = [], [], 0.0
+        for i, r in enumerate(reqs):
+            a0 = batch.row_offsets[i]
+            sel = torch.arange(0, r.compute_positions.shape[0], 16)
+            qs.append(q[a0:a0 + r.compute_positions.shape[0]].cpu()[sel])
+            poss.append(r.compute_positions.cpu()[sel])
+            sample_p1 += float((poss[-1].double() + 1).sum())
+
+        def attn_sample():
+            for i in range(len(reqs)):
+                ref.partial_attention_paged(qs[i], kv0, tables[i], poss[i])
+
+        dt_a = median_time(attn_sample)
+        sample_flops = 4.0 * d * hq * sample_p1
+        attn_s = dt_a * flops / sample_flops
+        sr_s = dt_s * layers
         res["cpu_baseline"] = {
-            "attention_tflops": 4.0 * d * hq * float((pos.double() + 1).sum()) / dt_a / 1e12,
-            "scatter_rope_gbps": 512 * 2 * hkv * d * 2 * 2 / dt_s / 1e9,
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"layer 0, largest request: 64 recompute rows ({dt_a:.2f} s) and 512 "
-                      f"reuse pairs ({dt_s:.2f} s); rates, not whole-batch times"}
+            "extrapolated": True,
+            "scatter_rope_ms": round(1e3 * sr_s, 1),
+            "scatter_rope_gbps": moved / sr_s / 1e9,
+            "attention_ms": round(1e3 * attn_s, 1),
+            "attention_tflops": flops / attn_s / 1e12,
+            "cores": torch.get_num_threads(), "kind": "port", "timing": "median of 3",
+            "sample": f"layer 0: RoPE scatter of all {pairs} pairs ({dt_s:.2f} s, x{layers} "
+                      f"layers) and attention of every 16th recompute row of each request "
+                      f"({sum(x.shape[0] for x in poss)} rows, {dt_a:.2f} s, scaled by "
+                      f"{flops / sample_flops:.1f}x = total / sampled FLOPs)"}
     del caches, reqs, batch
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -746,6 +890,11 @@ def main() -> int:
     log(f"chunk load: copies only {cl['copies_only']['ms']:.2f} ms "
         f"({cl['copies_only']['host_gbps']:.1f} GB/s), serial {cl['serial']['ms']:.2f} ms, "
         f"streamed {cl['streamed']['ms']:.2f} ms (overlap {cl['overlap_efficiency']:.3f})")
+    log("Qwen2.5-0.5B one-layer pipeline (fp32)")
+    result["qwen05b_pipeline"] = qwen05b_section(dev, args.steps, not args.no_cpu_baseline)
+    qp = result["qwen05b_pipeline"]
+    log(f"qwen0.5b pipeline: gpu {qp['gpu']['ms']:.3f} ms"
+        + (f", cpu {qp['cpu_baseline']['ms']:.1f} ms" if "cpu_baseline" in qp else ""))
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle on host cores)")
         result["cpu_baseline"] = cpu_baseline(inp)

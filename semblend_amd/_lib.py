@@ -14,10 +14,8 @@ from pathlib import Path
 
 import torch
 
-# The library built in-tree next to this file; SEMBLEND_AMD_LIB names another build of the
-# same C ABI (for example one compiled with different tuning macros).
-LIB_PATH = Path(os.environ.get("SEMBLEND_AMD_LIB") or
-                Path(__file__).resolve().parent / "libsemblend_hip.so")
+# The library built in-tree next to this file (semblend_amd/_build.py writes it).
+LIB_PATH = Path(__file__).resolve().parent / "libsemblend_hip.so"
 
 SB_OK = 0
 SB_ERR_INVALID_ARGUMENT = 100001
@@ -213,6 +211,9 @@ def as_index(t, device: torch.device) -> torch.Tensor:
 
 _ADDR_TABLES: dict[tuple, torch.Tensor] = {}
 _ADDR_TABLES_MAX = 64
+# Tables used by a launch recorded into a HIP graph: a replay may come at any time, so these
+# are never evicted (with the pinned host copy a captured upload reads from).
+_CAPTURED_TABLES: dict[tuple, tuple[torch.Tensor, torch.Tensor | None]] = {}
 
 
 def address_table(tensors, device: torch.device) -> torch.Tensor:
@@ -222,16 +223,32 @@ def address_table(tensors, device: torch.device) -> torch.Tensor:
     Tables are cached by (device, addresses), so repeated calls over the same layer tensors
     enqueue no host-to-device copy; a new table is copied from pinned memory without blocking
     the host. Keying by the addresses themselves keeps a cached table correct even when the
-    tensors are freed and others reuse the memory.
+    tensors are freed and others reuse the memory. Lifetime: a table is marked as used on
+    the current stream at every call, so evicting it from the bounded cache never releases
+    memory that a kernel enqueued on another stream still reads; a table requested while the
+    current stream is capturing a HIP graph is kept for the life of the process, since the
+    graph holds its raw address. Callers that repeat one launch should prefer the prepared
+    forms (``rope_correction.prepare_scatter_paged_layers``), which own their tables.
     """
     key = (device, tuple(t.data_ptr() for t in tensors))
+    capturing = torch.cuda.is_current_stream_capturing()
+    kept = _CAPTURED_TABLES.get(key)
+    if kept is not None:
+        return kept[0]
     tab = _ADDR_TABLES.get(key)
+    host = None
     if tab is None:
         if len(_ADDR_TABLES) >= _ADDR_TABLES_MAX:
             _ADDR_TABLES.pop(next(iter(_ADDR_TABLES)))
         host = torch.tensor(key[1], dtype=torch.int64).pin_memory()
         tab = host.to(device, non_blocking=True)
-        _ADDR_TABLES[key] = tab
+        if not capturing:
+            _ADDR_TABLES[key] = tab
+    if capturing:
+        _ADDR_TABLES.pop(key, None)
+        _CAPTURED_TABLES[key] = (tab, host)
+    else:
+        tab.record_stream(torch.cuda.current_stream(device))
     return tab
 
 

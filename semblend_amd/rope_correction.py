@@ -87,7 +87,10 @@ def rope_correct_scatter_paged(
     physical block is out of range are skipped.
     Reference: semblend_core/rope_correction.py:193-282.
     """
-    num_pairs = donor_positions.shape[0]
+    num_pairs = len(donor_positions)
+    if len(target_positions) != num_pairs:
+        raise ValueError(f"donor_positions ({num_pairs}) and target_positions "
+                         f"({len(target_positions)}) differ in length")
     if num_pairs == 0:
         return kv_cache
     nb_total, _, num_heads, block_size, hd = kv_cache.shape
@@ -161,11 +164,11 @@ def prepare_scatter_paged_layers(
     is done here, not per launch; the tensors must keep their storage afterwards."""
     if len(kv_caches) != len(donor_kvs):
         raise ValueError("kv_caches and donor_kvs must have the same length")
-    num_pairs = donor_positions.shape[0]
+    num_pairs = len(donor_positions)
+    if len(target_positions) != num_pairs:
+        raise ValueError("donor_positions and target_positions differ in length")
     if num_pairs == 0 or not kv_caches:
         return None
-    if target_positions.shape[0] != num_pairs:
-        raise ValueError("donor_positions and target_positions differ in length")
     ref, dref = kv_caches[0], donor_kvs[0]
     nb_total, _, num_heads, block_size, head_dim = ref.shape
     rope = rope_base is not None

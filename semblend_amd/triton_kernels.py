@@ -54,6 +54,16 @@ __all__ = [
 # Donor-KV scatter
 # ------------------------------------------------------------------------------------------
 
+def _check_pair_lengths(donor_positions, target_positions) -> int:
+    """Number of (donor, target) pairs; the two position lists must have the same length
+    (the kernels read one target per donor position)."""
+    n = len(donor_positions)
+    if len(target_positions) != n:
+        raise ValueError(f"donor_positions ({n}) and target_positions "
+                         f"({len(target_positions)}) differ in length")
+    return n
+
+
 def _contig_last(t: torch.Tensor) -> tuple[torch.Tensor, bool]:
     """(tensor with unit stride in the last dim, whether it is a temporary copy)."""
     if t.stride(-1) == 1:
@@ -74,7 +84,7 @@ def scatter_donor_kv(
     Pairs with d >= donor_seq_len or t >= target_seq_len (or negative) are skipped.
     Returns target (modified in place). Reference: semblend_core/triton_kernels.py:132-191.
     """
-    num_pairs = donor_positions.shape[0]
+    num_pairs = _check_pair_lengths(donor_positions, target_positions)
     if num_pairs == 0:
         return target
     dev = _lib.require_device(target, donor)
@@ -113,7 +123,7 @@ def scatter_donor_kv_paged(
     (the reference GPU kernel's rule, semblend_core/triton_kernels.py:246-260).
     Returns kv_cache (modified in place). Reference: semblend_core/triton_kernels.py:279-356.
     """
-    num_pairs = donor_positions.shape[0]
+    num_pairs = _check_pair_lengths(donor_positions, target_positions)
     if num_pairs == 0:
         return kv_cache
     dev = _lib.require_device(kv_cache, donor_kv)
@@ -152,7 +162,7 @@ def scatter_donor_kv_paged_layers(
     """
     if len(kv_caches) != len(donor_kvs):
         raise ValueError("kv_caches and donor_kvs must have the same length")
-    num_pairs = donor_positions.shape[0]
+    num_pairs = _check_pair_lengths(donor_positions, target_positions)
     if num_pairs == 0 or not kv_caches:
         return kv_caches
     dev = _lib.require_device(*kv_caches, *donor_kvs)

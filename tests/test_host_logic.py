@@ -290,3 +290,25 @@ def test_prepare_scatter_paged_layers_host_checks():
     assert rc.rope_correct_scatter_paged_layers(kv, donors, bt, empty, empty) is kv
     with pytest.raises((ValueError, RuntimeError)):
         rc.prepare_scatter_paged_layers(kv, donors, bt, d, d)
+
+
+def test_pair_length_mismatch_is_rejected_before_launch():
+    """A target list shorter than the donor list would make the kernels read past it: every
+    scatter entry refuses it with ValueError before looking at the device (CPU tensors here,
+    so reaching the device check would raise RuntimeError instead)."""
+    kv = torch.zeros(4, 2, 1, 4, 8)
+    donor = torch.zeros(2, 1, 8, 8)
+    bt = torch.tensor([0, 1], dtype=torch.int32)
+    d = torch.tensor([0, 1, 2], dtype=torch.int32)
+    t = torch.tensor([0, 1], dtype=torch.int32)
+    flat = torch.zeros(1, 2, 1, 8, 8)
+    calls = [
+        lambda: tk.scatter_donor_kv(flat, flat.clone(), d, t),
+        lambda: tk.scatter_donor_kv_paged(kv, donor, bt, d, t),
+        lambda: tk.scatter_donor_kv_paged_layers([kv], [donor], bt, d, t),
+        lambda: rc.rope_correct_scatter_paged(kv, donor, bt, d, t),
+        lambda: rc.rope_correct_scatter_paged_layers([kv], [donor], bt, d, t),
+    ]
+    for call in calls:
+        with pytest.raises(ValueError, match="differ in length"):
+            call()
