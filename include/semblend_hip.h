@@ -273,6 +273,27 @@ int sb_partial_attention_paged(void* out, const void* q, const void* kv_cache,
                                const int64_t* q_strides, const int64_t* o_strides,
                                const int64_t* kv_strides, int32_t dtype, void* stream);
 
+/* No-allocation form of sb_partial_attention_paged, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments minus the workspace, same kernels, same plan and bit-identical
+ * results; the split-key partials live in a fixed array inside the library, one per GPU,
+ * of sb_partial_attention_paged_noalloc_max_scratch() bytes (128 MiB), held from module load
+ * until the process ends. A call whose partials would exceed it fails with
+ * SB_ERR_INVALID_ARGUMENT before any launch. Calls on one GPU share that GPU's array:
+ * calls that overlap on one GPU (concurrent streams, or threads) race and must be
+ * serialised by the caller. Nothing in the array needs clearing between calls. The call
+ * makes no hipMalloc/hipFree or allocating library call.
+ * No reference counterpart (the reference has no paged GQA attention entry). */
+int64_t sb_partial_attention_paged_noalloc_max_scratch(void);
+int sb_partial_attention_paged_noalloc(void* out, const void* q, const void* kv_cache,
+                                       const int32_t* block_table, const int32_t* positions,
+                                       int64_t num_rows, int64_t num_q_heads,
+                                       int64_t num_kv_heads, int64_t head_dim,
+                                       int64_t block_size, int64_t num_blocks_total,
+                                       int64_t num_blocks_per_seq, float scale,
+                                       const int64_t* q_strides, const int64_t* o_strides,
+                                       const int64_t* kv_strides, int32_t dtype, void* stream);
+
 /* Batched GQA attention over a paged cache: num_reqs requests share kv_cache, request r
  * has rows_per_req[r] query rows and the first blocks_per_req[r] entries of block-table row
  * block_tables[r * block_table_stride ...]. q, out and positions hold the requests' rows back

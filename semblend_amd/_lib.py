@@ -58,6 +58,9 @@ SIGNATURES: dict[str, list] = {
     "sb_partial_attention_paged_varlen": [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64p, _i64p,
                                           _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                                           _i64p, _i64p, _i64p, _i32, _vp],
+    "sb_partial_attention_paged_noalloc": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                           _i64, _i64, _i64, _f32, _i64p, _i64p, _i64p, _i32,
+                                           _vp],
     "sb_masked_qkv_projection": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                  _i64, _i64, _i32, _vp],
     "sb_qkv_projection_paged": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -73,6 +76,7 @@ SIZE_QUERIES: dict[str, list] = {
     "sb_partial_attention_paged_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i64, _i32],
     "sb_partial_attention_paged_varlen_workspace_size": [_i64, _i64p, _i64p, _i64, _i64, _i64,
                                                          _i64, _i32],
+    "sb_partial_attention_paged_noalloc_max_scratch": [],
     "sb_masked_qkv_projection_workspace_size": [_i64],
     "sb_qkv_projection_paged_workspace_size": [_i64, _i64, _i32],
 }

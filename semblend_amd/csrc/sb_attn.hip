@@ -36,6 +36,7 @@
 #include "sb_common.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -1411,4 +1412,100 @@ extern "C" int sb_partial_attention_paged_varlen(
   return launch_attention_varlen(fn, a, dtype, num_reqs, rows_per_req, blocks_per_req,
                                  block_table_stride, aligned16, workspace, workspace_bytes,
                                  static_cast<hipStream_t>(stream));
+}
+
+// ------------------------------------------------------------------------------------------
+// No-allocation form of sb_partial_attention_paged: the split-key partials live in a fixed
+// device array of this library instead of a caller workspace.
+// ------------------------------------------------------------------------------------------
+
+namespace sb {
+namespace {
+
+// Largest partial buffer the no-allocation entry serves (the Qwen2.5-7B 16K-context call
+// with 2458 recompute rows needs 72 MB). Every GPU the library runs on holds one copy of the
+// array, from module load until the process ends.
+constexpr int64_t kNoAllocScratchBytes = int64_t{128} << 20;
+
+}  // namespace
+}  // namespace sb
+
+// File scope, one copy per device. Host code never passes this name to a kernel: the host
+// symbol is only a handle; the device address comes from hipGetSymbolAddress below.
+static __device__ __align__(256) char scratch[sb::kNoAllocScratchBytes];
+
+namespace sb {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device (with that
+// device current) and kept; nullptr with the error recorded when the lookup fails.
+void* scratch_for_current_device(const char* fn) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error(std::string(fn) + ": hipGetDevice failed: " + hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error(std::string(fn) + ": device index out of range");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (r != hipSuccess || !ptr) {
+      set_error(std::string(fn) + ": hipGetSymbolAddress(scratch) failed: " +
+                hipGetErrorString(r));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace sb
+
+extern "C" int64_t sb_partial_attention_paged_noalloc_max_scratch(void) {
+  return sb::kNoAllocScratchBytes;
+}
+
+extern "C" int sb_partial_attention_paged_noalloc(
+    void* out, const void* q, const void* kv_cache, const int32_t* block_table,
+    const int32_t* positions, int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t block_size, int64_t num_blocks_total, int64_t num_blocks_per_seq,
+    float scale, const int64_t* qs, const int64_t* os, const int64_t* kvs, int32_t dtype,
+    void* stream) {
+  const char* fn = "sb_partial_attention_paged_noalloc";
+  clear_error();
+  if (num_rows == 0 || num_q_heads == 0 || head_dim == 0) return SB_OK;
+  if (num_blocks_per_seq <= 0) return fail(fn, "empty block table or pool");
+  const int64_t need = sb_partial_attention_paged_workspace_size(
+      num_rows, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks_per_seq, dtype);
+  if (need > kNoAllocScratchBytes)
+    return fail(fn, "this call needs " + std::to_string(need) +
+                        " bytes of split-key partials; the no-allocation entry holds at most " +
+                        std::to_string(kNoAllocScratchBytes) +
+                        " (use sb_partial_attention_paged with a workspace)");
+  AttnArgs a;
+  bool aligned16 = false;
+  const int rc = paged_args(fn, &a, &aligned16, out, q, kv_cache, block_table, positions,
+                            num_q_heads, num_kv_heads, head_dim, block_size, num_blocks_total,
+                            scale, qs, os, kvs, dtype);
+  if (rc) return rc;
+  void* ws = nullptr;
+  if (need > 0) {
+    ws = scratch_for_current_device(fn);
+    if (!ws) return SB_ERR_INVALID_ARGUMENT;
+  }
+  a.num_rows = num_rows;
+  a.nb_per_seq = num_blocks_per_seq;
+  a.kv_len = num_blocks_per_seq * block_size;
+  return launch_attention(fn, a, dtype, num_rows, aligned16, ws, need,
+                          static_cast<hipStream_t>(stream));
 }
