@@ -230,6 +230,33 @@ int sb_nope_permute_paged_kv(void* kv_cache, const int32_t* block_table,
                              int64_t num_blocks_total, int64_t num_blocks_per_seq,
                              const int64_t* kv_strides, int32_t dtype, void* stream);
 
+/* Multi-layer forms of the two permutations above, for the production vLLM path, which
+ * corrects every layer of a request with the same permutation: one launch pair (snapshot,
+ * write) covers all layers. kv_layer_ptrs: device array of num_layers per-layer cache base
+ * addresses (16-byte aligned), all with the element strides kv_strides[5] in
+ * (block, kv, head, pos, dim) order, so the vLLM flash-attn [2, NB, bs, H, D], TRT-LLM
+ * [NB, 2, tpb, H, D] and standard [NB, 2, H, bs, D] caches are all addressed without a copy.
+ * workspace: num_layers times the single-layer size (layer-major snapshot).
+ * Replace the per-layer loop of synapse_kv_connector/model_runner_hook.py:519-585 around
+ * rope_correction.py:407-476 (delta) and :599-697 (NoPE); the reference decodes every cache
+ * as [NB, 2, H, bs, D] (rope_correction.py:432, :623), which the strides here make exact. */
+int sb_permute_paged_kv_with_rope_layers(const uint64_t* kv_layer_ptrs, int64_t num_layers,
+                                         const int32_t* block_table, const int32_t* src_pos,
+                                         const int32_t* tgt_pos, const float* inv_freq,
+                                         void* workspace, int64_t num_pairs, int64_t num_heads,
+                                         int64_t block_size, int64_t head_dim,
+                                         int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                                         const int64_t* kv_strides, int32_t dtype,
+                                         void* stream);
+int sb_nope_permute_paged_kv_layers(const uint64_t* kv_layer_ptrs, int64_t num_layers,
+                                    const int32_t* block_table, const int32_t* src_pos,
+                                    const int32_t* tgt_pos, int64_t num_pairs,
+                                    const int32_t* v_src_pos, const int32_t* v_tgt_pos,
+                                    int64_t num_v_pairs, const float* inv_freq, void* workspace,
+                                    int64_t num_heads, int64_t block_size, int64_t head_dim,
+                                    int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                                    const int64_t* kv_strides, int32_t dtype, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Partial-prefill attention (causal; row at position p attends to keys 0..p)
  * ---------------------------------------------------------------------------------------- */

@@ -51,6 +51,10 @@ SIGNATURES: dict[str, list] = {
                                       _i64, _i64, _i64p, _i32, _vp],
     "sb_nope_permute_paged_kv": [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64,
                                  _i64, _i64, _i64, _i64, _i64p, _i32, _vp],
+    "sb_permute_paged_kv_with_rope_layers": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                                             _i64, _i64, _i64, _i64, _i64p, _i32, _vp],
+    "sb_nope_permute_paged_kv_layers": [_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp,
+                                        _vp, _i64, _i64, _i64, _i64, _i64, _i64p, _i32, _vp],
     "sb_partial_prefill_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                      _f32, _i64p, _i64p, _i64p, _i64p, _i32, _vp],
     "sb_partial_attention_paged": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,

@@ -1018,20 +1018,34 @@ extern "C" int sb_apply_rope_delta_inplace(void* k_plane, const int32_t* block_t
                                                               static_cast<hipStream_t>(stream));
 }
 
-extern "C" int sb_permute_paged_kv_with_rope(void* kv_cache, const int32_t* block_table,
-                                             const int32_t* src_pos, const int32_t* tgt_pos,
-                                             const float* inv_freq, void* workspace,
-                                             int64_t num_pairs, int64_t num_heads,
-                                             int64_t block_size, int64_t head_dim,
-                                             int64_t num_blocks_total,
-                                             int64_t num_blocks_per_seq, const int64_t* ks,
-                                             int32_t dtype, void* stream) {
-  const char* fn = "sb_permute_paged_kv_with_rope";
+namespace sb {
+namespace {
+
+// Dense staging side [L, P, planes, H, D] (contiguous): side_index with a layer stride.
+RowSide side_index_layers(void* base, int64_t num_pairs, int64_t num_heads, int64_t head_dim,
+                          int64_t es, int planes) {
+  RowSide s = side_index(base, num_heads, head_dim, es, planes);
+  s.s_layer = num_pairs * s.s_row;
+  return s;
+}
+
+// Layers per grid.y slice of the permutation launches: one layer per slice (every slice is a
+// pair-parallel grid already; longer groups only help the rotating scatter's cos/sin reuse).
+constexpr int kPermuteLpg = 1;
+
+int permute_impl(const char* fn, void* kv_cache, const uint64_t* layers, int64_t num_layers,
+                 const int32_t* block_table, const int32_t* src_pos, const int32_t* tgt_pos,
+                 const float* inv_freq, void* workspace, int64_t num_pairs, int64_t num_heads,
+                 int64_t block_size, int64_t head_dim, int64_t num_blocks_total,
+                 int64_t num_blocks_per_seq, const int64_t* ks, int32_t dtype,
+                 hipStream_t st) {
   clear_error();
-  if (num_pairs == 0 || num_heads == 0 || head_dim == 0) return SB_OK;
+  if (num_pairs == 0 || num_heads == 0 || head_dim == 0 || num_layers == 0) return SB_OK;
   if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
-  if (!kv_cache || !block_table || !src_pos || !tgt_pos || !inv_freq || !workspace || !ks)
+  if ((!kv_cache && !layers) || !block_table || !src_pos || !tgt_pos || !inv_freq ||
+      !workspace || !ks)
     return fail(fn, "null pointer argument");
+  if (num_layers < 0 || num_layers > 65535) return fail(fn, "invalid layer count");
   if ((head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
   if (block_size <= 0) return fail(fn, "block_size must be positive");
   if (ks[4] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
@@ -1042,11 +1056,11 @@ extern "C" int sb_permute_paged_kv_with_rope(void* kv_cache, const int32_t* bloc
                       ks[0] * es, ks[1] * es, ks[2] * es, ks[3] * es},
                      true, &g))
     return fail(fn, "rows are not aligned for vector access");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  // Phase 1: snapshot every source row (K and V) into workspace[P, 2, H, D].
+  const int grid_y = static_cast<int>(2 * ((num_layers + kPermuteLpg - 1) / kPermuteLpg));
+  // Phase 1: snapshot every source row (K and V) of every layer into workspace[L, P, 2, H, D].
   MoveArgs a{};
-  a.src = side_paged(kv_cache, nullptr, ks, es);
-  a.dst = side_index(workspace, num_heads, head_dim, es, 2);
+  a.src = side_paged(kv_cache, layers, ks, es);
+  a.dst = side_index_layers(workspace, num_pairs, num_heads, head_dim, es, 2);
   a.src_pos = src_pos;
   a.dst_pos = tgt_pos;
   a.block_table = block_table;
@@ -1056,35 +1070,34 @@ extern "C" int sb_permute_paged_kv_with_rope(void* kv_cache, const int32_t* bloc
   a.inv_freq = inv_freq;
   a.num_pairs = num_pairs;
   a.num_heads = static_cast<int>(num_heads);
-  a.num_layers = 1;
-  a.layers_per_group = 1;
+  a.num_layers = static_cast<int>(num_layers);
+  a.layers_per_group = kPermuteLpg;
   a.kv_first = 0;
   a.num_kv = 2;
-  int rc = launch_move<ROT_NONE, ROW_PAGED_POS, ROW_INDEX>(fn, a, dtype, g, 2, st);
+  int rc = launch_move<ROT_NONE, ROW_PAGED_POS, ROW_INDEX>(fn, a, dtype, g, grid_y, st);
   if (rc) return rc;
   // Phase 2: write every target: V copied, K rotated by (tgt - src).
   MoveArgs b = a;
   b.src = a.dst;
   b.dst = a.src;
   b.src_index_check = 1;
-  return launch_move<ROT_DELTA, ROW_INDEX, ROW_PAGED_POS>(fn, b, dtype, g, 2, st);
+  return launch_move<ROT_DELTA, ROW_INDEX, ROW_PAGED_POS>(fn, b, dtype, g, grid_y, st);
 }
 
-extern "C" int sb_nope_permute_paged_kv(void* kv_cache, const int32_t* block_table,
-                                        const int32_t* src_pos, const int32_t* tgt_pos,
-                                        int64_t num_pairs, const int32_t* v_src_pos,
-                                        const int32_t* v_tgt_pos, int64_t num_v_pairs,
-                                        const float* inv_freq, void* workspace,
-                                        int64_t num_heads, int64_t block_size,
-                                        int64_t head_dim, int64_t num_blocks_total,
-                                        int64_t num_blocks_per_seq, const int64_t* ks,
-                                        int32_t dtype, void* stream) {
-  const char* fn = "sb_nope_permute_paged_kv";
+int nope_impl(const char* fn, void* kv_cache, const uint64_t* layers, int64_t num_layers,
+              const int32_t* block_table, const int32_t* src_pos, const int32_t* tgt_pos,
+              int64_t num_pairs, const int32_t* v_src_pos, const int32_t* v_tgt_pos,
+              int64_t num_v_pairs, const float* inv_freq, void* workspace, int64_t num_heads,
+              int64_t block_size, int64_t head_dim, int64_t num_blocks_total,
+              int64_t num_blocks_per_seq, const int64_t* ks, int32_t dtype, hipStream_t st) {
   clear_error();
-  if ((num_pairs == 0 && num_v_pairs == 0) || num_heads == 0 || head_dim == 0) return SB_OK;
+  if ((num_pairs == 0 && num_v_pairs == 0) || num_heads == 0 || head_dim == 0 ||
+      num_layers == 0)
+    return SB_OK;
   if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
-  if (!kv_cache || !block_table || !inv_freq || !workspace || !ks)
+  if ((!kv_cache && !layers) || !block_table || !inv_freq || !workspace || !ks)
     return fail(fn, "null pointer argument");
+  if (num_layers < 0 || num_layers > 65535) return fail(fn, "invalid layer count");
   if (num_pairs > 0 && (!src_pos || !tgt_pos)) return fail(fn, "null pointer argument");
   if (num_v_pairs > 0 && (!v_src_pos || !v_tgt_pos)) return fail(fn, "null pointer argument");
   if ((head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
@@ -1097,9 +1110,9 @@ extern "C" int sb_nope_permute_paged_kv(void* kv_cache, const int32_t* block_tab
                       ks[0] * es, ks[1] * es, ks[2] * es, ks[3] * es},
                      true, &g))
     return fail(fn, "rows are not aligned for vector access");
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid_y = static_cast<int>((num_layers + kPermuteLpg - 1) / kPermuteLpg);
   char* ws_k = static_cast<char*>(workspace);
-  char* ws_v = ws_k + num_pairs * num_heads * head_dim * es;
+  char* ws_v = ws_k + num_layers * num_pairs * num_heads * head_dim * es;
 
   MoveArgs base{};
   base.block_table = block_table;
@@ -1108,58 +1121,133 @@ extern "C" int sb_nope_permute_paged_kv(void* kv_cache, const int32_t* block_tab
   base.nb_per_seq = num_blocks_per_seq;
   base.inv_freq = inv_freq;
   base.num_heads = static_cast<int>(num_heads);
-  base.num_layers = 1;
-  base.layers_per_group = 1;
+  base.num_layers = static_cast<int>(num_layers);
+  base.layers_per_group = kPermuteLpg;
   base.num_kv = 1;
-  const RowSide cache = side_paged(kv_cache, nullptr, ks, es);
+  const RowSide cache = side_paged(kv_cache, layers, ks, es);
+  const RowSide snap_k = side_index_layers(ws_k, num_pairs, num_heads, head_dim, es, 1);
+  const RowSide snap_v = side_index_layers(ws_v, num_v_pairs, num_heads, head_dim, es, 1);
   int rc;
-  // Snapshot K at every source (kv plane 0) and V at every resolved V source (plane 1)
-  // before anything is written.
+  // Snapshot K at every source (kv plane 0) and V at every resolved V source (plane 1) of
+  // every layer before anything is written.
   if (num_pairs > 0) {
     MoveArgs a = base;
     a.src = cache;
-    a.dst = side_index(ws_k, num_heads, head_dim, es, 1);
+    a.dst = snap_k;
     a.src_pos = src_pos;
     a.dst_pos = tgt_pos;
     a.num_pairs = num_pairs;
     a.kv_first = 0;
-    rc = launch_move<ROT_NONE, ROW_PAGED_POS, ROW_INDEX>(fn, a, dtype, g, 1, st);
+    rc = launch_move<ROT_NONE, ROW_PAGED_POS, ROW_INDEX>(fn, a, dtype, g, grid_y, st);
     if (rc) return rc;
   }
   if (num_v_pairs > 0) {
     MoveArgs a = base;
     a.src = cache;
-    a.dst = side_index(ws_v, num_heads, head_dim, es, 1);
+    a.dst = snap_v;
     a.src_pos = v_src_pos;
     a.dst_pos = v_tgt_pos;
     a.num_pairs = num_v_pairs;
     a.kv_first = 1;
-    rc = launch_move<ROT_NONE, ROW_PAGED_POS, ROW_INDEX>(fn, a, dtype, g, 1, st);
+    rc = launch_move<ROT_NONE, ROW_PAGED_POS, ROW_INDEX>(fn, a, dtype, g, grid_y, st);
     if (rc) return rc;
   }
   if (num_v_pairs > 0) {
     MoveArgs a = base;
-    a.src = side_index(ws_v, num_heads, head_dim, es, 1);
+    a.src = snap_v;
     a.dst = cache;
     a.src_pos = v_src_pos;
     a.dst_pos = v_tgt_pos;
     a.num_pairs = num_v_pairs;
     a.kv_first = 1;
     a.src_index_check = 1;
-    rc = launch_move<ROT_NONE, ROW_INDEX, ROW_PAGED_POS>(fn, a, dtype, g, 1, st);
+    rc = launch_move<ROT_NONE, ROW_INDEX, ROW_PAGED_POS>(fn, a, dtype, g, grid_y, st);
     if (rc) return rc;
   }
   if (num_pairs > 0) {
     MoveArgs a = base;
-    a.src = side_index(ws_k, num_heads, head_dim, es, 1);
+    a.src = snap_k;
     a.dst = cache;
     a.src_pos = src_pos;
     a.dst_pos = tgt_pos;
     a.num_pairs = num_pairs;
     a.kv_first = 0;
     a.src_index_check = 1;
-    rc = launch_move<ROT_NOPE, ROW_INDEX, ROW_PAGED_POS>(fn, a, dtype, g, 1, st);
+    rc = launch_move<ROT_NOPE, ROW_INDEX, ROW_PAGED_POS>(fn, a, dtype, g, grid_y, st);
     if (rc) return rc;
   }
   return SB_OK;
+}
+
+}  // namespace
+}  // namespace sb
+
+extern "C" int sb_permute_paged_kv_with_rope(void* kv_cache, const int32_t* block_table,
+                                             const int32_t* src_pos, const int32_t* tgt_pos,
+                                             const float* inv_freq, void* workspace,
+                                             int64_t num_pairs, int64_t num_heads,
+                                             int64_t block_size, int64_t head_dim,
+                                             int64_t num_blocks_total,
+                                             int64_t num_blocks_per_seq, const int64_t* ks,
+                                             int32_t dtype, void* stream) {
+  if (!kv_cache && num_pairs != 0) {
+    clear_error();
+    return fail("sb_permute_paged_kv_with_rope", "null pointer argument");
+  }
+  return permute_impl("sb_permute_paged_kv_with_rope", kv_cache, nullptr, 1, block_table,
+                      src_pos, tgt_pos, inv_freq, workspace, num_pairs, num_heads, block_size,
+                      head_dim, num_blocks_total, num_blocks_per_seq, ks, dtype,
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sb_permute_paged_kv_with_rope_layers(
+    const uint64_t* kv_layer_ptrs, int64_t num_layers, const int32_t* block_table,
+    const int32_t* src_pos, const int32_t* tgt_pos, const float* inv_freq, void* workspace,
+    int64_t num_pairs, int64_t num_heads, int64_t block_size, int64_t head_dim,
+    int64_t num_blocks_total, int64_t num_blocks_per_seq, const int64_t* kv_strides,
+    int32_t dtype, void* stream) {
+  if (!kv_layer_ptrs && num_pairs != 0 && num_layers != 0) {
+    clear_error();
+    return fail("sb_permute_paged_kv_with_rope_layers", "null layer table");
+  }
+  return permute_impl("sb_permute_paged_kv_with_rope_layers", nullptr, kv_layer_ptrs,
+                      num_layers, block_table, src_pos, tgt_pos, inv_freq, workspace,
+                      num_pairs, num_heads, block_size, head_dim, num_blocks_total,
+                      num_blocks_per_seq, kv_strides, dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sb_nope_permute_paged_kv(void* kv_cache, const int32_t* block_table,
+                                        const int32_t* src_pos, const int32_t* tgt_pos,
+                                        int64_t num_pairs, const int32_t* v_src_pos,
+                                        const int32_t* v_tgt_pos, int64_t num_v_pairs,
+                                        const float* inv_freq, void* workspace,
+                                        int64_t num_heads, int64_t block_size,
+                                        int64_t head_dim, int64_t num_blocks_total,
+                                        int64_t num_blocks_per_seq, const int64_t* ks,
+                                        int32_t dtype, void* stream) {
+  if (!kv_cache && (num_pairs != 0 || num_v_pairs != 0)) {
+    clear_error();
+    return fail("sb_nope_permute_paged_kv", "null pointer argument");
+  }
+  return nope_impl("sb_nope_permute_paged_kv", kv_cache, nullptr, 1, block_table, src_pos,
+                   tgt_pos, num_pairs, v_src_pos, v_tgt_pos, num_v_pairs, inv_freq, workspace,
+                   num_heads, block_size, head_dim, num_blocks_total, num_blocks_per_seq, ks,
+                   dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sb_nope_permute_paged_kv_layers(
+    const uint64_t* kv_layer_ptrs, int64_t num_layers, const int32_t* block_table,
+    const int32_t* src_pos, const int32_t* tgt_pos, int64_t num_pairs,
+    const int32_t* v_src_pos, const int32_t* v_tgt_pos, int64_t num_v_pairs,
+    const float* inv_freq, void* workspace, int64_t num_heads, int64_t block_size,
+    int64_t head_dim, int64_t num_blocks_total, int64_t num_blocks_per_seq,
+    const int64_t* kv_strides, int32_t dtype, void* stream) {
+  if (!kv_layer_ptrs && (num_pairs != 0 || num_v_pairs != 0) && num_layers != 0) {
+    clear_error();
+    return fail("sb_nope_permute_paged_kv_layers", "null layer table");
+  }
+  return nope_impl("sb_nope_permute_paged_kv_layers", nullptr, kv_layer_ptrs, num_layers,
+                   block_table, src_pos, tgt_pos, num_pairs, v_src_pos, v_tgt_pos, num_v_pairs,
+                   inv_freq, workspace, num_heads, block_size, head_dim, num_blocks_total,
+                   num_blocks_per_seq, kv_strides, dtype, static_cast<hipStream_t>(stream));
 }

@@ -34,7 +34,12 @@ __all__ = [
     "apply_rope_delta_inplace",
     "inv_freq_table",
     "nope_permute_paged_kv",
+    "nope_permute_paged_kv_layers",
+    "paged_layout",
     "permute_paged_kv_with_rope",
+    "permute_paged_kv_with_rope_layers",
+    "prepare_permute_paged_kv_layers",
+    "standard_view",
     "rope_correct_k",
     "rope_correct_k_inplace",
     "rope_correct_scatter_paged",
@@ -136,17 +141,25 @@ def rope_correct_scatter_paged_layers(
     return kv_caches
 
 
-class PreparedScatter:
-    """A validated multi-layer paged scatter bound to its tensors' addresses; calling it
-    enqueues the launch on torch's current stream. It holds the device tables and index
-    tensors it reads, so they live as long as it does."""
+class PreparedLaunch:
+    """Validated launches of the library bound to their tensors' addresses; calling the object
+    enqueues them on torch's current stream. It holds the device tables, index tensors and
+    workspaces they read, so those live as long as it does."""
 
-    def __init__(self, entry: str, args: tuple, keep: tuple, device: torch.device):
+    def __init__(self, entry: str, args: tuple, keep: tuple, device: torch.device,
+                 more: tuple = ()):
+        self.launches = [(entry, args)] + list(more)
         self.entry, self.args, self.keep, self.device = entry, args, keep, device
 
     def __call__(self) -> None:
         with torch.cuda.device(self.device):
-            _lib.call(self.entry, *self.args, _lib.stream_handle(self.device))
+            st = _lib.stream_handle(self.device)
+            for entry, args in self.launches:
+                _lib.call(entry, *args, st)
+
+
+# The multi-layer scatter's prepared form (kept under its first name).
+PreparedScatter = PreparedLaunch
 
 
 def prepare_scatter_paged_layers(
@@ -301,8 +314,7 @@ def permute_paged_kv_with_rope(
     dev = _lib.require_device(kv_cache)
     nb_total, _, num_heads, block_size, head_dim = kv_cache.shape
     _check_head_dim(head_dim, head_dim, "permute_paged_kv_with_rope")
-    src = torch.tensor([p[0] for p in permutation], dtype=torch.int32).to(dev)
-    tgt = torch.tensor([p[1] for p in permutation], dtype=torch.int32).to(dev)
+    src, tgt = _pairs_on_device(permutation, dev)
     bt = _lib.as_index(block_table, dev)
     inv_freq = inv_freq_table(rope_base, head_dim, dev)
     ws = torch.empty((len(permutation), 2, num_heads, head_dim), dtype=kv_cache.dtype,
@@ -351,12 +363,10 @@ def nope_permute_paged_kv(
     dev = _lib.require_device(kv_cache)
     nb_total, _, num_heads, block_size, head_dim = kv_cache.shape
     _check_head_dim(head_dim, head_dim, "nope_permute_paged_kv")
-    src = torch.tensor([p[0] for p in permutation], dtype=torch.int32).to(dev)
-    tgt = torch.tensor([p[1] for p in permutation], dtype=torch.int32).to(dev)
+    src, tgt = _pairs_on_device(permutation, dev)
     vmoves = _sequential_v_moves(permutation)
     # holds maps target -> original source; emit (source, target) pairs.
-    vsrc = torch.tensor([s for _, s in vmoves], dtype=torch.int32).to(dev)
-    vtgt = torch.tensor([t for t, _ in vmoves], dtype=torch.int32).to(dev)
+    vsrc, vtgt = _pairs_on_device([(s_, t_) for t_, s_ in vmoves], dev)
     bt = _lib.as_index(block_table, dev)
     inv_freq = inv_freq_table(rope_base, head_dim, dev)
     ws = torch.empty((len(permutation) + len(vmoves), num_heads, head_dim),
@@ -453,3 +463,169 @@ def apply_rope_delta_inplace(
             _lib.i64_array(kst), _lib.dtype_code(kv_cache), _lib.stream_handle(dev),
         )
     return modified
+
+
+# ------------------------------------------------------------------------------------------
+# Engine cache layouts and the multi-layer permutations
+# ------------------------------------------------------------------------------------------
+
+_LAYOUT_AXES = {
+    # layout -> axes of (block, kv, head, pos, dim) in the tensor's own dimension order
+    "standard": (0, 1, 2, 3, 4),   # [NB, 2, H, bs, D]
+    "vllm": (1, 0, 3, 2, 4),       # [2, NB, bs, H, D]   (vLLM flash-attn)
+    "trt": (0, 1, 3, 2, 4),        # [NB, 2, tpb, H, D]  (TensorRT-LLM)
+}
+
+
+def _resolve_layout(kv_cache: torch.Tensor, layout: str | None) -> str:
+    if layout is None:
+        # the reference's detection rule (semblend_core/rope_correction.py:740); TRT-LLM
+        # caches cannot be told from standard ones by shape and need layout="trt"
+        vllm = kv_cache.dim() == 5 and kv_cache.shape[0] == 2 and kv_cache.shape[1] != 2
+        return "vllm" if vllm else "standard"
+    if layout not in _LAYOUT_AXES:
+        raise ValueError(f"layout must be one of {sorted(_LAYOUT_AXES)}, got {layout!r}")
+    return layout
+
+
+def standard_view(kv_cache: torch.Tensor, layout: str | None = None) -> torch.Tensor:
+    """The cache as a [num_blocks, 2, num_heads, block_size, head_dim] view (no copy), from the
+    standard, vLLM flash-attn [2, NB, bs, H, D] or TRT-LLM [NB, 2, tpb, H, D] layout. Every
+    entry point of this package that takes a paged cache addresses it through its strides,
+    so the view is what they take."""
+    if kv_cache.dim() != 5:
+        raise ValueError("a paged cache is 5-dimensional")
+    return kv_cache.permute(*_LAYOUT_AXES[_resolve_layout(kv_cache, layout)])
+
+
+def paged_layout(kv_cache: torch.Tensor, layout: str | None = None):
+    """(num_blocks, num_heads, block_size, head_dim, element strides in (block, kv, head, pos,
+    dim) order) of a paged cache in the given layout (None: the reference's detection rule)."""
+    v = standard_view(kv_cache, layout)
+    if v.shape[1] != 2:
+        raise ValueError(f"no K/V axis of size 2 in a {layout or 'standard'} cache of shape "
+                         f"{tuple(kv_cache.shape)}")
+    nb, _, h, bs, d = v.shape
+    return nb, h, bs, d, tuple(v.stride())
+
+
+def _pairs_on_device(permutation, dev: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    """(sources, targets) int32 device tensors from a list of (src, tgt) pairs or a [P, 2]
+    tensor, uploaded once from pinned memory without blocking the host."""
+    if isinstance(permutation, torch.Tensor):
+        pairs = permutation.reshape(-1, 2).to(torch.int32)
+    else:
+        pairs = torch.tensor([(int(a), int(b)) for a, b in permutation],
+                             dtype=torch.int32).reshape(-1, 2)
+    if pairs.device.type == "cpu":
+        pairs = pairs.contiguous().pin_memory().to(dev, non_blocking=True)
+    else:
+        pairs = pairs.to(dev)
+    pairs = pairs.t().contiguous()
+    return pairs[0], pairs[1]
+
+
+def prepare_permute_paged_kv_layers(
+    kv_caches: list[torch.Tensor],
+    block_table: torch.Tensor,
+    permutation,
+    rope_base: float = 10000.0,
+    nope: bool = False,
+    layout: str | None = None,
+    max_workspace_bytes: int = 1 << 30,
+) -> PreparedLaunch | None:
+    """Validate and bind the permutation of every layer's cache (``permute_paged_kv_with_rope``
+    semantics, or ``nope_permute_paged_kv`` with ``nope=True``) once: the pairs are uploaded
+    once, the layer table and the snapshot workspace are built once, and calling the returned
+    object enqueues one snapshot launch and one write launch per group of layers (all layers
+    in one group while the snapshot fits ``max_workspace_bytes``). Each call applies the
+    permutation again (it is not idempotent). Returns None for an empty permutation.
+
+    kv_caches: one cache per layer, all in ``layout`` ("standard" [NB, 2, H, bs, D], "vllm"
+    [2, NB, bs, H, D], "trt" [NB, 2, tpb, H, D]; None: the reference's detection rule) with
+    the same shape, strides and dtype; block_table: [num_blocks_per_seq]; permutation: list of
+    (source, target) logical positions, or a [P, 2] integer tensor.
+    Replaces the per-layer loop of synapse_kv_connector/model_runner_hook.py:519-585.
+    """
+    if not kv_caches or len(permutation) == 0:
+        return None
+    dev = _lib.require_device(*kv_caches)
+    _check_uniform(kv_caches, "kv_caches")
+    nb, heads, bs, hd, st = paged_layout(kv_caches[0], layout)
+    _check_head_dim(hd, hd, "prepare_permute_paged_kv_layers")
+    if st[4] != 1:
+        raise ValueError("head_dim must be contiguous (stride 1)")
+    src, tgt = _pairs_on_device(permutation, dev)
+    num_pairs = int(src.shape[0])
+    bt = _lib.as_index(block_table, dev)
+    inv = inv_freq_table(rope_base, hd, dev)
+    es = kv_caches[0].element_size()
+    keep = [src, tgt, bt, inv]
+    if nope:
+        if isinstance(permutation, torch.Tensor):
+            permutation = [tuple(p) for p in permutation.reshape(-1, 2).tolist()]
+        vmoves = _sequential_v_moves(list(permutation))
+        vsrc, vtgt = _pairs_on_device([(s_, t_) for t_, s_ in vmoves], dev)
+        keep += [vsrc, vtgt]
+        per_layer = (num_pairs + len(vmoves)) * heads * hd * es
+    else:
+        per_layer = num_pairs * 2 * heads * hd * es
+    group = max(1, min(len(kv_caches), max_workspace_bytes // max(per_layer, 1)))
+    ws = torch.empty(group * per_layer, dtype=torch.uint8, device=dev)
+    keep.append(ws)
+    strides = _lib.i64_array(st)
+    keep.append(strides)
+    launches = []
+    for g0 in range(0, len(kv_caches), group):
+        layers = kv_caches[g0:g0 + group]
+        tab = _lib.address_table(layers, dev)
+        keep.append(tab)
+        if nope:
+            args = (tab.data_ptr(), len(layers), bt.data_ptr(), src.data_ptr(), tgt.data_ptr(),
+                    num_pairs, vsrc.data_ptr(), vtgt.data_ptr(), int(vsrc.shape[0]),
+                    inv.data_ptr(), ws.data_ptr(), heads, bs, hd, nb, bt.shape[0], strides,
+                    _lib.dtype_code(kv_caches[0]))
+            launches.append(("sb_nope_permute_paged_kv_layers", args))
+        else:
+            args = (tab.data_ptr(), len(layers), bt.data_ptr(), src.data_ptr(), tgt.data_ptr(),
+                    inv.data_ptr(), ws.data_ptr(), num_pairs, heads, bs, hd, nb, bt.shape[0],
+                    strides, _lib.dtype_code(kv_caches[0]))
+            launches.append(("sb_permute_paged_kv_with_rope_layers", args))
+    return PreparedLaunch(launches[0][0], launches[0][1], tuple(keep), dev,
+                          more=tuple(launches[1:]))
+
+
+def permute_paged_kv_with_rope_layers(
+    kv_caches: list[torch.Tensor],
+    block_table: torch.Tensor,
+    permutation,
+    rope_base: float = 10000.0,
+    layout: str | None = None,
+) -> None:
+    """``permute_paged_kv_with_rope`` applied to every layer's cache in one launch pair, in the
+    standard, vLLM flash-attn or TRT-LLM layout (addressed through strides, so the vLLM
+    caches the reference mis-decodes at rope_correction.py:432 are corrected exactly).
+    Extension with no reference counterpart; replaces the per-layer loop of
+    synapse_kv_connector/model_runner_hook.py:519-585. See
+    :func:`prepare_permute_paged_kv_layers` to bind once and launch per step."""
+    call = prepare_permute_paged_kv_layers(kv_caches, block_table, permutation, rope_base,
+                                           nope=False, layout=layout)
+    if call is not None:
+        call()
+
+
+def nope_permute_paged_kv_layers(
+    kv_caches: list[torch.Tensor],
+    block_table: torch.Tensor,
+    permutation,
+    rope_base: float = 10000.0,
+    layout: str | None = None,
+) -> None:
+    """``nope_permute_paged_kv`` (K: R(tgt) R(-src); V: the reference's sequential copies) on
+    every layer's cache in one set of launches, in any of the three layouts. Extension with no
+    reference counterpart; replaces the NoPE branch of the per-layer loop at
+    synapse_kv_connector/model_runner_hook.py:543-551."""
+    call = prepare_permute_paged_kv_layers(kv_caches, block_table, permutation, rope_base,
+                                           nope=True, layout=layout)
+    if call is not None:
+        call()

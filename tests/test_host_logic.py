@@ -312,3 +312,16 @@ def test_pair_length_mismatch_is_rejected_before_launch():
     for call in calls:
         with pytest.raises(ValueError, match="differ in length"):
             call()
+
+
+def test_layout_detection_and_empty():
+    """Engine cache layouts resolve to the standard [NB, 2, H, bs, D] view; unknown layout
+    names are refused; an empty permutation prepares nothing."""
+    vllm = torch.zeros(2, 12, 16, 4, 64)
+    assert rc.paged_layout(vllm)[:4] == (12, 4, 16, 64)
+    assert rc.standard_view(vllm).shape == (12, 2, 4, 16, 64)
+    std = torch.zeros(12, 2, 4, 16, 64)
+    assert rc.paged_layout(std)[:4] == (12, 4, 16, 64)
+    with pytest.raises(ValueError):
+        rc.paged_layout(std, "nhd")
+    assert rc.prepare_permute_paged_kv_layers([std], torch.zeros(2), []) is None
