@@ -15,11 +15,16 @@ One step is one pass of the path over synthetic inputs resident in HBM:
 
 The reported ``value`` is the attention phase's throughput in TFLOP/s (useful causal FLOPs
 4 * D * Hq * sum(p + 1)); the scatter and RoPE phases are reported in GB/s of useful bytes
-(each moved row read once and written once). Each phase's launches are captured once into a
-HIP graph and the timed steps replay the graphs (as a serving loop would), so host launch
-overhead stays out of the phase times; every phase is timed with HIP events on the stream
-its kernels run on and ``ms_per_step`` is the sum of the three phase times. A separate eager
-pass brackets each library kernel launch with HIP events inside the library (``kernels``);
+(each moved row read once and written once). The timed steps are K whole steps, each one HIP
+graph replay (RoPE, scatter and attention launches back to back inside it, as a serving loop
+would launch them), enqueued back to back between one pair of HIP events: ``ms_per_step``.
+Phase durations come from the eager pass that precedes the graphs, in which the library
+brackets each of its kernel launches with HIP events that the runtime stamps with the
+kernel's own start and end (``kernels``); a phase is its kernels (attention: the MFMA kernel
+and the split-key merge). ``launch_inclusive_ms`` times each phase as its own graph with
+events around every replay, which adds one graph launch (about 8 us on this GPU) per phase.
+The RoPE and scatter phases stream 2 GB through the 256 MB Infinity Cache before every
+attention launch, so no timed kernel finds its inputs cached from the previous step.
 ``roofline`` prices the MFMA attention kernel's average launch against the bf16 peak.
 ``phases.copy_ceiling`` is a plain 1 GiB device copy, the achievable HBM rate.
 ``rope_scatter`` times the scatter workload again with K rotated on the way (one donor, and
@@ -738,6 +743,12 @@ def main() -> int:
     rope_bytes = float(L * HKV * ROPE_TOKENS * D * 2 * 2)
 
     def phase_rope(i):
+        # every position is named once (d = 0..8191): the one-launch distinct-donor form
+        rc.rope_correct_k_inplace(inp["rope_k"][i % 4], inp["rope_d"], inp["rope_t"],
+                                  head_dim=D, rope_base=ROPE_BASE, distinct_donors=True)
+
+    def rope_indexed(i):
+        # the general form (per-position pair index built on the device, then the rotation)
         rc.rope_correct_k_inplace(inp["rope_k"][i % 4], inp["rope_d"], inp["rope_t"],
                                   head_dim=D, rope_base=ROPE_BASE)
 
@@ -771,21 +782,41 @@ def main() -> int:
         if n:
             kernels[name] = {"launches": n, "avg_us": round(1e3 * total / n, 2)}
 
-    log("capturing one HIP graph per phase")
+    log("capturing one HIP graph per step (RoPE, scatter, attention) and one per phase")
+
+    def one_step(c):
+        phase_rope(c)
+        phase_scatter(c)
+        phase_attn(c)
+
+    step_graphs = [capture(lambda c=c: one_step(c)) for c in range(4)]
     graphs = {
         "rope": [capture(lambda c=c: phase_rope(c)) for c in range(4)],
         "scatter": [capture(lambda: phase_scatter(0))],
         "attention": [capture(lambda: phase_attn(0))],
     }
-    for name, gs in graphs.items():
-        for g in gs:
-            g.replay()
+    for g in step_graphs:
+        g.replay()
     torch.cuda.synchronize()
 
-    log(f"timing {args.steps} steps (graph replays)")
-    ev = {name: [] for name, _ in phases}
+    # The timed region: K whole steps, each one graph replay (the step's kernels run back to
+    # back inside it), all enqueued back to back between one pair of HIP events.
+    log(f"timing {args.steps} steps (whole-step graph replays)")
     torch.cuda.synchronize()
     t_wall0 = time.perf_counter()
+    e_step0 = torch.cuda.Event(enable_timing=True)
+    e_step1 = torch.cuda.Event(enable_timing=True)
+    e_step0.record()
+    for i in range(args.steps):
+        step_graphs[i % 4].replay()
+    e_step1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall0
+    ms_per_step = e_step0.elapsed_time(e_step1) / args.steps
+
+    # Launch-inclusive phase times: each phase as its own graph, events around every replay,
+    # phases interleaved as in a step (each includes one graph launch, ~8 us on this GPU).
+    ev = {name: [] for name, _ in phases}
     for i in range(args.steps):
         for name, _ in phases:
             gs = graphs[name]
@@ -796,15 +827,29 @@ def main() -> int:
             e1.record()
             ev[name].append((e0, e1))
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall0
+    launch_ms = {name: sum(a.elapsed_time(b) for a, b in v) / len(v) for name, v in ev.items()}
+    idx_graphs = [capture(lambda c=c: rope_indexed(c)) for c in range(4)]
+    idx_ev = []
+    for i in range(args.steps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        idx_graphs[i % 4].replay()
+        e1.record()
+        idx_ev.append((e0, e1))
+        phase_scatter(0)  # keep the interleaving: K must not stay in the Infinity Cache
+    torch.cuda.synchronize()
+    rope_idx_ms = sum(a.elapsed_time(b) for a, b in idx_ev) / len(idx_ev)
+    del idx_graphs, step_graphs
     copy_gbps = copy_ceiling(dev)
     gemm_tflops = gemm_ceiling(dev)
     log("kernels (avg us): " + ", ".join(f"{k} {v['avg_us']}" for k, v in kernels.items())
         + f"; copy ceiling {copy_gbps:.0f} GB/s")
-    ms = {name: [a.elapsed_time(b) for a, b in pairs] for name, pairs in ev.items()}
-    med = {name: sorted(v)[len(v) // 2] for name, v in ms.items()}
-    avg = {name: sum(v) / len(v) for name, v in ms.items()}
-    ms_per_step = sum(avg.values())
+    # Phase durations on the GPU: the phase's kernels, each bracketed by HIP events that the
+    # runtime stamps with the kernel's start and end, in the interleaved eager pass above.
+    avg = {"rope": kernels["rope_rows"]["avg_us"] * 1e-3,
+           "scatter": kernels["move_rows"]["avg_us"] * 1e-3,
+           "attention": (kernels["attn_mfma"]["avg_us"] + kernels["attn_merge"]["avg_us"]) * 1e-3}
 
     attn_tflops = attn_flops / (avg["attention"] * 1e-3) / 1e12
     # Dominant kernel: the MFMA attention kernel, one launch per step.
@@ -850,19 +895,27 @@ def main() -> int:
             "traffic": MEASURED_TRAFFIC_BYTES["attn_mfma"],
         },
         "phases": {
-            "attention": {"ms": round(avg["attention"], 4), "ms_median": round(med["attention"], 4),
+            "attention": {"ms": round(avg["attention"], 4),
+                          "launch_inclusive_ms": round(launch_ms["attention"], 4),
                           "tflops": round(attn_tflops, 2),
                           "frac_of_peak": round(attn_tflops / BF16_PEAK_TFLOPS, 4)},
-            "scatter": {"ms": round(avg["scatter"], 4), "ms_median": round(med["scatter"], 4),
+            "scatter": {"ms": round(avg["scatter"], 4),
+                        "launch_inclusive_ms": round(launch_ms["scatter"], 4),
                         "gbps": round(scatter_gbps, 1),
                         "kernel_gbps": round(scatter_bytes / (kernels["move_rows"]["avg_us"] * 1e-6) / 1e9, 1),
                         "traffic_bytes": MEASURED_TRAFFIC_BYTES["move_rows"],
                         "frac_of_peak": round(scatter_gbps / HBM_PEAK_GBS, 4)},
-            "rope": {"ms": round(avg["rope"], 4), "ms_median": round(med["rope"], 4),
+            "rope": {"ms": round(avg["rope"], 4),
+                     "launch_inclusive_ms": round(launch_ms["rope"], 4),
                      "gbps": round(rope_gbps, 1),
                      "kernel_gbps": round(rope_bytes / (kernels["rope_rows"]["avg_us"] * 1e-6) / 1e9, 1),
                      "traffic_bytes": MEASURED_TRAFFIC_BYTES["rope_rows"],
-                     "frac_of_peak": round(rope_gbps / HBM_PEAK_GBS, 4)},
+                     "frac_of_peak": round(rope_gbps / HBM_PEAK_GBS, 4),
+                     "what": "one launch per step (donor positions distinct: d = 0..8191)",
+                     "indexed": {"ms": round(rope_idx_ms, 4),
+                                 "gbps": round(rope_bytes / (rope_idx_ms * 1e-3) / 1e9, 1),
+                                 "what": "general form: pair index on the device, then the "
+                                         "rotation (two launches)"}},
             "gemm_ceiling": {"tflops": round(gemm_tflops, 1),
                              "frac_of_peak": round(gemm_tflops / BF16_PEAK_TFLOPS, 4),
                              "what": "8192^3 bf16 torch matmul (hipBLASLt), 10 repeats"},

@@ -193,6 +193,17 @@ int sb_rope_correct_k(void* out, const void* k, const int32_t* donor_pos,
                       int64_t head_dim, const int64_t* out_strides, const int64_t* k_strides,
                       int32_t dtype, void* stream);
 
+/* In-place sb_rope_correct_k for callers that guarantee that no donor position repeats
+ * (for instance the identity d = 0..S-1 of a whole-sequence correction): one thread group per
+ * pair rotates the rows at its donor position, with no per-position index and no workspace,
+ * so a call is one launch. Repeated donor positions race here; use sb_rope_correct_k for
+ * them. Same rotation and rounding as sb_rope_correct_k.
+ * Replaces semblend_core/rope_correction.py:336-399 for distinct donor positions. */
+int sb_rope_correct_k_distinct(void* k, const int32_t* donor_pos, const int32_t* target_pos,
+                               const float* inv_freq, int64_t num_pairs, int64_t num_layers,
+                               int64_t num_heads, int64_t seq_len, int64_t head_dim,
+                               const int64_t* k_strides, int32_t dtype, void* stream);
+
 /* In-place rotation of K rows in a paged cache by one delta:
  *   K[bt[p / bs], h, p % bs, :] = R(delta) K[...], applied repeat[i] times (rounded to dtype
  *   after each application) for positions[i]. repeat may be NULL (once each).

@@ -45,6 +45,8 @@ SIGNATURES: dict[str, list] = {
                                           _vp],
     "sb_rope_correct_k": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p,
                           _i64p, _i32, _vp],
+    "sb_rope_correct_k_distinct": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p,
+                                   _i32, _vp],
     "sb_apply_rope_delta_inplace": [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                     _i64, _i64, _i64p, _i32, _vp],
     "sb_permute_paged_kv_with_rope": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,

@@ -48,6 +48,10 @@ enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3 };
 #ifndef SB_ROPE_TARGET_BLOCKS
 #define SB_ROPE_TARGET_BLOCKS 4096
 #endif
+// (layer, head) rows per thread of the row-centric RoPE; 0 derives it from the block target.
+#ifndef SB_ROPE_ROWS_PER_GROUP
+#define SB_ROPE_ROWS_PER_GROUP 0
+#endif
 // Pair movers' access hints (nontemporal loads / stores).
 #ifndef SB_MOVE_NT_LOAD
 #define SB_MOVE_NT_LOAD 1
@@ -422,12 +426,26 @@ __global__ __launch_bounds__(kThreads) void rope_rows_kernel(RopeRowsArgs a) {
   constexpr int NP = E / 2;
   const int tpr = 1 << a.tpr_log2;
   const int lane = threadIdx.x & (tpr - 1);
-  const int64_t s = static_cast<int64_t>(blockIdx.x) * (kThreads >> a.tpr_log2) +
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * (kThreads >> a.tpr_log2) +
                     (threadIdx.x >> a.tpr_log2);
-  if (s >= a.seq_len) return;
-  const int cnt = a.ws[s];
-  if (cnt == 0 && a.in_place) return;
-  const int64_t first = a.num_pairs - a.ws[a.seq_len + s];
+  int64_t s, first;
+  int cnt;
+  if (a.ws) {
+    // Row-centric: thread t owns position t; the index names its pairs.
+    s = t;
+    if (s >= a.seq_len) return;
+    cnt = a.ws[s];
+    if (cnt == 0 && a.in_place) return;
+    first = a.num_pairs - a.ws[a.seq_len + s];
+  } else {
+    // Pair-centric (in place, donor positions distinct by the caller's guarantee): thread t
+    // owns pair t and rotates the row at its donor position.
+    if (t >= a.num_pairs) return;
+    s = a.dpos[t];
+    if (s < 0 || s >= a.seq_len) return;
+    cnt = 1;
+    first = t;
+  }
 
   const int total_rows = a.num_layers * a.num_heads;
   const int r_begin = static_cast<int>(blockIdx.y) * a.rows_per_group;
@@ -882,13 +900,44 @@ extern "C" int sb_composite_scatter_paged_layers(
   return SB_OK;
 }
 
+namespace sb {
+namespace {
+int rope_k_impl(const char* fn, void* out, const void* k, const int32_t* donor_pos,
+                const int32_t* target_pos, const float* inv_freq, int32_t* workspace,
+                bool distinct, int64_t num_pairs, int64_t num_layers, int64_t num_heads,
+                int64_t seq_len, int64_t head_dim, const int64_t* os, const int64_t* ks,
+                int32_t dtype, void* stream);
+}  // namespace
+}  // namespace sb
+
 extern "C" int sb_rope_correct_k(void* out, const void* k, const int32_t* donor_pos,
                                  const int32_t* target_pos, const float* inv_freq,
                                  int32_t* workspace, int64_t num_pairs, int64_t num_layers,
                                  int64_t num_heads, int64_t seq_len, int64_t head_dim,
                                  const int64_t* os, const int64_t* ks, int32_t dtype,
                                  void* stream) {
-  const char* fn = "sb_rope_correct_k";
+  return rope_k_impl("sb_rope_correct_k", out, k, donor_pos, target_pos, inv_freq, workspace,
+                     false, num_pairs, num_layers, num_heads, seq_len, head_dim, os, ks, dtype,
+                     stream);
+}
+
+extern "C" int sb_rope_correct_k_distinct(void* k, const int32_t* donor_pos,
+                                          const int32_t* target_pos, const float* inv_freq,
+                                          int64_t num_pairs, int64_t num_layers,
+                                          int64_t num_heads, int64_t seq_len, int64_t head_dim,
+                                          const int64_t* ks, int32_t dtype, void* stream) {
+  return rope_k_impl("sb_rope_correct_k_distinct", k, k, donor_pos, target_pos, inv_freq,
+                     nullptr, true, num_pairs, num_layers, num_heads, seq_len, head_dim, ks, ks,
+                     dtype, stream);
+}
+
+namespace sb {
+namespace {
+int rope_k_impl(const char* fn, void* out, const void* k, const int32_t* donor_pos,
+                const int32_t* target_pos, const float* inv_freq, int32_t* workspace,
+                bool distinct, int64_t num_pairs, int64_t num_layers, int64_t num_heads,
+                int64_t seq_len, int64_t head_dim, const int64_t* os, const int64_t* ks,
+                int32_t dtype, void* stream) {
   clear_error();
   if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
   if (!out || !k || !os || !ks) return fail(fn, "null pointer argument");
@@ -908,12 +957,16 @@ extern "C" int sb_rope_correct_k(void* out, const void* k, const int32_t* donor_
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool in_place = out == k;
   if (num_pairs == 0 && in_place) return SB_OK;
-  if (!workspace) return fail(fn, "null workspace");
+  if (distinct && !in_place) return fail(fn, "the distinct-donor form runs in place");
+  if (!distinct && !workspace) return fail(fn, "null workspace");
 
-  // Per-position pair index: counts in ws[0:S], (P - first pair) in ws[S:2S].
-  int32_t* ws = workspace;
+  // Per-position pair index: counts in ws[0:S], (P - first pair) in ws[S:2S]. Not needed
+  // when the caller guarantees distinct donor positions (one thread per pair, in place).
+  int32_t* ws = distinct ? nullptr : workspace;
   const int64_t n = 2 * seq_len;
-  if (n + num_pairs <= kIndexFusedMax) {
+  if (distinct) {
+    // no index
+  } else if (n + num_pairs <= kIndexFusedMax) {
     SB_LAUNCH("rope_index", rope_index_fused_kernel, dim3(1), dim3(kIndexThreads), st,
               donor_pos, num_pairs, seq_len, ws);
   } else {
@@ -947,11 +1000,16 @@ extern "C" int sb_rope_correct_k(void* out, const void* k, const int32_t* donor_
   const int total_rows = static_cast<int>(num_layers * num_heads);
   // Split the (layer, head) rows over grid.y so that short sequences still fill 256 CUs.
   const int64_t rows_per_block = kThreads >> g.tpr_log2;
-  const int64_t gx = (seq_len + rows_per_block - 1) / rows_per_block;
+  const int64_t units = distinct ? num_pairs : seq_len;  // threads groups: pairs or positions
+  const int64_t gx = (units + rows_per_block - 1) / rows_per_block;
+  if (gx > 0x7fffffff) return fail(fn, "grid too large");
   int splits = 1;
   while (splits < total_rows && gx * splits < SB_ROPE_TARGET_BLOCKS) splits *= 2;
   if (splits > total_rows) splits = total_rows;
   a.rows_per_group = (total_rows + splits - 1) / splits;
+#if SB_ROPE_ROWS_PER_GROUP > 0
+  a.rows_per_group = total_rows < SB_ROPE_ROWS_PER_GROUP ? total_rows : SB_ROPE_ROWS_PER_GROUP;
+#endif
   const int gy = (total_rows + a.rows_per_group - 1) / a.rows_per_group;
   dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
 #define SB_ROWS_CASE(DT, VB)                                                              \
@@ -970,6 +1028,8 @@ extern "C" int sb_rope_correct_k(void* out, const void* k, const int32_t* donor_
 #undef SB_ROWS_CASE
   return fail(fn, "unsupported dtype / vector width combination");
 }
+}  // namespace
+}  // namespace sb
 
 extern "C" int sb_apply_rope_delta_inplace(void* k_plane, const int32_t* block_table,
                                            const int32_t* positions, const int32_t* repeat,

@@ -280,12 +280,42 @@ def rope_correct_k_inplace(
     target_positions: torch.Tensor,
     head_dim: int = 128,
     rope_base: float = 10000.0,
+    distinct_donors: bool = False,
 ) -> torch.Tensor:
     """In-place form of :func:`rope_correct_k` (same result, written back into k_tensor).
 
-    Only rows named by a pair are read and written. Extension with no reference counterpart.
+    Only rows named by a pair are read and written. ``distinct_donors=True`` is the caller's
+    guarantee that no donor position repeats (e.g. a whole-sequence correction with
+    d = 0..S-1): the rows are then rotated pair by pair in one launch, without building the
+    per-position index that orders repeated rotations (a repeated position would race).
+    Extension with no reference counterpart.
     """
     _lib.require_device(k_tensor)
+    if distinct_donors and k_tensor.stride(-1) == 1:
+        dev = k_tensor.device
+        if k_tensor.dim() == 3:
+            k4 = k_tensor.unsqueeze(0)
+        elif k_tensor.dim() == 4:
+            k4 = k_tensor
+        else:
+            raise ValueError("k_tensor must be [H, S, D] or [L, H, S, D]")
+        num_layers, num_heads, seq_len, hd = k4.shape
+        _check_head_dim(head_dim, hd, "rope_correct_k_inplace")
+        d = _lib.as_index(donor_positions, dev)
+        t = _lib.as_index(target_positions, dev)
+        if d.shape[0] != t.shape[0]:
+            raise ValueError("donor_positions and target_positions differ in length")
+        if d.shape[0] == 0:
+            return k_tensor
+        inv_freq = inv_freq_table(rope_base, head_dim, dev)
+        with torch.cuda.device(dev):
+            _lib.call(
+                "sb_rope_correct_k_distinct",
+                k4.data_ptr(), d.data_ptr(), t.data_ptr(), inv_freq.data_ptr(), d.shape[0],
+                num_layers, num_heads, seq_len, head_dim, _lib.strides(k4),
+                _lib.dtype_code(k4), _lib.stream_handle(dev),
+            )
+        return k_tensor
     if k_tensor.stride(-1) != 1:
         work = k_tensor.contiguous()
         _rope_k(work, work, donor_positions, target_positions, head_dim, rope_base)

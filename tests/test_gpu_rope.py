@@ -161,6 +161,44 @@ def test_rope_correct_k_full_size_7b_inplace(dev):
     assert float(err.max()) <= 0.07, float(err.max())  # two bf16 roundings of |x| <= ~6
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_rope_correct_k_distinct_donors(dev, dtype):
+    """The one-launch form for distinct donor positions (shuffled pair order, a donor out of
+    range skipped) lands the same bits as the indexed in-place form, and matches the oracle."""
+    k = randn((3, 4, 600, 64), dtype, 49)
+    g = gen(50)
+    dp = torch.randperm(600, generator=g)[:450].to(torch.int32)
+    dp[7] = 600  # out of range: skipped by both forms (and by the oracle)
+    tp = torch.randint(-3000, 3000, (450,), generator=g, dtype=torch.int32)
+    want = ref.rope_correct_k(k, dp, tp, head_dim=64, rope_base=1e4)
+    a = k.to(dev)
+    rc.rope_correct_k_inplace(a, dp.to(dev), tp.to(dev), head_dim=64, rope_base=1e4)
+    b = k.to(dev)
+    rc.rope_correct_k_inplace(b, dp.to(dev), tp.to(dev), head_dim=64, rope_base=1e4,
+                              distinct_donors=True)
+    assert_bit_exact(b, a.cpu())
+    assert_rope_close(b, want)
+    # 3-D input
+    c = k[0].to(dev)
+    rc.rope_correct_k_inplace(c, dp.to(dev), tp.to(dev), head_dim=64, rope_base=1e4,
+                              distinct_donors=True)
+    assert_bit_exact(c, b[0].cpu())
+
+
+def test_rope_correct_k_distinct_full_size_7b(dev):
+    """The 7B RoPE workload in its one-launch form equals the indexed form bit for bit."""
+    k = randn((28, 4, 8192, 128), torch.bfloat16, 56)
+    deltas = torch.randint(-2048, 2049, (32,), generator=gen(57))
+    d = torch.arange(8192)
+    t = d + deltas[d // 256]
+    dd, td = d.to(torch.int32).to(dev), t.to(torch.int32).to(dev)
+    a = k.to(dev)
+    rc.rope_correct_k_inplace(a, dd, td, head_dim=128, rope_base=1e6)
+    b = k.to(dev)
+    rc.rope_correct_k_inplace(b, dd, td, head_dim=128, rope_base=1e6, distinct_donors=True)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 # ---- apply_rope_delta_inplace (rope_correction.py:699-783) ----
 
 @pytest.mark.parametrize("dtype", DTYPES)
