@@ -58,10 +58,13 @@ def _ulp16(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return torch.pow(2.0, e - mant)
 
 
-def assert_rope_close(got: torch.Tensor, ref: torch.Tensor, composed: bool = False) -> None:
+def assert_rope_close(got: torch.Tensor, ref: torch.Tensor, composed: bool = False) -> dict:
     """RoPE parity bar (see the constants above). ``composed``: rows rotated several times
     with a rounding to the dtype in between; a rounding that falls differently in an
-    intermediate step then carries through, so the bound is one ulp of the pair norm."""
+    intermediate step then carries through, so the bound is one ulp of the pair norm.
+    Returns element counts per clause for 16-bit dtypes: ``exact``, ``within_1ulp`` (1 ulp
+    apart, not equal) and ``norm_only`` (more than 1 ulp apart, within 2^-21 of the pair
+    norm), plus ``total``."""
     got = got.cpu()
     ref = ref.cpu()
     assert got.shape == ref.shape and got.dtype == ref.dtype
@@ -70,11 +73,17 @@ def assert_rope_close(got: torch.Tensor, ref: torch.Tensor, composed: bool = Fal
     if got.dtype == torch.float32:
         allowed = ROPE_F32_RTOL * torch.maximum(ref.abs(), 0.1 * norm)
         bad = diff > allowed
+        stats = {"total": bad.numel()}
     else:
-        ok = (ulp_distance(got, ref) <= ROPE_16_ULPS) | (diff <= ROPE_16_NORM_TOL * norm)
+        ulps = ulp_distance(got, ref)
+        by_norm = diff <= ROPE_16_NORM_TOL * norm
+        ok = (ulps <= ROPE_16_ULPS) | by_norm
         if composed:
             ok |= diff <= _ulp16(norm, got.dtype)
         bad = ~ok
+        stats = {"total": bad.numel(), "exact": int((ulps == 0).sum()),
+                 "within_1ulp": int(((ulps > 0) & (ulps <= ROPE_16_ULPS)).sum()),
+                 "norm_only": int(((ulps > ROPE_16_ULPS) & by_norm).sum())}
     n_bad = int(bad.sum())
     if n_bad:
         i = bad.nonzero()[0].tolist()
@@ -82,6 +91,7 @@ def assert_rope_close(got: torch.Tensor, ref: torch.Tensor, composed: bool = Fal
             f"{n_bad} of {bad.numel()} elements outside the RoPE bar; first at {i}: "
             f"got {float(got[tuple(i)])}, want {float(ref[tuple(i)])}, "
             f"pair norm {float(norm[tuple(i)])}")
+    return stats
 
 
 def assert_bit_exact(got: torch.Tensor, ref: torch.Tensor) -> None:

@@ -199,6 +199,36 @@ def test_rope_correct_k_distinct_full_size_7b(dev):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+def test_rope_bar_clause_statistics(dev, capsys):
+    """How the bf16 outputs of the fused RoPE scatter meet the bar on one full Qwen2.5-7B
+    layer (13926 pairs, 4 heads, deltas up to 2048, theta 1e6): most are bit-identical to the
+    oracle, the rest one ulp apart; the pair-norm clause, which covers results that cancel far
+    below their pair's norm, is needed by a vanishing fraction."""
+    import bench
+
+    g = torch.Generator("cpu").manual_seed(0)
+    torch.randint(-2048, 2049, (32,), generator=g)
+    pos_r = bench.recompute_positions(g)
+    perm = torch.randperm(64, generator=g)
+    t = torch.arange(16384)
+    dpos = perm[t // 256] * 256 + t % 256
+    keep = torch.ones(16384, dtype=torch.bool)
+    keep[pos_r.long()] = False
+    dp, tp = dpos[keep].to(torch.int32), t[keep].to(torch.int32)
+    bt = torch.randperm(2048, generator=g)[:1024].to(torch.int32)
+    kv = torch.zeros((2048, 2, 4, 16, 128), dtype=torch.bfloat16)
+    donor = randn((2, 4, 16384, 128), torch.bfloat16, 70)
+    got = rc.rope_correct_scatter_paged(kv.to(dev), donor.to(dev), bt.to(dev), dp.to(dev),
+                                        tp.to(dev), rope_base=1e6).cpu()
+    want = ref.rope_correct_scatter_paged(kv.clone(), donor, bt, dp, tp, rope_base=1e6)
+    slots = bt.long()
+    stats = assert_rope_close(got[slots, 0], want[slots, 0])
+    with capsys.disabled():
+        print(f"\n[rope bar] 7B layer, bf16 K: {stats}")
+    assert stats["exact"] + stats["within_1ulp"] + stats["norm_only"] == stats["total"]
+    assert stats["norm_only"] <= 1e-4 * stats["total"]
+
+
 # ---- apply_rope_delta_inplace (rope_correction.py:699-783) ----
 
 @pytest.mark.parametrize("dtype", DTYPES)
