@@ -622,9 +622,10 @@ QWEN7B_HIDDEN = 3584
 def projection_section(dev: torch.device, inp, steps: int) -> dict:
     """Compacted QKV projection of the attention workload's recompute rows (Qwen2.5-7B:
     hidden 3584 -> 28 q + 2 x 4 KV heads x 128 = 4608 features, QKV bias), RoPE theta 1e6 at
-    the new positions, K/V written into the paged cache: ``qkv_projection_paged`` (one MFMA
-    kernel) timed as graph replays and per launch. For comparison, torch on the same rows:
-    gather + addmm (hipBLASLt), without RoPE and without the K/V write."""
+    the new positions, K/V written into the paged cache: ``qkv_projection_paged`` with the
+    fused MFMA kernel (graph replays and per launch) and with the library GEMM plus the
+    epilogue kernel (graph replays). For comparison, torch on the same rows: gather + addmm
+    (hipBLASLt), without RoPE and without the K/V write."""
     from semblend_amd import _lib
     from semblend_amd import triton_kernels as tk
 
@@ -641,7 +642,11 @@ def projection_section(dev: torch.device, inp, steps: int) -> dict:
 
     def fused():
         tk.qkv_projection_paged(x, w, pos, inp["attn_kv"], inp["block_table"], HQ, HKV, D,
-                                qkv_bias=b, rope_base=ROPE_BASE, out=q)
+                                qkv_bias=b, rope_base=ROPE_BASE, out=q, backend="fused")
+
+    def library_epilogue():
+        tk.qkv_projection_paged(x, w, pos, inp["attn_kv"], inp["block_table"], HQ, HKV, D,
+                                qkv_bias=b, rope_base=ROPE_BASE, out=q, backend="library")
 
     pos_l = pos.long()
 
@@ -673,6 +678,7 @@ def projection_section(dev: torch.device, inp, steps: int) -> dict:
     total, n = _lib.kernel_time("qkv_mfma")
     kern_us = 1e3 * total / n
     ms_lib = timed(library, False)
+    ms_lib_epi = timed(library_epilogue, True)
     wo = (torch.randn((hidden, HQ * D), generator=gd, device=dev) * (HQ * D) ** -0.5).to(
         torch.bfloat16)
 
@@ -687,6 +693,10 @@ def projection_section(dev: torch.device, inp, steps: int) -> dict:
         "kernel": {"avg_us": round(kern_us, 2),
                    "tflops": round(flops / (kern_us * 1e-6) / 1e12, 1),
                    "frac_of_peak": round(flops / (kern_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)},
+        "library_with_epilogue": {
+            "ms": round(ms_lib_epi, 4), "tflops": round(flops / (ms_lib_epi * 1e-3) / 1e12, 1),
+            "what": "qkv_projection_paged(backend='library'): row gather + hipBLASLt GEMM "
+                    "(fp32 out) + the epilogue kernel (bias, RoPE, Q and paged K/V write)"},
         "torch_gather_addmm": {"ms": round(ms_lib, 4),
                                "tflops": round(flops / (ms_lib * 1e-3) / 1e12, 1),
                                "what": "x[pos] @ W^T + b via torch (hipBLASLt), no RoPE, no K/V write"},
@@ -933,7 +943,8 @@ def main() -> int:
     log("compacted QKV projection with the K/V write")
     result["projection"] = projection_section(dev, inp, args.steps)
     pj = result["projection"]
-    log(f"projection: fused {pj['fused']['ms']:.4f} ms ({pj['fused']['tflops']} TFLOP/s), kernel "
+    log(f"projection: library+epilogue {pj['library_with_epilogue']['ms']:.4f} ms; "
+        f"fused {pj['fused']['ms']:.4f} ms ({pj['fused']['tflops']} TFLOP/s), kernel "
         f"{pj['kernel']['avg_us']} us ({pj['kernel']['tflops']} TFLOP/s), torch gather+addmm "
         f"{pj['torch_gather_addmm']['ms']:.4f} ms ({pj['torch_gather_addmm']['tflops']} TFLOP/s); "
         f"whole layer {pj['layer']['ms']:.3f} ms")

@@ -123,6 +123,29 @@ int sb_qkv_projection_paged(void* q_out, const void* hidden, const void* weight,
                             int64_t hidden_stride, int64_t weight_stride, int64_t q_stride,
                             const int64_t* kv_strides, int32_t dtype, void* stream);
 
+/* Library-GEMM form of sb_qkv_projection_paged, in three steps around a GEMM the caller
+ * runs (hipBLASLt): sb_qkv_gather_rows copies hidden row positions[n] to xg[n] ([num_rows,
+ * hidden_dim] contiguous; rows without a valid position are zero) and, with inv_freq,
+ * fills rope_table (num_rows * head_dim * 4 bytes, as the workspace of
+ * sb_qkv_projection_paged) in the same launch; the caller computes proj = xg . W^T in fp32;
+ * sb_qkv_epilogue_paged adds the bias, rotates Q and K by the row's position from
+ * rope_table (NULL: no RoPE), rounds once to dtype and writes Q to q_out (compact) and K / V
+ * into the paged cache: the same results as the fused kernel on the same products. Rows
+ * whose position is outside [0, seq_len) get a zero Q row and no K / V write.
+ * Fuse the K/V write of semblend_core/triton_kernels.py:904-909 and the RoPE at the new
+ * positions into the GEMM's epilogue; no reference counterpart. */
+int sb_qkv_gather_rows(void* xg, const void* hidden, const int32_t* positions,
+                       int64_t num_rows, int64_t seq_len, int64_t hidden_dim,
+                       int64_t hidden_stride, const float* inv_freq, int64_t head_dim,
+                       void* rope_table, int32_t dtype, void* stream);
+int sb_qkv_epilogue_paged(void* q_out, const float* proj, const void* bias,
+                          const int32_t* positions, int64_t num_rows, int64_t seq_len,
+                          int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                          const void* rope_table, void* kv_cache, const int32_t* block_table,
+                          int64_t block_size, int64_t num_blocks_total,
+                          int64_t num_blocks_per_seq, int64_t proj_stride, int64_t q_stride,
+                          const int64_t* kv_strides, int32_t dtype, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * RoPE delta correction (interleaved pairs (2i, 2i+1); inv_freq is a device fp32 array of
  * head_dim/2 entries, 1 / base^(2i/head_dim))

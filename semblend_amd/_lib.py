@@ -72,6 +72,9 @@ SIGNATURES: dict[str, list] = {
     "sb_qkv_projection_paged": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _i64p, _i32, _vp],
+    "sb_qkv_gather_rows": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp],
+    "sb_qkv_epilogue_paged": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp,
+                              _vp, _i64, _i64, _i64, _i64, _i64, _i64p, _i32, _vp],
     "sb_kernel_timing_enable": [_i32],
     "sb_kernel_timing_read": [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), _i64p],
 }

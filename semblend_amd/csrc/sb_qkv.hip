@@ -393,6 +393,111 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
   }
 }
 
+// Row gather for a library GEMM, plus the RoPE table in the same launch: threads
+// [0, R * hidden / 8) copy 16-byte chunks of hidden row positions[n] to xg[n] (rows without
+// a valid position are zero); the next R * D / 4 threads fill table entries as
+// qkv_rope_table_kernel does.
+__global__ __launch_bounds__(256) void qkv_gather_kernel(char* xg, const char* hidden,
+                                                         int64_t h_s_row, int64_t hidden_dim,
+                                                         const int32_t* positions,
+                                                         int64_t num_rows, int64_t seq_len,
+                                                         const float* inv_freq, int half_d,
+                                                         float4* table) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t cpr = hidden_dim / 8;  // 16-byte chunks of a bf16 / fp16 row
+  const int64_t n_copy = num_rows * cpr;
+  if (idx < n_copy) {
+    const int64_t n = idx / cpr;
+    const int64_t c = idx - n * cpr;
+    const int p = positions[n];
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (p >= 0 && p < seq_len) v = *reinterpret_cast<const uint4*>(hidden + p * h_s_row + 16 * c);
+    *reinterpret_cast<uint4*>(xg + n * hidden_dim * 2 + 16 * c) = v;
+    return;
+  }
+  if (!table) return;
+  const int64_t t = idx - n_copy;
+  const int quads = half_d / 2;
+  if (t >= num_rows * quads) return;
+  const int64_t n = t / quads;
+  const int k = static_cast<int>(t - n * quads);
+  const int p = positions[n];
+  float4 v = make_float4(1.f, 0.f, 1.f, 0.f);
+  if (p >= 0 && p < seq_len) {
+    sincos_rn(static_cast<float>(p) * inv_freq[2 * k], &v.y, &v.x);
+    sincos_rn(static_cast<float>(p) * inv_freq[2 * k + 1], &v.w, &v.z);
+  }
+  table[t] = v;
+}
+
+// Epilogue of a projection computed elsewhere (a library GEMM with fp32 output): for row n
+// and the 8 features [f0, f0 + 8) of one thread, out = proj[n, f] + bias[f], Q and K rotated
+// by the row's position from the same (cos, sin) table as the fused kernel, one rounding to
+// the input dtype, then Q to q_out[n] and K / V to the paged slot of positions[n] (rows
+// without a valid position: Q zero, no K / V write). Same results as the fused kernel's
+// epilogue on the same fp32 products.
+template <int DT>
+__global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a, const float* proj,
+                                                           int64_t p_s_row) {
+  const int64_t cpr = a.num_features / 8;  // 8-feature chunks per row
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= a.num_rows * cpr) return;
+  const int64_t n = idx / cpr;
+  const int64_t f0 = (idx - n * cpr) * 8;
+  const int p = a.positions[n];
+  const bool valid = p >= 0 && p < a.seq_len;
+  const int64_t kf0 = a.q_features, vf0 = a.q_features + a.kv_features;
+  int64_t slot = -1;
+  if (f0 >= kf0) {
+    if (!valid) return;
+    const int64_t lb = p / a.block_size;
+    if (lb >= a.nb_per_seq) return;
+    const int64_t pb = a.block_table[lb];
+    if (pb < 0 || pb >= a.nb_total) return;
+    slot = pb * a.s_blk + (p - lb * a.block_size) * a.s_pos;
+  }
+  uint4 w = make_uint4(0u, 0u, 0u, 0u);
+  if (valid) {
+    const float4* src = reinterpret_cast<const float4*>(proj + n * p_s_row + f0);
+    const float4 x0 = src[0], x1 = src[1];
+    float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    if (a.bias) {
+      const uint16_t* b = reinterpret_cast<const uint16_t*>(a.bias) + f0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] += qkv_elem<DT>(b[e]);
+    }
+    if (a.rope_cs && f0 < vf0) {
+      const int64_t rf = f0 - (f0 < kf0 ? 0 : kf0);
+      const int64_t d0 = rf % a.head_dim;  // multiple of 8: two table entries
+      const int quads = a.head_dim / 4;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4 c = a.rope_cs[n * quads + d0 / 4 + h];
+        float ev = v[4 * h], od = v[4 * h + 1];
+        v[4 * h] = ev * c.x - od * c.y;
+        v[4 * h + 1] = ev * c.y + od * c.x;
+        ev = v[4 * h + 2];
+        od = v[4 * h + 3];
+        v[4 * h + 2] = ev * c.z - od * c.w;
+        v[4 * h + 3] = ev * c.w + od * c.z;
+      }
+    }
+    w.x = qkv_pack2<DT>(v[0], v[1]);
+    w.y = qkv_pack2<DT>(v[2], v[3]);
+    w.z = qkv_pack2<DT>(v[4], v[5]);
+    w.w = qkv_pack2<DT>(v[6], v[7]);
+  }
+  if (f0 < kf0) {
+    *reinterpret_cast<uint4*>(a.out + n * a.o_s_row + 2 * f0) = w;
+  } else {
+    const bool is_v = f0 >= vf0;
+    const int64_t rf = f0 - (is_v ? vf0 : kf0);
+    const int64_t h = rf / a.head_dim;
+    *reinterpret_cast<uint4*>(a.kv + slot + (is_v ? a.s_kv : 0) + h * a.s_head +
+                              2 * (rf - h * a.head_dim)) = w;
+  }
+}
+
 // Checks shared by both entries; fills the operand part of QkvArgs.
 int qkv_common(const char* fn, QkvArgs* a, const void* hidden, const void* weight,
                const void* bias, int64_t seq_len, int64_t hidden_dim, int64_t num_features,
@@ -532,6 +637,95 @@ extern "C" int sb_qkv_projection_paged(
   a.nb_total = num_blocks_total;
   a.nb_per_seq = num_blocks_per_seq;
   return launch_qkv<QKV_SPLIT>(fn, a, dtype, st);
+}
+
+extern "C" int sb_qkv_gather_rows(void* xg, const void* hidden, const int32_t* positions,
+                                  int64_t num_rows, int64_t seq_len, int64_t hidden_dim,
+                                  int64_t hidden_stride, const float* inv_freq,
+                                  int64_t head_dim, void* rope_table, int32_t dtype,
+                                  void* stream) {
+  const char* fn = "sb_qkv_gather_rows";
+  clear_error();
+  if (num_rows == 0) return SB_OK;
+  if (dtype != SB_DTYPE_BF16 && dtype != SB_DTYPE_F16) return fail(fn, "dtype must be bf16 or fp16");
+  if (!xg || !hidden || !positions) return fail(fn, "null pointer argument");
+  if (num_rows < 0 || hidden_dim <= 0 || hidden_dim % 8 != 0)
+    return fail(fn, "hidden size must be a positive multiple of 8");
+  if (reinterpret_cast<uintptr_t>(xg) % 16 || reinterpret_cast<uintptr_t>(hidden) % 16 ||
+      (hidden_stride * 2) % 16)
+    return fail(fn, "rows must be 16-byte aligned");
+  if (inv_freq && (!rope_table || reinterpret_cast<uintptr_t>(rope_table) % 16 ||
+                   head_dim <= 0 || head_dim % 4 != 0))
+    return fail(fn, "RoPE needs a 16-byte aligned table and head_dim a multiple of 4");
+  const int64_t threads = num_rows * (hidden_dim / 8) + (inv_freq ? num_rows * (head_dim / 4) : 0);
+  if ((threads + 255) / 256 > 0x7fffffff) return fail(fn, "grid too large");
+  SB_LAUNCH("qkv_gather", qkv_gather_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)),
+            dim3(256), static_cast<hipStream_t>(stream), static_cast<char*>(xg),
+            static_cast<const char*>(hidden), hidden_stride * 2, hidden_dim, positions, num_rows,
+            seq_len, inv_freq, static_cast<int>(head_dim / 2),
+            inv_freq ? static_cast<float4*>(rope_table) : nullptr);
+  return check_launch(fn);
+}
+
+extern "C" int sb_qkv_epilogue_paged(
+    void* q_out, const float* proj, const void* bias, const int32_t* positions,
+    int64_t num_rows, int64_t seq_len, int64_t num_q_heads, int64_t num_kv_heads,
+    int64_t head_dim, const void* rope_table, void* kv_cache, const int32_t* block_table,
+    int64_t block_size, int64_t num_blocks_total, int64_t num_blocks_per_seq,
+    int64_t proj_stride, int64_t q_stride, const int64_t* kv_strides, int32_t dtype,
+    void* stream) {
+  const char* fn = "sb_qkv_epilogue_paged";
+  clear_error();
+  if (num_rows == 0) return SB_OK;
+  if (dtype != SB_DTYPE_BF16 && dtype != SB_DTYPE_F16) return fail(fn, "dtype must be bf16 or fp16");
+  if (num_rows < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0)
+    return fail(fn, "invalid sizes");
+  if (head_dim % 8 != 0) return fail(fn, "head_dim must be a multiple of 8");
+  if (!q_out || !proj || !positions || !kv_cache || !block_table || !kv_strides)
+    return fail(fn, "null pointer argument");
+  if (block_size <= 0) return fail(fn, "block_size must be positive");
+  if (kv_strides[4] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
+  const int64_t qf = num_q_heads * head_dim, kvf = num_kv_heads * head_dim;
+  if (proj_stride < qf + 2 * kvf) return fail(fn, "projection rows shorter than the features");
+  if (reinterpret_cast<uintptr_t>(proj) % 16 || (proj_stride * 4) % 16 ||
+      reinterpret_cast<uintptr_t>(q_out) % 16 || (q_stride * 2) % 16 ||
+      reinterpret_cast<uintptr_t>(kv_cache) % 16 || (kv_strides[0] * 2) % 16 ||
+      (kv_strides[1] * 2) % 16 || (kv_strides[2] * 2) % 16 || (kv_strides[3] * 2) % 16 ||
+      reinterpret_cast<uintptr_t>(rope_table) % 16)
+    return fail(fn, "projection, q_out, cache rows and table must be 16-byte aligned");
+  if (bias && reinterpret_cast<uintptr_t>(bias) % 2) return fail(fn, "misaligned bias");
+  QkvArgs a{};
+  a.bias = static_cast<const char*>(bias);
+  a.positions = positions;
+  a.num_rows = num_rows;
+  a.seq_len = seq_len;
+  a.num_features = qf + 2 * kvf;
+  a.q_features = qf;
+  a.kv_features = kvf;
+  a.head_dim = static_cast<int>(head_dim);
+  a.rope_cs = static_cast<const float4*>(rope_table);
+  a.out = static_cast<char*>(q_out);
+  a.o_s_row = q_stride * 2;
+  a.kv = static_cast<char*>(kv_cache);
+  a.s_blk = kv_strides[0] * 2;
+  a.s_kv = kv_strides[1] * 2;
+  a.s_head = kv_strides[2] * 2;
+  a.s_pos = kv_strides[3] * 2;
+  a.block_table = block_table;
+  a.block_size = block_size;
+  a.nb_total = num_blocks_total;
+  a.nb_per_seq = num_blocks_per_seq;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t threads = num_rows * (a.num_features / 8);
+  if ((threads + 255) / 256 > 0x7fffffff) return fail(fn, "grid too large");
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  if (dtype == SB_DTYPE_BF16)
+    SB_LAUNCH("qkv_epilogue", qkv_epilogue_kernel<SB_DTYPE_BF16>, grid, dim3(256), st, a, proj,
+              proj_stride);
+  else
+    SB_LAUNCH("qkv_epilogue", qkv_epilogue_kernel<SB_DTYPE_F16>, grid, dim3(256), st, a, proj,
+              proj_stride);
+  return check_launch(fn);
 }
 
 extern "C" int64_t sb_masked_qkv_projection_workspace_size(int64_t seq_len) {

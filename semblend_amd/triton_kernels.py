@@ -250,6 +250,10 @@ def masked_qkv_projection(
     return (projected * mask.unsqueeze(1).float()).to(dt)
 
 
+# Row count from which qkv_projection_paged's "auto" backend takes the library GEMM.
+_LIBRARY_PROJECTION_ROWS = 512
+
+
 def qkv_projection_paged(
     hidden_states: torch.Tensor,
     qkv_weight: torch.Tensor,
@@ -262,6 +266,7 @@ def qkv_projection_paged(
     qkv_bias: torch.Tensor | None = None,
     rope_base: float | None = None,
     out: torch.Tensor | None = None,
+    backend: str = "auto",
 ) -> torch.Tensor:
     """Project only the rows at ``positions`` and write their new K/V into the paged cache.
 
@@ -272,6 +277,12 @@ def qkv_projection_paged(
     path before the single rounding. K/V slots out of the table are skipped; a position
     outside the hidden states gives a zero Q row. bf16 / fp16, hidden a multiple of 64,
     head_dim a multiple of 8.
+    ``backend``: "fused" runs one MFMA kernel that gathers the rows, multiplies and writes
+    Q and K/V from its epilogue; "library" gathers the rows, multiplies them with the
+    library GEMM (hipBLASLt through torch, fp32 output) and runs the same epilogue as a
+    kernel of its own (bias, RoPE, one rounding, Q and the paged K/V write); "auto" takes
+    the library form from 512 rows up, where it is the faster of the two on MI355X. Both
+    accumulate in fp32 and round once.
     Fuses the masked projection (semblend_core/triton_kernels.py:451-522) with the K/V write
     of partial_prefill (:904-909), compacted and paged; no reference counterpart.
     """
@@ -309,6 +320,26 @@ def qkv_projection_paged(
     ws_bytes = _lib.size_query("sb_qkv_projection_paged_workspace_size", n, head_dim,
                                int(inv is not None))
     ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=dev)
+    if backend not in ("auto", "fused", "library"):
+        raise ValueError("backend must be 'auto', 'fused' or 'library'")
+    if backend == "library" or (backend == "auto" and n >= _LIBRARY_PROJECTION_ROWS):
+        # rows outside the hidden states are gathered as zeros; the epilogue zeroes their Q
+        # and writes no K/V for them
+        xg = torch.empty((n, hidden), dtype=dt, device=dev)
+        dt_code = _lib.dtype_code(hidden_states)
+        with torch.cuda.device(dev):
+            _lib.call("sb_qkv_gather_rows", xg.data_ptr(), hidden_states.data_ptr(),
+                      pos.data_ptr(), n, seq_len, hidden, hidden_states.stride(0),
+                      _lib.ptr(inv), head_dim, ws.data_ptr(), dt_code, _lib.stream_handle(dev))
+            proj = torch.mm(xg, qkv_weight.t(), out_dtype=torch.float32)
+            _lib.call(
+                "sb_qkv_epilogue_paged",
+                out.data_ptr(), proj.data_ptr(), _lib.ptr(bias), pos.data_ptr(), n, seq_len,
+                num_heads, num_kv_heads, head_dim, ws.data_ptr() if inv is not None else None,
+                kv_cache.data_ptr(), bt.data_ptr(), bs, nb, bt.shape[0], proj.stride(0),
+                num_heads * head_dim, _lib.strides(kv_cache), dt_code, _lib.stream_handle(dev),
+            )
+        return out
     with torch.cuda.device(dev):
         _lib.call(
             "sb_qkv_projection_paged",

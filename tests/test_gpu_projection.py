@@ -61,11 +61,11 @@ def _case(seq, hidden, hq, hkv, d, n_rows, dtype, seed, nb_extra=5, bs=16, bias=
     return x, w, b, pos, bt, cache
 
 
-def _check_paged(dev, x, w, b, pos, bt, cache, hq, hkv, d, rope_base):
+def _check_paged(dev, x, w, b, pos, bt, cache, hq, hkv, d, rope_base, backend="auto"):
     kv_dev = cache.to(dev)
     q = tk.qkv_projection_paged(x.to(dev), w.to(dev), pos.to(dev), kv_dev, bt.to(dev), hq, hkv,
                                 d, qkv_bias=None if b is None else b.to(dev),
-                                rope_base=rope_base)
+                                rope_base=rope_base, backend=backend)
     want_kv = cache.clone()
     want_q = ref.qkv_project_paged(x, w, pos, want_kv, bt, hq, hkv, d, qkv_bias=b,
                                    rope_base=rope_base)
@@ -96,16 +96,21 @@ def _check_paged(dev, x, w, b, pos, bt, cache, hq, hkv, d, rope_base):
                        cache.permute(0, 3, 1, 2, 4)[keep].view(torch.int16))
 
 
+BACKENDS = ["fused", "library"]
+
+
+@pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("rope_base", [None, 1e6], ids=["plain", "rope"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_projection_paged_qwen05b_shape(dev, dtype, rope_base):
+def test_projection_paged_qwen05b_shape(dev, dtype, rope_base, backend):
     # Qwen2.5-0.5B attention: hidden 896, 14 q heads / 2 KV heads x 64, QKV bias
     x, w, b, pos, bt, cache = _case(300, 896, 14, 2, 64, 77, dtype, 10)
     pos = torch.cat([pos, torch.tensor([-1, 300], dtype=torch.int32)])  # zero Q, no K/V
-    _check_paged(dev, x, w, b, pos, bt, cache, 14, 2, 64, rope_base)
+    _check_paged(dev, x, w, b, pos, bt, cache, 14, 2, 64, rope_base, backend)
 
 
-def test_projection_paged_qwen7b_full(dev):
+@pytest.mark.parametrize("backend", BACKENDS)
+def test_projection_paged_qwen7b_full(dev, backend):
     """Qwen2.5-7B attention at the benchmark's size: hidden 3584, 28 / 4 heads x 128, bias,
     2458 computed rows of a 16384-token sequence, RoPE theta 1e6, paged cache of 2048 blocks."""
     import bench
@@ -117,16 +122,17 @@ def test_projection_paged_qwen7b_full(dev):
     x = randn((seq, hidden), torch.bfloat16, 22)
     bt = torch.randperm(2048, generator=g)[:1024].to(torch.int32)
     cache = randn((2048, 2, 4, 16, 128), torch.bfloat16, 23)
-    _check_paged(dev, x, w, b, pos, bt, cache, 28, 4, 128, 1e6)
+    _check_paged(dev, x, w, b, pos, bt, cache, 28, 4, 128, 1e6, backend)
 
 
+@pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("n_rows", [700, 2100])
-def test_projection_paged_llama_shape(dev, n_rows):
+def test_projection_paged_llama_shape(dev, n_rows, backend):
     # Llama-3-8B attention: hidden 4096, 32 / 8 heads x 128, no bias, theta 5e5 (700 rows
     # take 256 x 128 tiles, 2100 rows 256 x 256; the 7B test above takes 256 x 192)
     x, w, b, pos, bt, cache = _case(4096, 4096, 32, 8, 128, n_rows, torch.bfloat16, 30,
                                     bias=False)
-    _check_paged(dev, x, w, b, pos, bt, cache, 32, 8, 128, 5e5)
+    _check_paged(dev, x, w, b, pos, bt, cache, 32, 8, 128, 5e5, backend)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
