@@ -77,6 +77,18 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// Two floats to a bf16 pair (low half = lo) with v_cvt_pk_bf16_f32: round to nearest even
+// in one instruction where the integer form above takes about five per value. The hardware
+// writes a quiet NaN of its own; it is replaced by 0x7FC0, so the bits equal f32_to_bf16's.
+__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  uint32_t w = __builtin_bit_cast(uint32_t, v);
+  if (lo != lo) w = (w & 0xffff0000u) | 0x7fc0u;
+  if (hi != hi) w = (w & 0x0000ffffu) | 0x7fc00000u;
+  return w;
+}
+
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   _Float16 x = __builtin_bit_cast(_Float16, h);
   return static_cast<float>(x);

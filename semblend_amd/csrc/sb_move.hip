@@ -176,17 +176,19 @@ __device__ __forceinline__ void unpack_words(const uint32_t* w, float* f) {
 
 template <int DT, int W>
 __device__ __forceinline__ void pack_words(const float* f, uint32_t* w) {
+  if (DT == SB_DTYPE_BF16) {
+#pragma unroll
+    for (int k = 0; k < W; ++k) w[k] = pack2_bf16(f[2 * k], f[2 * k + 1]);
+    return;
+  }
   if (DT == SB_DTYPE_F32) {
 #pragma unroll
     for (int k = 0; k < W; ++k) w[k] = __float_as_uint(f[k]);
   } else {
 #pragma unroll
-    for (int k = 0; k < W; ++k) {
-      const uint32_t lo = DT == SB_DTYPE_BF16 ? f32_to_bf16(f[2 * k]) : f32_to_f16(f[2 * k]);
-      const uint32_t hi =
-          DT == SB_DTYPE_BF16 ? f32_to_bf16(f[2 * k + 1]) : f32_to_f16(f[2 * k + 1]);
-      w[k] = lo | (hi << 16);
-    }
+    for (int k = 0; k < W; ++k)
+      w[k] = static_cast<uint32_t>(f32_to_f16(f[2 * k])) |
+             (static_cast<uint32_t>(f32_to_f16(f[2 * k + 1])) << 16);
   }
 }
 

@@ -141,18 +141,10 @@ template <int DT>
 __device__ __forceinline__ float qkv_elem(uint16_t h) {
   return DT == SB_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
 }
-// Two floats rounded to the input dtype (round to nearest even, one instruction per pair);
-// a bf16 NaN becomes 0x7FC0 as in torch, so the bits equal f32_to_bf16's.
+// Two floats rounded to the input dtype (round to nearest even, one instruction per pair).
 template <int DT>
 __device__ __forceinline__ uint32_t qkv_pack2(float lo, float hi) {
-  if (DT == SB_DTYPE_BF16) {
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
-    uint32_t w = __builtin_bit_cast(uint32_t, v);
-    if (lo != lo) w = (w & 0xffff0000u) | 0x7fc0u;
-    if (hi != hi) w = (w & 0x0000ffffu) | 0x7fc00000u;
-    return w;
-  }
+  if (DT == SB_DTYPE_BF16) return pack2_bf16(lo, hi);
   return static_cast<uint32_t>(f32_to_f16(lo)) | (static_cast<uint32_t>(f32_to_f16(hi)) << 16);
 }
 
