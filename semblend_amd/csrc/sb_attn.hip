@@ -55,14 +55,9 @@ constexpr int kWaveRows = 32;   // flattened query rows per MFMA row group
 #ifndef SB_ATTN_PV_PRIO
 #define SB_ATTN_PV_PRIO 2
 #endif
-// VALU instructions scheduled after each QK MFMA (and its fragment read) in the block that
-// forms P(it) under S(it+1) (3, 4, 6 and 8 measured within noise of 5).
-#ifndef SB_ATTN_IL_VALU
-#define SB_ATTN_IL_VALU 5
-#endif
-#ifndef SB_ATTN_QK_PRIO
-#define SB_ATTN_QK_PRIO 0
-#endif
+// LDS fragment reads issued ahead of the MFMA that consumes them (fragment rings are 4
+// deep, so at most 3).
+constexpr int kFragAhead = 3;
 #ifndef SB_ATTN_ROW_GROUPS
 #define SB_ATTN_ROW_GROUPS 1
 #endif
@@ -232,6 +227,16 @@ template <> struct Mma<SB_DTYPE_BF16> {
     return r;
   }
   __device__ __forceinline__ static uint16_t cvt1(float f) { return f32_to_bf16(f); }
+  // Two values rounded to a packed pair (one v_cvt_pk_bf16_f32), and acc + their sum.
+  typedef __bf16 x2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static x2 cvt2(float a, float b) {
+    const x2 r = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+    return r;
+  }
+  __device__ __forceinline__ static float sum2(x2 v, float acc) {
+    const x2 one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+    return __builtin_amdgcn_fdot2_f32_bf16(v, one, acc, false);
+  }
   // acc + sum of the 8 (rounded) elements of v, two per v_dot2.
   __device__ __forceinline__ static float sum8(vec8 v, float acc) {
     typedef __bf16 x2 __attribute__((ext_vector_type(2)));
@@ -260,6 +265,15 @@ template <> struct Mma<SB_DTYPE_F16> {
     return r;
   }
   __device__ __forceinline__ static uint16_t cvt1(float f) { return f32_to_f16(f); }
+  typedef _Float16 x2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static x2 cvt2(float a, float b) {
+    const x2 r = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+    return r;
+  }
+  __device__ __forceinline__ static float sum2(x2 v, float acc) {
+    const x2 one = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
+    return __builtin_amdgcn_fdot2(v, one, acc, false);
+  }
   __device__ __forceinline__ static float sum8(vec8 v, float acc) {
     typedef _Float16 x2 __attribute__((ext_vector_type(2)));
     const x2 one = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
@@ -393,13 +407,16 @@ attn_mfma_kernel(const AttnBatch batch) {
     }
     pmax_l = max(pmax_l, p[g]);
   }
-  const int pmax_w = wave_max_i(pmax_l);
+  // Wave-uniform values are moved to scalar registers (readfirstlane) so that the compiler
+  // sees them as uniform: branches on them stay scalar branches instead of being turned into
+  // per-lane selects (the mask below would otherwise run on every tile).
+  const int pmax_w = __builtin_amdgcn_readfirstlane(wave_max_i(pmax_l));
   if (lane == 0) red_max[wave] = pmax_w;
   __syncthreads();
-  int kend = red_max[0];
+  int kend_l = red_max[0];
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) kend = max(kend, red_max[w]);
-  kend += 1;
+  for (int w = 1; w < kWaves; ++w) kend_l = max(kend_l, red_max[w]);
+  const int kend = __builtin_amdgcn_readfirstlane(kend_l) + 1;
   const int k0 = item.chunk * a.ksplit;
   if (k0 >= kend) return;  // uniform: kend comes from shared memory
   const int k1 = min(k0 + a.ksplit, kend);
@@ -411,7 +428,7 @@ attn_mfma_kernel(const AttnBatch batch) {
     plim[g] = min(p[g], k1 - 1);
     if (p[g] >= 0) pmin_l = min(pmin_l, plim[g]);
   }
-  const int pmin_w = wave_min_i(pmin_l);
+  const int pmin_w = __builtin_amdgcn_readfirstlane(wave_min_i(pmin_l));
   const int pmax_c = min(pmax_w, k1 - 1);
 
   // Q fragments (B operand), pre-multiplied by scale * log2(e) and rounded to the input
@@ -628,32 +645,68 @@ attn_mfma_kernel(const AttnBatch batch) {
       fill_offsets(slot, t0 + 3 * kTileKeys, wave * (kTileKeys / kWaves) + lane);
     const bool live = t0 <= pmax_c;
     // ---- S(it+1) on the matrix cores while P(it) is formed on the vector ALUs ----
-#if SB_ATTN_QK_PRIO
-    __builtin_amdgcn_s_setprio(SB_ATTN_QK_PRIO);
-#endif
-    if (NEXT) qk((it + 1) & 1, s_nxt);
+    // The block is laid out by hand: step n reads the K fragment of step n + kFragAhead,
+    // issues the MFMAs of step n and forms one share of P(it) (exp2, pair conversion, pair
+    // sum); scheduling barriers keep the steps in this order, so every fragment read has
+    // kFragAhead MFMAs to land and the vector work sits between independent MFMAs.
     bool bad_any = false;
     bool bad[RG];
+    if (NEXT) {
+      constexpr int NQ = kHalves * NKS;                // MFMA steps (each RG MFMAs)
+      constexpr int NPAIR = RG * kHalves * 8;          // P pairs per lane
+      static_assert(NPAIR % NQ == 0, "P pairs split evenly over the MFMA steps");
+      constexpr int PPS = NPAIR / NQ;                  // pairs per step
+      const int ks = (it + 1) & 1;
+      vec8 ring[4];
+#pragma unroll
+      for (int n = 0; n < kFragAhead; ++n) ring[n] = kfrag(ks, n);
+      uint32_t pw[RG][kHalves][2][4];  // P words: [group][half][8-element pack][word]
+      float acc[RG][kHalves][2];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int n = 0; n < NQ; ++n) {
+        if (n + kFragAhead < NQ) ring[(n + kFragAhead) & 3] = kfrag(ks, n + kFragAhead);
+        const int j = n % kHalves;
+#pragma unroll
+        for (int g = 0; g < RG; ++g)
+          s_nxt[g][j] = M::mma(ring[n & 3], qf[g][n / kHalves], n < kHalves ? negm[g] : s_nxt[g][j]);
+#pragma unroll
+        for (int pp = 0; pp < PPS; ++pp) {
+          const int q = n * PPS + pp;
+          const int g = q / (kHalves * 8), r = q % (kHalves * 8);
+          const int hj = r / 8, h = (r / 4) % 2, w = r % 4;
+          const float e0 = __builtin_amdgcn_exp2f(s_cur[g][hj][8 * h + 2 * w]);
+          const float e1 = __builtin_amdgcn_exp2f(s_cur[g][hj][8 * h + 2 * w + 1]);
+          const auto pr = M::cvt2(e0, e1);
+          pw[g][hj][h][w] = __builtin_bit_cast(uint32_t, pr);
+          acc[g][hj][h] = M::sum2(pr, w == 0 ? 0.f : acc[g][hj][h]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int g = 0; g < RG; ++g) {
+        float t = 0.f;
+#pragma unroll
+        for (int hj = 0; hj < kHalves; ++hj)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const u32x4_t wv = {pw[g][hj][h][0], pw[g][hj][h][1], pw[g][hj][h][2],
+                                pw[g][hj][h][3]};
+            pb[g][hj][h] = __builtin_bit_cast(vec8, wv);
+            t += acc[g][hj][h];
+          }
+        tsum[g] = t;
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < RG; ++g) exp_tile(g, s_cur, 0.f);
+    }
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
-      exp_tile(g, s_cur, 0.f);
       const float pair = tsum[g] + xor32(tsum[g]);
       bad[g] = !seeded[g] || !(pair <= M::kPMax);
       bad_any |= bad[g];
     }
-    if (NEXT) {
-      // Interleave: each QK^T MFMA is followed by one LDS fragment read and a share of the
-      // softmax VALU work (exp, conversion, sums), so the vector ALUs run under the MFMAs.
-#pragma unroll
-      for (int n = 0; n < kHalves * NKS; ++n) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-        __builtin_amdgcn_sched_group_barrier(0x002, SB_ATTN_IL_VALU, 0);  // VALU
-      }
-    }
-#if SB_ATTN_QK_PRIO
-    __builtin_amdgcn_s_setprio(0);
-#endif
     if (NEXT) mask(t0 + kTileKeys, s_nxt);
     // ---- rare: seed the reference with the first live tile's max, or move it up when a
     // tile would push P past kPMax; O and l are rescaled by 2^(m_old - m_new) and the
@@ -690,7 +743,7 @@ attn_mfma_kernel(const AttnBatch batch) {
     }
 #pragma unroll
     for (int g = 0; g < RG; ++g) l_run[g] += tsum[g];
-    // ---- O^T += V^T P^T; V fragments stream through a 4-deep ring ----
+    // ---- O^T += V^T P^T; V fragments stream through a 4-deep ring, kFragAhead ahead ----
     if (live) {
 #if SB_ATTN_PV_PRIO
       __builtin_amdgcn_s_setprio(SB_ATTN_PV_PRIO);
@@ -699,14 +752,15 @@ attn_mfma_kernel(const AttnBatch batch) {
       const int vb = it & 1;
       vec8 vring[4];
 #pragma unroll
-      for (int n = 0; n < 4; ++n) vring[n] = vfrag(vb, n);
+      for (int n = 0; n < kFragAhead; ++n) vring[n] = vfrag(vb, n);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int n = 0; n < NV; ++n) {
-        const vec8 va = vring[n & 3];
-        if (n + 4 < NV) vring[n & 3] = vfrag(vb, n + 4);
+        if (n + kFragAhead < NV) vring[(n + kFragAhead) & 3] = vfrag(vb, n + kFragAhead);
         const int t = n % NDT, st = (n / NDT) & 1, j = n / (2 * NDT);
 #pragma unroll
-        for (int g = 0; g < RG; ++g) o[g][t] = M::mma(va, pb[g][j][st], o[g][t]);
+        for (int g = 0; g < RG; ++g) o[g][t] = M::mma(vring[n & 3], pb[g][j][st], o[g][t]);
+        __builtin_amdgcn_sched_barrier(0);
       }
 #if SB_ATTN_PV_PRIO
       __builtin_amdgcn_s_setprio(0);
