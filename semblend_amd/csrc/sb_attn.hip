@@ -353,9 +353,18 @@ __device__ __forceinline__ Item decode_item(const AttnArgs& a, int64_t n_tiles_l
   return it;
 }
 
-template <int DT, int D, int RG>
+// Key-row addressing, fixed per instantiation so that the tile loop carries no branch on it
+// (and no scalar registers for the other forms).
+enum AttnAddressing { kAddrFlat = 0, kAddrPagedNarrow = 1, kAddrPaged = 2 };
+
+__host__ __forceinline__ int attn_addressing(const AttnArgs& a) {
+  return !a.paged ? kAddrFlat : (a.narrow_ofs ? kAddrPagedNarrow : kAddrPaged);
+}
+
+template <int DT, int D, int RG, int AM>
 __global__ __launch_bounds__(kThreads, RG == 1 ? SB_ATTN_OCCUPANCY * 4 / kWaves : 1) void
 attn_mfma_kernel(const AttnBatch batch) {
+  constexpr bool kPaged = AM != kAddrFlat;
   AttnArgs a = batch.a;
   const int64_t item_b = select_request(batch, a, blockIdx.x, false);
   using M = Mma<DT>;
@@ -450,7 +459,7 @@ attn_mfma_kernel(const AttnBatch batch) {
 
   // Stage the chunk's block-table slice, then the key-offset tables of the first three tiles.
   int lb0 = 0;
-  if (a.paged) {
+  if (kPaged) {
     lb0 = static_cast<int>(k0 / a.block_size);
     const int nb = static_cast<int>((k1 - 1) / a.block_size) - lb0 + 1;
     for (int i = tid; i < nb; i += kThreads) bt_s[i] = clamp_block(a, a.block_table[lb0 + i]);
@@ -462,9 +471,9 @@ attn_mfma_kernel(const AttnBatch batch) {
   // and V rows share one offset, kept in kofs only.
   auto fill_offsets = [&](int slot, int t0, int i) {
     const int key = min(t0 + i, k1 - 1);
-    if (a.paged) {
+    if (kPaged) {
       uint64_t off;
-      if (a.narrow_ofs) {
+      if (AM == kAddrPagedNarrow) {
         const int lb = key >> a.bs_log2;
         const uint32_t in_block =
             static_cast<uint32_t>(key) & (static_cast<uint32_t>(a.block_size) - 1u);
@@ -528,7 +537,7 @@ attn_mfma_kernel(const AttnBatch batch) {
   };
   auto load_k = [&](int slot, int stage) { load_rows(ksrc, kofs[slot], Ks[stage]); };
   auto load_v = [&](int slot, int stage) {
-    load_rows(vsrc, a.paged ? kofs[slot] : vofs[slot], Vs[stage]);
+    load_rows(vsrc, kPaged ? kofs[slot] : vofs[slot], Vs[stage]);
   };
 
   // K fragment of (half n % kHalves, k-step n / kHalves): key row 32 * half + lq, 16-byte
@@ -998,6 +1007,24 @@ constexpr int kResidentSlots = kRowGroups == 1 ? 256 * SB_ATTN_OCCUPANCY * 4 / k
 #endif
 constexpr int kItemsPerSlot = SB_ATTN_ITEMS_PER_SLOT;
 
+// Launches the MFMA attention kernel instantiated for the addressing of `args.a`.
+#define SB_ATT_LAUNCH(DT, D, grid, st, args)                                              \
+  do {                                                                                    \
+    switch (attn_addressing((args).a)) {                                                  \
+      case kAddrFlat:                                                                     \
+        SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups, kAddrFlat>), grid,    \
+                  dim3(kThreads), st, args);                                              \
+        break;                                                                            \
+      case kAddrPagedNarrow:                                                              \
+        SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups, kAddrPagedNarrow>),   \
+                  grid, dim3(kThreads), st, args);                                        \
+        break;                                                                            \
+      default:                                                                            \
+        SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups, kAddrPaged>), grid,   \
+                  dim3(kThreads), st, args);                                              \
+    }                                                                                     \
+  } while (0)
+
 bool mfma_path(int32_t dtype, int64_t head_dim) {
   return (dtype == SB_DTYPE_BF16 || dtype == SB_DTYPE_F16) &&
          (head_dim == 64 || head_dim == 128);
@@ -1065,7 +1092,7 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
     one.num_reqs = 0;
 #define SB_ATT_CASE(DT, D)                                                              \
   if (dtype == DT && a.head_dim == D) {                                                 \
-    SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(kThreads), st, one); \
+    SB_ATT_LAUNCH(DT, D, grid, st, one);                                               \
     if (pl.max_chunks > 1)                                                              \
       SB_LAUNCH("attn_merge", (attn_merge_kernel<DT, D>), mgrid, dim3(256), st, one);   \
     return check_launch(fn);                                                            \
@@ -1207,7 +1234,7 @@ int launch_attention_varlen(const char* fn, AttnArgs a, int32_t dtype, int64_t n
     const dim3 mgrid(static_cast<unsigned>(merges));
 #define SB_ATT_VCASE(DT, D)                                                             \
   if (dtype == DT && a.head_dim == D) {                                                 \
-    SB_LAUNCH("attn_mfma", (attn_mfma_kernel<DT, D, kRowGroups>), grid, dim3(kThreads), st, b); \
+    SB_ATT_LAUNCH(DT, D, grid, st, b);                                                 \
     if (split) SB_LAUNCH("attn_merge", (attn_merge_kernel<DT, D>), mgrid, dim3(256), st, b); \
     const int rc = check_launch(fn);                                                    \
     if (rc) return rc;                                                                  \
