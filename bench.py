@@ -281,15 +281,17 @@ def cpu_model() -> dict:
                 info[key] = val.strip()
     except (OSError, ValueError):
         pass
-    if "Model name" not in info:
-        try:
-            with open("/proc/cpuinfo") as f:
-                for line in f:
-                    if line.startswith("model name"):
-                        info["Model name"] = line.split(":", 1)[1].strip()
-                        break
-        except OSError:
-            info["Model name"] = "unknown"
+    # /proc/cpuinfo's own string too: a virtual machine may report a shortened model name
+    # to lscpu, and the family / model numbers above then identify the part.
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    info["cpuinfo model name"] = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    info.setdefault("Model name", info.get("cpuinfo model name", "unknown"))
     return info
 
 
