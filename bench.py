@@ -63,10 +63,12 @@ KERNELS = ("attn_mfma", "attn_merge", "move_rows", "rope_rows", "rope_index", "f
 # this script, scaled by what the same counters read for the 1 GiB copy of copy_ceiling()
 # (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); kernel changes call for a new measurement.
 MEASURED_TRAFFIC_BYTES = {
-    "attn_mfma": (2 * 69196 + 43829) * 1024,
-    "move_rows": (2 * 390462 + 779859) * 1024,
-    "rope_rows": (2 * 114938 + 229392) * 1024,
+    "attn_mfma": (2 * 62559 + 40892) * 1024,
+    "move_rows": (2 * 390457 + 779858) * 1024,
+    "rope_rows": (2 * 114880 + 229388) * 1024,
 }
+MEASURED_TRAFFIC_SOURCE = ("rocprofv3 FETCH_SIZE / WRITE_SIZE passes at commit 1502a8d, "
+                           "profiles/kv_reuse_7b_16k_hbm_traffic.md")
 
 
 def log(msg: str) -> None:
@@ -905,6 +907,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(mfma_tflops / BF16_PEAK_TFLOPS, 4),
             "traffic": MEASURED_TRAFFIC_BYTES["attn_mfma"],
+            "traffic_source": MEASURED_TRAFFIC_SOURCE,
         },
         "phases": {
             "attention": {"ms": round(avg["attention"], 4),
