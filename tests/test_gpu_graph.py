@@ -100,3 +100,97 @@ def test_graph_rope_inplace(dev):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(k.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("nope", [False, True])
+def test_graph_prepared_permute_layers(dev, nope):
+    """The prepared multi-layer permutation (the RoPE hook's per-request call) replays the
+    eager permutation of vLLM-layout caches; it is not idempotent, so each replay starts from
+    the original caches."""
+    layers, nb, hkv, bs, d = 3, 14, 4, 16, 128
+    std = [randn((nb, 2, hkv, bs, d), torch.bfloat16, 30 + i) for i in range(layers)]
+    c0 = [s.permute(*rc._LAYOUT_AXES["vllm"]).contiguous().to(dev) for s in std]
+    caches = [c.clone() for c in c0]
+    bt = torch.randperm(nb, generator=gen(31))[:10].to(torch.int32).to(dev)
+    g0 = gen(32)
+    src = torch.randperm(160, generator=g0)[:100].tolist()
+    tgt = torch.randperm(160, generator=g0)[:100].tolist()
+    perm = list({t: (s_, t) for s_, t in zip(src, tgt)}.values())
+    call = rc.prepare_permute_paged_kv_layers(caches, bt, perm, rope_base=1e6, nope=nope,
+                                              layout="vllm")
+    call()
+    torch.cuda.synchronize()
+    want = [c.clone() for c in caches]
+    for c, o in zip(caches, c0):
+        c.copy_(o)
+    g = _capture(call)
+    for _ in range(3):
+        for c, o in zip(caches, c0):
+            c.copy_(o)
+        _noise(dev)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for c, w in zip(caches, want):
+            assert torch.equal(c.view(torch.int16), w.view(torch.int16))
+
+
+def test_graph_rope_scatter_layers(dev):
+    layers, hkv, d, bs, seq, pool = 4, 4, 128, 16, 2048, 160
+    caches = [torch.zeros((pool, 2, hkv, bs, d), dtype=torch.bfloat16, device=dev)
+              for _ in range(layers)]
+    donors = [randn((2, hkv, seq, d), torch.bfloat16, 40 + i).to(dev) for i in range(layers)]
+    bt = torch.randperm(pool, generator=gen(41))[: seq // bs].to(torch.int32).to(dev)
+    dp = torch.randperm(seq, generator=gen(42))[:1500].to(torch.int32).to(dev)
+    tp = torch.randperm(seq, generator=gen(43))[:1500].to(torch.int32).to(dev)
+
+    def step():
+        rc.rope_correct_scatter_paged_layers(caches, donors, bt, dp, tp, rope_base=5e5)
+
+    step()
+    torch.cuda.synchronize()
+    want = [c.clone() for c in caches]
+    g = _capture(step)
+    for _ in range(3):
+        for c in caches:
+            c.zero_()
+        _noise(dev)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for c, w in zip(caches, want):
+            assert torch.equal(c.view(torch.int16), w.view(torch.int16))
+
+
+@pytest.mark.parametrize("backend", ["fused", "library"])
+def test_graph_projection_paged(dev, backend):
+    """The compacted projection with its K/V write, both backends (the library one runs the
+    hipBLASLt GEMM through torch inside the graph)."""
+    rows, hidden, hq, hkv, d, bs, seq = 600, 1024, 8, 2, 128, 16, 2048
+    nb = seq // bs + 4
+    x = randn((seq, hidden), torch.bfloat16, 50).to(dev)
+    w = (randn(((hq + 2 * hkv) * d, hidden), torch.bfloat16, 51) * 0.03).to(dev)
+    b = randn(((hq + 2 * hkv) * d,), torch.bfloat16, 52).to(dev)
+    pos = torch.randperm(seq, generator=gen(53))[:rows].sort().values.to(torch.int32).to(dev)
+    bt = torch.randperm(nb, generator=gen(54))[: seq // bs].to(torch.int32).to(dev)
+    kv = torch.zeros((nb, 2, hkv, bs, d), dtype=torch.bfloat16, device=dev)
+    out = {}
+
+    def step():
+        out["q"] = tk.qkv_projection_paged(x, w, pos, kv, bt, num_heads=hq, num_kv_heads=hkv,
+                                           head_dim=d, qkv_bias=b, rope_base=1e6,
+                                           backend=backend)
+
+    step()
+    torch.cuda.synchronize()
+    want_q, want_kv = out["q"].clone(), kv.clone()
+    g = _capture(step)
+    for _ in range(3):
+        kv.zero_()
+        out["q"].zero_()
+        _noise(dev)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out["q"].view(torch.int16), want_q.view(torch.int16))
+        assert torch.equal(kv.view(torch.int16), want_kv.view(torch.int16))
