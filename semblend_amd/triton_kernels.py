@@ -273,8 +273,8 @@ def qkv_projection_paged(
     table. Returns Q [R, Hq, D] for the computed rows (``out`` may supply it). With
     ``rope_base``, Q and K are rotated by their position with the interleaved RoPE of this
     path before the single rounding. K/V slots out of the table are skipped; a position
-    outside the hidden states gives a zero Q row. bf16 / fp16, hidden a multiple of 64,
-    head_dim a multiple of 8.
+    outside the hidden states gives a zero Q row. bf16 / fp16, head_dim a multiple of 8,
+    hidden a multiple of 64 for the fused form and of 8 for the library form.
     ``backend``: "fused" runs one MFMA kernel that gathers the rows, multiplies and writes
     Q and K/V from its epilogue; "library" gathers the rows, multiplies them with the
     library GEMM (hipBLASLt through torch, fp32 output) and runs the same epilogue as a
@@ -288,6 +288,8 @@ def qkv_projection_paged(
     """
     from .rope_correction import inv_freq_table
 
+    if backend not in ("auto", "fused", "library"):
+        raise ValueError("backend must be 'auto', 'fused' or 'library'")
     dev = _lib.require_device(hidden_states, qkv_weight, kv_cache)
     dt = hidden_states.dtype
     if dt not in (torch.bfloat16, torch.float16):
@@ -320,8 +322,6 @@ def qkv_projection_paged(
     ws_bytes = _lib.size_query("sb_qkv_projection_paged_workspace_size", n, head_dim,
                                int(inv is not None))
     ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=dev)
-    if backend not in ("auto", "fused", "library"):
-        raise ValueError("backend must be 'auto', 'fused' or 'library'")
     if backend in ("library", "auto"):
         # rows outside the hidden states are gathered as zeros; the epilogue zeroes their Q
         # and writes no K/V for them

@@ -179,7 +179,9 @@ def test_projection_paged_rejects(dev):
     pos = torch.arange(4, dtype=torch.int32, device=dev)
     bt = torch.arange(1, dtype=torch.int32, device=dev)
     with pytest.raises(RuntimeError, match="multiple of 64"):
-        tk.qkv_projection_paged(x, w, pos, cache, bt, 2, 2, 16)
+        tk.qkv_projection_paged(x, w, pos, cache, bt, 2, 2, 16, backend="fused")
+    with pytest.raises(ValueError, match="backend"):
+        tk.qkv_projection_paged(x, w, pos, cache, bt, 2, 2, 16, backend="triton")
     with pytest.raises(TypeError):
         tk.qkv_projection_paged(x.float(), w.float(), pos, cache.float(), bt, 2, 2, 16)
     with pytest.raises(ValueError):
