@@ -173,6 +173,30 @@ def test_paged_layers_matches_per_layer(dev, dtype):
         assert_bit_exact(g, w)
 
 
+def test_paged_layers_full_size_7b(dev):
+    """The timed 28-layer launch of the 7B scatter workload (13926 pairs, caches
+    [2048, 2, 4, 16, 128] bf16, donors [2, 4, 16384, 128]): every layer equals the oracle's
+    scatter of that layer bit for bit. The oracle runs on the first, a middle and the last
+    layer; the other layers are compared with the single-layer entry, whose full-size result
+    is the oracle's (test_paged_full_size_7b_layer)."""
+    L = 28
+    bt = torch.randperm(2048, generator=gen(60))[:1024].to(torch.int32)
+    dp, tp = _chunk_pairs(16384, 256, 2458, 61)
+    assert dp.shape[0] == 13926
+    kvs = [randn((2048, 2, 4, 16, 128), torch.bfloat16, 100 + i).to(dev) for i in range(L)]
+    donors = [randn((2, 4, 16384, 128), torch.bfloat16, 200 + i).to(dev) for i in range(L)]
+    single = [k.clone() for k in kvs]
+    btd, dpd, tpd = bt.to(dev), dp.to(dev), tp.to(dev)
+    tk.scatter_donor_kv_paged_layers(kvs, donors, btd, dpd, tpd)
+    for layer in range(L):
+        tk.scatter_donor_kv_paged(single[layer], donors[layer], btd, dpd, tpd)
+        assert torch.equal(kvs[layer].view(torch.int16), single[layer].view(torch.int16))
+    for layer in (0, 13, L - 1):
+        kv0 = randn((2048, 2, 4, 16, 128), torch.bfloat16, 100 + layer)
+        want = ref.scatter_donor_kv_paged(kv0, donors[layer].cpu(), bt, dp, tp)
+        assert_bit_exact(kvs[layer], want)
+
+
 def test_cpu_tensors_rejected():
     kv = torch.zeros((2, 2, 1, 4, 8))
     with pytest.raises(RuntimeError, match="device tensors"):
