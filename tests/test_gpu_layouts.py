@@ -185,3 +185,51 @@ def test_paged_attention_layouts(dev, layout):
         cache, layout), bt, pos))
     assert_attn_close(outb[150:], ref.partial_attention_paged(q2[150:], rc.standard_view(
         cache, layout), bt[:32], pos2))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_trt_64_token_blocks(dev, dtype):
+    """TensorRT-LLM's common 64-token blocks [NB, 2, 64, H, D]: scatter bit-exact, the fused
+    RoPE scatter within the RoPE bar, the multi-layer delta permutation and paged attention,
+    each against the oracle on the standard view."""
+    nb, h, bs, d, s = 24, 4, 64, 128, 1024
+    cache = _cache("trt", nb, h, bs, d, dtype, 60)
+    donor = randn((2, h, s, d), dtype, 61)
+    bt = torch.randperm(nb, generator=gen(62))[:s // bs].to(torch.int32)
+    dp, tp = _pairs(s, 700, 63)
+    got = cache.to(dev)
+    tk.scatter_donor_kv_paged(rc.standard_view(got, "trt"), donor.to(dev), bt.to(dev),
+                              dp.to(dev), tp.to(dev))
+    want = cache.clone()
+    ref.scatter_donor_kv_paged(rc.standard_view(want, "trt"), donor, bt, dp, tp)
+    assert_bit_exact(got, want)
+    got = cache.to(dev)
+    rc.rope_correct_scatter_paged(rc.standard_view(got, "trt"), donor.to(dev), bt.to(dev),
+                                  dp.to(dev), tp.to(dev), rope_base=1e6)
+    want = cache.clone()
+    ref.rope_correct_scatter_paged(rc.standard_view(want, "trt"), donor, bt, dp, tp,
+                                   rope_base=1e6)
+    gv, wv = rc.standard_view(got.cpu(), "trt"), rc.standard_view(want, "trt")
+    assert_bit_exact(gv[:, 1], wv[:, 1])
+    assert_rope_close(gv, wv)
+    # permutation over two layers
+    caches = [_cache("trt", nb, h, bs, d, dtype, 64 + i) for i in range(2)]
+    perm = [(a_, b_) for a_, b_ in zip(torch.randperm(s, generator=gen(66))[:300].tolist(),
+                                      torch.randperm(s, generator=gen(67))[:300].tolist())]
+    perm = list({t: (s_, t) for s_, t in perm}.values())
+    got = [c.to(dev) for c in caches]
+    rc.permute_paged_kv_with_rope_layers(got, bt.to(dev), perm, rope_base=1e6, layout="trt")
+    for layer in range(2):
+        want = caches[layer].clone()
+        ref.permute_paged_kv_with_rope(rc.standard_view(want, "trt"), bt, perm, rope_base=1e6)
+        gv = rc.standard_view(got[layer].cpu(), "trt")
+        wv = rc.standard_view(want, "trt")
+        assert_bit_exact(gv[:, 1], wv[:, 1])
+        assert_rope_close(gv, wv)
+    # attention over the 64-token-block cache
+    pos = torch.randperm(s, generator=gen(68))[:120].sort().values.to(torch.int32)
+    q = randn((120, 28, d), dtype, 69)
+    out = tk.partial_prefill_attention_paged(q.to(dev), rc.standard_view(cache.to(dev), "trt"),
+                                             bt.to(dev), pos.to(dev))
+    assert_attn_close(out, ref.partial_attention_paged(q, rc.standard_view(cache, "trt"), bt,
+                                                       pos))
