@@ -49,11 +49,11 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWaveRows = 32;   // flattened query rows per MFMA row group
 // Wave priority (s_setprio) raised around the PV MFMA burst, so that of the two waves on a
-// SIMD the one with MFMAs ready issues first while the other forms P on the VALUs (3% on the
-// 7B workload: 368 -> 357 us); raising it around the QK MFMA + softmax block instead was
-// slower. 0 turns either off.
+// SIMD the one with MFMAs ready issues first while the other forms P on the VALUs. On the 7B
+// workload with the hand-laid tile loop: priority 1 319-324 us, 2 328-329, 3 327-330, none
+// about 360; raising it around the QK MFMA + softmax block instead was slower. 0 turns it off.
 #ifndef SB_ATTN_PV_PRIO
-#define SB_ATTN_PV_PRIO 2
+#define SB_ATTN_PV_PRIO 1
 #endif
 // LDS fragment reads issued ahead of the MFMA that consumes them (fragment rings are 4
 // deep, so at most 3).
