@@ -9,9 +9,11 @@
 // as (row, q-head-in-group), so the whole GQA group shares every K/V tile. A workgroup owns
 // 32 flattened rows per wave and one chunk of the key range, walked in tiles of 64 keys:
 //   * S^T = K Q^T with v_mfma_f32_32x32x16: K tile rows are the A operand (one ds_read_b128
-//     per lane per 16-wide k-step), Q stays in registers as the B operand, pre-multiplied by
-//     scale * log2(e). The accumulator starts at -m_ref, so the MFMA yields s - m_ref in the
-//     log2 domain. In the S^T accumulator each lane owns ONE query row and 16 keys.
+//     per lane per 16-wide k-step), Q stays in registers as the B operand exactly as given
+//     (no pre-scaling, which would add a bf16 rounding whose error grows with the score). The
+//     accumulation starts at 0; P = exp2(fma(scale * log2(e), s, -m_ref)), so the scale is
+//     applied to the fp32 score. In the S^T accumulator each lane owns ONE query row and 16
+//     keys.
 //   * O^T += V^T P^T with the same MFMA: P^T comes straight from the S^T accumulators (after
 //     exp2 and conversion) as the B operand. V stays in [key][d] layout in LDS; each A-operand
 //     fragment is two ds_read_b64_tr_b16 transpose loads, which hand every lane 4 consecutive
@@ -55,9 +57,17 @@ constexpr int kWaveRows = 32;   // flattened query rows per MFMA row group
 #ifndef SB_ATTN_PV_PRIO
 #define SB_ATTN_PV_PRIO 1
 #endif
-// LDS fragment reads issued ahead of the MFMA that consumes them (fragment rings are 4
-// deep, so at most 3).
-constexpr int kFragAhead = 3;
+// LDS fragment reads issued ahead of the MFMA that consumes them, through rings of kRing
+// fragments (a power of two above kFragAhead).
+#ifndef SB_ATTN_FRAG_AHEAD
+#define SB_ATTN_FRAG_AHEAD 3
+#endif
+#ifndef SB_ATTN_FRAG_RING
+#define SB_ATTN_FRAG_RING 4
+#endif
+constexpr int kFragAhead = SB_ATTN_FRAG_AHEAD;
+constexpr int kRing = SB_ATTN_FRAG_RING;
+static_assert(kRing > kFragAhead && (kRing & (kRing - 1)) == 0, "fragment ring");
 #ifndef SB_ATTN_ROW_GROUPS
 #define SB_ATTN_ROW_GROUPS 1
 #endif
@@ -440,8 +450,7 @@ attn_mfma_kernel(const AttnBatch batch) {
   const int pmin_w = __builtin_amdgcn_readfirstlane(wave_min_i(pmin_l));
   const int pmax_c = min(pmax_w, k1 - 1);
 
-  // Q fragments (B operand), pre-multiplied by scale * log2(e) and rounded to the input
-  // type, so that the MFMA yields scores in the log2 domain directly.
+  // Q fragments (B operand), the query rows as given.
   vec8 qf[RG][NKS];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
@@ -450,12 +459,10 @@ attn_mfma_kernel(const AttnBatch batch) {
     for (int s = 0; s < NKS; ++s) {
       vec8 v = {};
       if (p[g] >= 0) v = *reinterpret_cast<const vec8*>(qp + (16 * s + 8 * lg) * 2);
-      float f[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = static_cast<float>(v[e]) * a.scale_log2;
-      qf[g][s] = M::cvt8(f);
+      qf[g][s] = v;
     }
   }
+  const float c_log2 = a.scale_log2;  // scale * log2(e): score units -> log2 domain
 
   // Stage the chunk's block-table slice, then the key-offset tables of the first three tiles.
   int lb0 = 0;
@@ -495,20 +502,19 @@ attn_mfma_kernel(const AttnBatch batch) {
                                         tid % kTileKeys);
   __syncthreads();
 
-  // Softmax state per row: O and l are relative to a reference max m_ref (log2 domain).
-  // negm holds -m_ref in every accumulator slot and seeds the QK^T accumulation, so the MFMA
-  // output is already s - m_ref. A row is "seeded" once m_ref is its first live tile's max;
+  // Softmax state per row: O and l are relative to a reference max m_ref (log2 domain,
+  // of scale * log2(e) * s); negm = -m_ref enters every exp2 through one fma. A row is
+  // "seeded" once m_ref is its first live tile's max;
   // rows with no key in this chunk start seeded (their scores are all masked).
   float m_ref[RG], l_run[RG];
   bool seeded[RG];
-  f32x16_t negm[RG];
+  float negm[RG];
   f32x16_t o[RG][NDT];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
     m_ref[g] = 0.f;
     seeded[g] = plim[g] < k0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) negm[g][i] = 0.f;
+    negm[g] = 0.f;
     l_run[g] = 0.f;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
@@ -568,14 +574,14 @@ attn_mfma_kernel(const AttnBatch batch) {
     return __builtin_bit_cast(vec8, w);
   };
   using Scores = f32x16_t[RG][kHalves];
-  // S^T - m_ref = K Q^T - m_ref for one tile. (half, k-step) pairs alternate halves, so two
+  // S^T = K Q^T for one tile (fp32 scores). (half, k-step) pairs alternate halves, so two
   // independent accumulation chains interleave; K fragments stream through a 4-deep ring.
   auto qk = [&](int stage, Scores& sc) {
     constexpr int NQ = kHalves * NKS;
 #pragma unroll
     for (int g = 0; g < RG; ++g)
 #pragma unroll
-      for (int j = 0; j < kHalves; ++j) sc[g][j] = negm[g];
+      for (int j = 0; j < kHalves; ++j) sc[g][j] = f32x16_t{};
     vec8 ring[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) ring[n] = kfrag(stage, n);
@@ -602,10 +608,11 @@ attn_mfma_kernel(const AttnBatch batch) {
         }
     }
   };
-  // P = exp2(s - shift), rounded to the input type; the tile sum from the rounded values.
+  // P = exp2(scale * log2(e) * s - m_ref), rounded to the input type; the tile sum from the
+  // rounded values.
   vec8 pb[RG][kHalves][2];
   float tsum[RG];
-  auto exp_tile = [&](int g, const Scores& sc, float shift) {
+  auto exp_tile = [&](int g, const Scores& sc) {
     float acc[kHalves][2];  // independent partial sums (v_dot2 accumulates in place)
 #pragma unroll
     for (int j = 0; j < kHalves; ++j)
@@ -613,7 +620,8 @@ attn_mfma_kernel(const AttnBatch batch) {
       for (int h = 0; h < 2; ++h) {
         float pf[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pf[e] = __builtin_amdgcn_exp2f(sc[g][j][8 * h + e] - shift);
+        for (int e = 0; e < 8; ++e)
+          pf[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(c_log2, sc[g][j][8 * h + e], negm[g]));
         pb[g][j][h] = M::cvt8(pf);
         acc[j][h] = M::sum8(pb[g][j][h], 0.f);
       }
@@ -642,7 +650,7 @@ attn_mfma_kernel(const AttnBatch batch) {
   __syncthreads();  // K stage 0 is refilled at the top of the first iteration
 
   // slot = it mod 3 (offset-table ring), advanced once per tile.
-  auto iteration = [&](int it, int slot, auto has_next) {
+  auto iteration = [&](int it, int slot, auto has_next, Scores& s_cur, Scores& s_nxt) {
     constexpr bool NEXT = decltype(has_next)::value;
     const int t0 = k0 + it * kTileKeys;
     const int slot1 = slot == 2 ? 0 : slot + 1;  // (it + 1) mod 3
@@ -666,7 +674,7 @@ attn_mfma_kernel(const AttnBatch batch) {
       static_assert(NPAIR % NQ == 0, "P pairs split evenly over the MFMA steps");
       constexpr int PPS = NPAIR / NQ;                  // pairs per step
       const int ks = (it + 1) & 1;
-      vec8 ring[4];
+      vec8 ring[kRing];
 #pragma unroll
       for (int n = 0; n < kFragAhead; ++n) ring[n] = kfrag(ks, n);
       uint32_t pw[RG][kHalves][2][4];  // P words: [group][half][8-element pack][word]
@@ -674,18 +682,21 @@ attn_mfma_kernel(const AttnBatch batch) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int n = 0; n < NQ; ++n) {
-        if (n + kFragAhead < NQ) ring[(n + kFragAhead) & 3] = kfrag(ks, n + kFragAhead);
+        if (n + kFragAhead < NQ) ring[(n + kFragAhead) % kRing] = kfrag(ks, n + kFragAhead);
         const int j = n % kHalves;
 #pragma unroll
         for (int g = 0; g < RG; ++g)
-          s_nxt[g][j] = M::mma(ring[n & 3], qf[g][n / kHalves], n < kHalves ? negm[g] : s_nxt[g][j]);
+          s_nxt[g][j] =
+              M::mma(ring[n % kRing], qf[g][n / kHalves], n < kHalves ? f32x16_t{} : s_nxt[g][j]);
 #pragma unroll
         for (int pp = 0; pp < PPS; ++pp) {
           const int q = n * PPS + pp;
           const int g = q / (kHalves * 8), r = q % (kHalves * 8);
           const int hj = r / 8, h = (r / 4) % 2, w = r % 4;
-          const float e0 = __builtin_amdgcn_exp2f(s_cur[g][hj][8 * h + 2 * w]);
-          const float e1 = __builtin_amdgcn_exp2f(s_cur[g][hj][8 * h + 2 * w + 1]);
+          const float e0 =
+              __builtin_amdgcn_exp2f(__builtin_fmaf(c_log2, s_cur[g][hj][8 * h + 2 * w], negm[g]));
+          const float e1 = __builtin_amdgcn_exp2f(
+              __builtin_fmaf(c_log2, s_cur[g][hj][8 * h + 2 * w + 1], negm[g]));
           const auto pr = M::cvt2(e0, e1);
           pw[g][hj][h][w] = __builtin_bit_cast(uint32_t, pr);
           acc[g][hj][h] = M::sum2(pr, w == 0 ? 0.f : acc[g][hj][h]);
@@ -708,7 +719,7 @@ attn_mfma_kernel(const AttnBatch batch) {
       }
     } else {
 #pragma unroll
-      for (int g = 0; g < RG; ++g) exp_tile(g, s_cur, 0.f);
+      for (int g = 0; g < RG; ++g) exp_tile(g, s_cur);
     }
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
@@ -718,8 +729,8 @@ attn_mfma_kernel(const AttnBatch batch) {
     }
     if (NEXT) mask(t0 + kTileKeys, s_nxt);
     // ---- rare: seed the reference with the first live tile's max, or move it up when a
-    // tile would push P past kPMax; O and l are rescaled by 2^(m_old - m_new) and the
-    // already computed S(it+1) is shifted to the new reference ----
+    // tile would push P past kPMax; O and l are rescaled by 2^(m_old - m_new). Scores are
+    // kept unshifted, so S(it+1) needs no adjustment ----
     if (__any(bad_any)) {
 #pragma unroll
       for (int g = 0; g < RG; ++g) {
@@ -728,7 +739,8 @@ attn_mfma_kernel(const AttnBatch batch) {
         for (int j = 0; j < kHalves; ++j)
 #pragma unroll
           for (int i = 0; i < 16; ++i) v = fmaxf(v, s_cur[g][j][i]);
-        const float mx = fmaxf(v, xor32(v));  // row max of s - m_ref
+        const float smax = fmaxf(v, xor32(v));                    // row max of s
+        const float mx = __builtin_fmaf(c_log2, smax, negm[g]);   // ... relative to m_ref
         if (bad[g] && mx != -INFINITY) {
           const float alpha = seeded[g] ? __builtin_amdgcn_exp2f(-mx) : 0.f;
           l_run[g] *= alpha;
@@ -737,38 +749,31 @@ attn_mfma_kernel(const AttnBatch batch) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[g][t][i] *= alpha;
           m_ref[g] += mx;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) negm[g][i] = -m_ref[g];
+          negm[g] = -m_ref[g];
           seeded[g] = true;
-          exp_tile(g, s_cur, mx);
-          if (NEXT) {
-#pragma unroll
-            for (int j = 0; j < kHalves; ++j)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) s_nxt[g][j][i] -= mx;
-          }
+          exp_tile(g, s_cur);
         }
       }
     }
 #pragma unroll
     for (int g = 0; g < RG; ++g) l_run[g] += tsum[g];
-    // ---- O^T += V^T P^T; V fragments stream through a 4-deep ring, kFragAhead ahead ----
+    // ---- O^T += V^T P^T; V fragments stream through a ring, kFragAhead ahead ----
     if (live) {
 #if SB_ATTN_PV_PRIO
       __builtin_amdgcn_s_setprio(SB_ATTN_PV_PRIO);
 #endif
       constexpr int NV = 2 * kHalves * NDT;  // (half, step, d-tile) triples
       const int vb = it & 1;
-      vec8 vring[4];
+      vec8 vring[kRing];
 #pragma unroll
       for (int n = 0; n < kFragAhead; ++n) vring[n] = vfrag(vb, n);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int n = 0; n < NV; ++n) {
-        if (n + kFragAhead < NV) vring[(n + kFragAhead) & 3] = vfrag(vb, n + kFragAhead);
+        if (n + kFragAhead < NV) vring[(n + kFragAhead) % kRing] = vfrag(vb, n + kFragAhead);
         const int t = n % NDT, st = (n / NDT) & 1, j = n / (2 * NDT);
 #pragma unroll
-        for (int g = 0; g < RG; ++g) o[g][t] = M::mma(vring[n & 3], pb[g][j][st], o[g][t]);
+        for (int g = 0; g < RG; ++g) o[g][t] = M::mma(vring[n % kRing], pb[g][j][st], o[g][t]);
         __builtin_amdgcn_sched_barrier(0);
       }
 #if SB_ATTN_PV_PRIO
@@ -786,10 +791,10 @@ attn_mfma_kernel(const AttnBatch batch) {
   };
   int slot = 0;
   for (int it = 0; it + 1 < ntiles; ++it) {
-    iteration(it, slot, std::true_type{});
+    iteration(it, slot, std::true_type{}, s_cur, s_nxt);
     slot = slot == 2 ? 0 : slot + 1;
   }
-  iteration(ntiles - 1, slot, std::false_type{});
+  iteration(ntiles - 1, slot, std::false_type{}, s_cur, s_nxt);
 
   // ---- finish: lane holds d = 32t + 8*(i/4) + 4*lg + (i%4) of each of its rows ----
 #pragma unroll
@@ -1069,7 +1074,9 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
                      bool aligned16, void* workspace, int64_t workspace_bytes,
                      hipStream_t st) {
   if (rows_upper <= 0) return SB_OK;
-  if (mfma_path(dtype, a.head_dim) && aligned16) {
+  // The MFMA kernel masks keys with -inf scores before the scale is applied, so it takes
+  // positive scales; any other scale goes to the VALU kernel, which never forms a masked score.
+  if (mfma_path(dtype, a.head_dim) && aligned16 && a.scale_log2 > 0.f) {
     const Plan pl = make_plan(rows_upper, a.group, a.num_kv_heads, a.kv_len, a.head_dim,
                               a.block_size, a.paged != 0);
     a.ksplit = pl.ksplit;
@@ -1176,7 +1183,7 @@ int launch_attention_varlen(const char* fn, AttnArgs a, int32_t dtype, int64_t n
                             hipStream_t st) {
   const VarlenPlan pl = make_varlen_plan(num_reqs, rows, blocks, a.block_size, a.group,
                                          a.num_kv_heads, a.head_dim);
-  if (!(mfma_path(dtype, a.head_dim) && aligned16)) {
+  if (!(mfma_path(dtype, a.head_dim) && aligned16 && a.scale_log2 > 0.f)) {
     // VALU path: one launch per request.
     for (int r : pl.order) {
       AttnArgs b = a;

@@ -170,3 +170,30 @@ def test_paged_gqa_full_size_7b(dev):
                       torch.randperm(2458, generator=gen(71))[:44]]).unique()
     want = ref.partial_attention_paged(q[rows], kv, bt, pos[rows])
     assert_attn_close(got.cpu()[rows], want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_paged_gqa_rising_scores_rescale(dev, dtype):
+    """Scores that keep rising along the context, so the kernel's reference max must move
+    (O and l rescaled, the next tile's scores shifted) many times within one row: K rows are
+    scaled from 1 to 24 (bf16) or 1 to 4 (fp16) along the positions, so a late tile's
+    scores exceed the first tile's maximum by far more than the 2^64 (bf16) or 2^8 (fp16)
+    tile-sum bound of P. Rows at every 64-key tile boundary and at the end of the context,
+    with several key chunks for the long rows."""
+    hq, hkv, d, bs, ctx = 8, 2, 128, 16, 4096
+    nb = ctx // bs
+    top = 24.0 if dtype == torch.bfloat16 else 4.0
+    kv = randn((nb, 2, hkv, bs, d), torch.float32, 120)
+    scale = torch.linspace(1.0, top, ctx).view(nb, bs)          # per position
+    kv[:, 0] *= scale[:, None, :, None]
+    kv = kv.to(dtype)
+    bt = torch.arange(nb, dtype=torch.int32)
+    pos = torch.cat([torch.arange(63, ctx, 256), torch.tensor([0, 64, 4094, 4095]),
+                     torch.randint(0, ctx, (60,), generator=gen(121))]).unique()
+    pos = pos.sort().values.to(torch.int32)
+    q = randn((pos.shape[0], hq, d), dtype, 122)
+    got = tk.partial_prefill_attention_paged(q.to(dev), kv.to(dev), bt.to(dev), pos.to(dev))
+    want = ref.partial_attention_paged(q, kv, bt, pos)
+    # the softmax is peaked: most rows put nearly all weight on a few late keys
+    assert float(want.abs().amax()) > 1.0
+    assert_attn_close(got, want)

@@ -1,8 +1,8 @@
 """The attention parity bar must accept a correct 16-bit computation and reject a plausible
 wrong one, at the long contexts where outputs are small. CPU only.
 
-A correct bf16 kernel is emulated on the CPU (Q pre-scaled and rounded to bf16, P rounded to
-bf16 before the PV sum, output rounded once); the planted mistake is a split-key merge that
+A correct bf16 kernel is emulated on the CPU (fp32 scores scaled in fp32, P rounded to bf16
+before the PV sum, output rounded once); the planted mistake is a split-key merge that
 drops one of four key chunks, planted in a copy of the oracle's computation. The old
 absolute-only bar (2e-2) accepts that mistake at these lengths; the per-row relative bar does
 not.
@@ -37,7 +37,7 @@ def _emulated_bf16(q, kv, bt, pos, drop_chunk: int | None = None, n_chunks: int 
     k, v = ref.gather_paged_kv(kv, bt, int(pos.max()) + 1)
     k = k.repeat_interleave(group, dim=0)
     v = v.repeat_interleave(group, dim=0)
-    qs = (q.float() * (math.log2(math.e) / math.sqrt(d))).to(torch.bfloat16).float()
+    qs = q.float() * (math.log2(math.e) / math.sqrt(d))
     out = torch.zeros((rows, hq, d))
     for r, p in enumerate(pos.tolist()):
         keys = torch.arange(p + 1)
