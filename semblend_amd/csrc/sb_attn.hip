@@ -353,12 +353,15 @@ struct Item {
 
 __device__ __forceinline__ Item decode_item(const AttnArgs& a, int64_t n_tiles_live,
                                            int64_t b) {
-  // b = (chunk * n_tiles + tile_rev) * Hkv + kvh; tiles taken in descending order.
+  // b = (chunk * n_tiles_live + tile_rev) * Hkv + kvh; tiles taken in descending order.
+  // Counting live tiles (not the launch's upper bound) puts every live item before the
+  // items past the last chunk, which exit at once: with a row count known only on the
+  // device (dense drop-in) the launch is sized for all rows and most items are such.
   Item it;
   it.kvh = static_cast<int>(b % a.num_kv_heads);
   const int64_t rest = b / a.num_kv_heads;
-  const int64_t tile_rev = rest % a.n_tiles;
-  it.chunk = static_cast<int>(rest / a.n_tiles);
+  const int64_t tile_rev = rest % n_tiles_live;
+  it.chunk = static_cast<int>(min(rest / n_tiles_live, static_cast<int64_t>(0x7fffffff)));
   it.tile = n_tiles_live - 1 - tile_rev;
   return it;
 }
@@ -402,6 +405,7 @@ attn_mfma_kernel(const AttnBatch batch) {
   const int64_t n_rows = attn_num_rows(a);
   const int64_t rows_kv = n_rows * a.group;
   const int64_t n_tiles_live = (rows_kv + TR - 1) / TR;
+  if (n_tiles_live <= 0) return;  // no rows (uniform)
   const Item item = decode_item(a, n_tiles_live, item_b);
   if (item.tile < 0 || item.chunk >= a.max_chunks) return;  // uniform, before any barrier
   const int kvh = item.kvh;
