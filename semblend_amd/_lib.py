@@ -211,10 +211,23 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def upload_index(t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """int32 contiguous device copy of a host index tensor, staged through pinned memory so
+    that the copy is enqueued on the current stream without blocking the host (torch's
+    pinned-memory cache keeps the staging block until the copy has run)."""
+    host = t.to(torch.int32).contiguous()
+    if host.numel() == 0:
+        return torch.empty(host.shape, dtype=torch.int32, device=device)
+    return host.pin_memory().to(device, non_blocking=True)
+
+
 def as_index(t, device: torch.device) -> torch.Tensor:
-    """int32 contiguous device copy of an index tensor or sequence (no copy if already so)."""
+    """int32 contiguous device copy of an index tensor or sequence (no copy if already so);
+    host data is uploaded without blocking the host."""
     if not isinstance(t, torch.Tensor):
         t = torch.as_tensor(list(t), dtype=torch.int32)
+    if t.device.type == "cpu":
+        return upload_index(t, device).reshape(-1)
     if t.device != device:
         t = t.to(device)
     if t.dtype != torch.int32:

@@ -478,10 +478,10 @@ def apply_rope_delta_inplace(
     counts, modified = _rotation_counts(positions, block_size, nbs)
     if not counts:
         return 0
-    pos_t = torch.tensor(list(counts.keys()), dtype=torch.int32).to(dev)
+    pos_t = _lib.upload_index(torch.tensor(list(counts.keys()), dtype=torch.int32), dev)
     rep_t = None
     if any(c != 1 for c in counts.values()):
-        rep_t = torch.tensor(list(counts.values()), dtype=torch.int32).to(dev)
+        rep_t = _lib.upload_index(torch.tensor(list(counts.values()), dtype=torch.int32), dev)
     bt = _lib.as_index(block_table, dev)
     inv_freq = inv_freq_table(rope_base, head_dim, dev)
     with torch.cuda.device(dev):
