@@ -36,6 +36,15 @@ extern "C" {
 #define SB_DTYPE_F16 1
 #define SB_DTYPE_BF16 2
 
+/* Flags of the multi-layer scatters (sb_*_paged_layers, sb_composite_scatter_paged_layers).
+ * SB_SCATTER_REPEATED_DONOR_ROWS: a donor row may be the source of several pairs (one
+ * donor position mapped to several targets). The launch then reads the donor through the
+ * caches so that the repeats are served from L2 / Infinity Cache; without it the donor is
+ * read with nontemporal loads, which is faster when every donor row is read once. Either
+ * setting gives the same results. */
+#define SB_SCATTER_REPEATED_DONOR_ROWS 1
+#define SB_SCATTER_FLAGS_ALL 1
+
 /* Library version string, e.g. "semblend_hip 0.1.0 gfx950". */
 const char* sb_version(void);
 
@@ -70,6 +79,7 @@ int sb_scatter_donor_kv_paged(void* kv_cache, const void* donor_kv, const int32_
 
 /* Paged scatter over several layers in one launch. kv_layer_ptrs / donor_layer_ptrs are
  * DEVICE arrays of num_layers base addresses (uint64); every layer shares the strides.
+ * flags: 0 or SB_SCATTER_REPEATED_DONOR_ROWS (other bits are rejected).
  * No reference counterpart: it replaces the per-layer loop of callers such as
  * synapse_kv_connector/model_runner_hook.py:215-276. */
 int sb_scatter_donor_kv_paged_layers(const uint64_t* kv_layer_ptrs,
@@ -79,7 +89,8 @@ int sb_scatter_donor_kv_paged_layers(const uint64_t* kv_layer_ptrs,
                                      int64_t num_heads, int64_t block_size, int64_t head_dim,
                                      int64_t donor_seq_len, int64_t num_blocks_total,
                                      int64_t num_blocks_per_seq, const int64_t* kv_strides,
-                                     const int64_t* d_strides, int32_t dtype, void* stream);
+                                     const int64_t* d_strides, int32_t dtype, int32_t flags,
+                                     void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * QKV projection (bf16 / fp16 on the matrix cores, fp32 accumulation, one rounding)
@@ -163,9 +174,9 @@ int sb_rope_correct_scatter_paged(void* kv_cache, const void* donor_kv,
                                   const int64_t* kv_strides, const int64_t* d_strides,
                                   int32_t dtype, void* stream);
 
-/* Multi-layer form of sb_rope_correct_scatter_paged (device arrays of layer base addresses,
- * as in sb_scatter_donor_kv_paged_layers). cos/sin are computed once per pair and shared by
- * every layer and head. No reference counterpart (replaces a per-layer caller loop, e.g.
+/* Multi-layer form of sb_rope_correct_scatter_paged (device arrays of layer base addresses
+ * and flags as in sb_scatter_donor_kv_paged_layers). cos/sin are computed once per pair and
+ * shared by every layer and head. No reference counterpart (replaces a per-layer caller loop, e.g.
  * semblend/integration/trtllm/pytorch_backend.py:106-154). */
 int sb_rope_correct_scatter_paged_layers(const uint64_t* kv_layer_ptrs,
                                          const uint64_t* donor_layer_ptrs, int64_t num_layers,
@@ -175,7 +186,8 @@ int sb_rope_correct_scatter_paged_layers(const uint64_t* kv_layer_ptrs,
                                          int64_t block_size, int64_t head_dim,
                                          int64_t donor_seq_len, int64_t num_blocks_total,
                                          int64_t num_blocks_per_seq, const int64_t* kv_strides,
-                                         const int64_t* d_strides, int32_t dtype, void* stream);
+                                         const int64_t* d_strides, int32_t dtype,
+                                         int32_t flags, void* stream);
 
 /* Composite (multi-donor) scatter over many layers in one pass: pair i moves the rows of
  * donor donor_index[i] at position donor_pos[i] (K and V, every layer and head) to
@@ -191,6 +203,7 @@ int sb_rope_correct_scatter_paged_layers(const uint64_t* kv_layer_ptrs,
  * Pairs whose donor index, donor position or target slot is out of range are skipped.
  * Target positions must be distinct across all pairs (a composite plan gives each target
  * position one donor); duplicates race. Donors are moved in launches of at most 16.
+ * flags: as for sb_scatter_donor_kv_paged_layers.
  * No reference counterpart: the reference carries the per-position donor map
  * (semblend_core/partial_attention.py:306-435, multi_donor_types.py:50-78) but loads and
  * scatters one donor at a time (synapse_kv_connector/semblend_connector.py:1508-1701). */
@@ -202,7 +215,7 @@ int sb_composite_scatter_paged_layers(const uint64_t* kv_layer_ptrs, int64_t num
                                       int64_t num_heads, int64_t block_size, int64_t head_dim,
                                       const int32_t* block_table, int64_t num_blocks_total,
                                       int64_t num_blocks_per_seq, const int64_t* kv_strides,
-                                      int32_t dtype, void* stream);
+                                      int32_t dtype, int32_t flags, void* stream);
 
 /* Flat RoPE correction over k [L, H, S, D] (k_strides[4]; pass L = 1 for [H, S, D]):
  * for each pair i in order, the row at donor position d_i is rotated by (t_i - d_i) and

@@ -19,6 +19,8 @@ LIB_PATH = Path(__file__).resolve().parent / "libsemblend_hip.so"
 
 SB_OK = 0
 SB_ERR_INVALID_ARGUMENT = 100001
+# Flag of the multi-layer scatters: a donor row may be the source of several pairs.
+SB_SCATTER_REPEATED_DONOR_ROWS = 1
 SB_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 _vp = ctypes.c_void_p
@@ -34,15 +36,15 @@ SIGNATURES: dict[str, list] = {
     "sb_scatter_donor_kv_paged": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _i64p, _i64p, _i32, _vp],
     "sb_scatter_donor_kv_paged_layers": [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
-                                         _i64, _i64, _i64, _i64p, _i64p, _i32, _vp],
+                                         _i64, _i64, _i64, _i64p, _i64p, _i32, _i32, _vp],
     "sb_rope_correct_scatter_paged": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                       _i64, _i64, _i64, _i64p, _i64p, _i32, _vp],
     "sb_rope_correct_scatter_paged_layers": [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
                                              _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i32,
-                                             _vp],
+                                             _i32, _vp],
     "sb_composite_scatter_paged_layers": [_vp, _i64, _vp, _i64, _i64p, _vp, _vp, _vp, _vp,
                                           _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64p, _i32,
-                                          _vp],
+                                          _i32, _vp],
     "sb_rope_correct_k": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p,
                           _i64p, _i32, _vp],
     "sb_rope_correct_k_distinct": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p,
@@ -233,6 +235,36 @@ def as_index(t, device: torch.device) -> torch.Tensor:
     if t.dtype != torch.int32:
         t = t.to(torch.int32)
     return t.contiguous().reshape(-1)
+
+
+def rows_repeat(positions, donor_index=None, sync: bool = False) -> bool:
+    """Whether some donor row is the source of more than one pair: a position that occurs
+    twice (with the same donor, when ``donor_index`` is given). Host data is checked on the
+    host; device tensors only when ``sync`` allows one device-to-host read, and are otherwise
+    taken as distinct. Only the scatters' load policy depends on the answer, not their
+    results."""
+    on_dev = any(isinstance(x, torch.Tensor) and x.device.type != "cpu"
+                 for x in (positions, donor_index))
+    if on_dev and not sync:
+        return False
+    if not isinstance(positions, torch.Tensor):
+        positions = torch.as_tensor(list(positions) if not hasattr(positions, "__array__")
+                                    else positions)
+    key = positions.reshape(-1).to(torch.int64)
+    n = key.numel()
+    if n < 2:
+        return False
+    if donor_index is not None:
+        if not isinstance(donor_index, torch.Tensor):
+            donor_index = torch.as_tensor(list(donor_index) if not hasattr(
+                donor_index, "__array__") else donor_index)
+        idx = donor_index.reshape(-1).to(device=key.device, dtype=torch.int64)
+        key = idx * (1 << 32) + (key & 0xFFFFFFFF)
+    return int(torch.unique(key).numel()) < n
+
+
+def scatter_flags(repeated: bool) -> int:
+    return SB_SCATTER_REPEATED_DONOR_ROWS if repeated else 0
 
 
 _ADDR_TABLES: dict[tuple, torch.Tensor] = {}

@@ -52,7 +52,9 @@ enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3 };
 #ifndef SB_ROPE_ROWS_PER_GROUP
 #define SB_ROPE_ROWS_PER_GROUP 0
 #endif
-// Pair movers' access hints (nontemporal loads / stores).
+// Pair movers' access hints (nontemporal loads / stores). A launch whose source rows repeat
+// across pairs (several targets of one donor row) reads through the caches instead
+// (MoveArgs::cached_loads): the repeats then hit L2 / Infinity Cache rather than HBM.
 #ifndef SB_MOVE_NT_LOAD
 #define SB_MOVE_NT_LOAD 1
 #endif
@@ -121,6 +123,7 @@ struct MoveArgs {
   int k_slices;
   int v_layers_per_group;
   int src_index_check;     // ROW_INDEX source: also require src_pos to be a valid paged slot
+  int cached_loads;        // source rows may repeat across pairs: cached, not nontemporal, loads
   int vpr;                 // vectors per row
   int tpr_log2;            // log2(threads per row)
 };
@@ -333,10 +336,16 @@ __global__ __launch_bounds__(kThreads) void move_rows_kernel(MoveArgs a) {
     const int64_t vofs = static_cast<int64_t>(j) * VB;
     for (int r0 = 0; r0 < nrows; r0 += kBatch) {
       uint32_t w[kBatch][W];
+      if (a.cached_loads) {
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b)
-        if (r0 + b < nrows)
-          load_vec<VB, SB_MOVE_NT_LOAD>(row_of(src, r0 + b) + src_off + vofs, w[b]);
+        for (int b = 0; b < kBatch; ++b)
+          if (r0 + b < nrows) load_vec<VB, false>(row_of(src, r0 + b) + src_off + vofs, w[b]);
+      } else {
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
+          if (r0 + b < nrows)
+            load_vec<VB, SB_MOVE_NT_LOAD>(row_of(src, r0 + b) + src_off + vofs, w[b]);
+      }
 #pragma unroll
       for (int b = 0; b < kBatch; ++b) {
         if (r0 + b >= nrows) continue;
@@ -707,7 +716,7 @@ static int paged_scatter_impl(const char* fn, void* kv_base, const uint64_t* kv_
                               int64_t block_size, int64_t head_dim, int64_t donor_seq_len,
                               int64_t num_blocks_total, int64_t num_blocks_per_seq,
                               const int64_t* ks, const int64_t* ds, int32_t dtype,
-                              bool rope, void* stream) {
+                              bool rope, int32_t flags, void* stream) {
   clear_error();
   if (num_pairs == 0 || num_layers == 0 || num_heads == 0 || head_dim == 0) return SB_OK;
   if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
@@ -717,6 +726,7 @@ static int paged_scatter_impl(const char* fn, void* kv_base, const uint64_t* kv_
   if (rope && !inv_freq) return fail(fn, "null inv_freq");
   if (rope && (head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
   if (block_size <= 0) return fail(fn, "block_size must be positive");
+  if (flags & ~SB_SCATTER_FLAGS_ALL) return fail(fn, "unknown flags");
   if (ks[4] != 1 || ds[3] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
   const int64_t es = elem_size(dtype);
   // Per-layer tables are checked for 16-byte alignment by the caller.
@@ -745,6 +755,7 @@ static int paged_scatter_impl(const char* fn, void* kv_base, const uint64_t* kv_
   a.layers_per_group = layers_per_group_for(num_layers, num_pairs, rope);
   a.kv_first = 0;
   a.num_kv = 2;
+  a.cached_loads = (flags & SB_SCATTER_REPEATED_DONOR_ROWS) ? 1 : 0;
   const int groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (rope)
@@ -764,7 +775,7 @@ extern "C" int sb_scatter_donor_kv_paged(void* kv_cache, const void* donor_kv,
   return paged_scatter_impl("sb_scatter_donor_kv_paged", kv_cache, nullptr, donor_kv, nullptr,
                             1, block_table, donor_pos, target_pos, nullptr, num_pairs,
                             num_heads, block_size, head_dim, donor_seq_len, num_blocks_total,
-                            num_blocks_per_seq, kv_strides, d_strides, dtype, false, stream);
+                            num_blocks_per_seq, kv_strides, d_strides, dtype, false, 0, stream);
 }
 
 extern "C" int sb_scatter_donor_kv_paged_layers(
@@ -772,7 +783,8 @@ extern "C" int sb_scatter_donor_kv_paged_layers(
     const int32_t* block_table, const int32_t* donor_pos, const int32_t* target_pos,
     int64_t num_pairs, int64_t num_heads, int64_t block_size, int64_t head_dim,
     int64_t donor_seq_len, int64_t num_blocks_total, int64_t num_blocks_per_seq,
-    const int64_t* kv_strides, const int64_t* d_strides, int32_t dtype, void* stream) {
+    const int64_t* kv_strides, const int64_t* d_strides, int32_t dtype, int32_t flags,
+    void* stream) {
   if (!kv_layer_ptrs || !donor_layer_ptrs) {
     clear_error();
     if (num_pairs == 0 || num_layers == 0) return SB_OK;
@@ -782,7 +794,7 @@ extern "C" int sb_scatter_donor_kv_paged_layers(
                             nullptr, donor_layer_ptrs, num_layers, block_table, donor_pos,
                             target_pos, nullptr, num_pairs, num_heads, block_size, head_dim,
                             donor_seq_len, num_blocks_total, num_blocks_per_seq, kv_strides,
-                            d_strides, dtype, false, stream);
+                            d_strides, dtype, false, flags, stream);
 }
 
 extern "C" int sb_rope_correct_scatter_paged(void* kv_cache, const void* donor_kv,
@@ -800,7 +812,7 @@ extern "C" int sb_rope_correct_scatter_paged(void* kv_cache, const void* donor_k
                             nullptr, 1, block_table, donor_pos, target_pos, inv_freq,
                             num_pairs, num_heads, block_size, head_dim, donor_seq_len,
                             num_blocks_total, num_blocks_per_seq, kv_strides, d_strides, dtype,
-                            true, stream);
+                            true, 0, stream);
 }
 
 extern "C" int sb_rope_correct_scatter_paged_layers(
@@ -809,7 +821,7 @@ extern "C" int sb_rope_correct_scatter_paged_layers(
     const float* inv_freq, int64_t num_pairs, int64_t num_heads, int64_t block_size,
     int64_t head_dim, int64_t donor_seq_len, int64_t num_blocks_total,
     int64_t num_blocks_per_seq, const int64_t* kv_strides, const int64_t* d_strides,
-    int32_t dtype, void* stream) {
+    int32_t dtype, int32_t flags, void* stream) {
   if (!kv_layer_ptrs || !donor_layer_ptrs) {
     clear_error();
     if (num_pairs == 0 || num_layers == 0) return SB_OK;
@@ -819,7 +831,7 @@ extern "C" int sb_rope_correct_scatter_paged_layers(
                             nullptr, donor_layer_ptrs, num_layers, block_table, donor_pos,
                             target_pos, inv_freq, num_pairs, num_heads, block_size, head_dim,
                             donor_seq_len, num_blocks_total, num_blocks_per_seq, kv_strides,
-                            d_strides, dtype, true, stream);
+                            d_strides, dtype, true, flags, stream);
 }
 
 // Composite (multi-donor) scatter over many layers: pair i moves donor
@@ -831,7 +843,7 @@ extern "C" int sb_composite_scatter_paged_layers(
     const int32_t* donor_pos, const int32_t* target_pos, const float* inv_freq,
     int64_t num_pairs, int64_t num_heads, int64_t block_size, int64_t head_dim,
     const int32_t* block_table, int64_t num_blocks_total, int64_t num_blocks_per_seq,
-    const int64_t* kv_strides, int32_t dtype, void* stream) {
+    const int64_t* kv_strides, int32_t dtype, int32_t flags, void* stream) {
   const char* fn = "sb_composite_scatter_paged_layers";
   clear_error();
   if (num_pairs == 0 || num_layers == 0 || num_heads == 0 || head_dim == 0 || num_donors == 0)
@@ -843,6 +855,7 @@ extern "C" int sb_composite_scatter_paged_layers(
   const bool rope = inv_freq != nullptr;
   if (rope && (head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
   if (block_size <= 0) return fail(fn, "block_size must be positive");
+  if (flags & ~SB_SCATTER_FLAGS_ALL) return fail(fn, "unknown flags");
   if (kv_strides[4] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
   if (num_donors > 0x7fffffff || num_layers > 0x7fffffff)
     return fail(fn, "too many donors or layers");
@@ -879,6 +892,7 @@ extern "C" int sb_composite_scatter_paged_layers(
   a.layers_per_group = layers_per_group_for(num_layers, num_pairs, rope);
   a.kv_first = 0;
   a.num_kv = 2;
+  a.cached_loads = (flags & SB_SCATTER_REPEATED_DONOR_ROWS) ? 1 : 0;
   const int groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
   hipStream_t st = static_cast<hipStream_t>(stream);
   for (int64_t first = 0; first < num_donors; first += kMaxDonors) {

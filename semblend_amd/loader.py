@@ -141,6 +141,7 @@ class ChunkedKVLoader:
         n_all = pairs.shape[1]
         if n_all == 0:
             return
+        flags = _lib.scatter_flags(_lib.rows_repeat(np.asarray(donor_positions)))
         cur = torch.cuda.current_stream(self.dev)
         side = self.scatter_stream
         side.wait_stream(cur)  # the caches' earlier users and the pair upload come first
@@ -178,7 +179,7 @@ class ChunkedKVLoader:
                 base + 4 * (2 * n_all + lo), base + 4 * lo, base + 4 * (n_all + lo), inv,
                 hi - lo, self.num_heads, self.block_size, self.head_dim,
                 self.block_table.data_ptr(), self.nb_total, self.block_table.shape[0],
-                self._kv_strides, self._dtype_code, side.cuda_stream)
+                self._kv_strides, self._dtype_code, flags, side.cuda_stream)
             if rc != _lib.SB_OK:
                 raise RuntimeError("sb_composite_scatter_paged_layers failed: "
                                    + lib.sb_last_error_string().decode())

@@ -110,6 +110,7 @@ def composite_scatter_paged_layers(
     rope: bool = True,
     rope_base: float = 10000.0,
     donor_first_positions: Sequence[int] | None = None,
+    repeated_donor_rows: bool | None = None,
 ) -> list[torch.Tensor]:
     """Scatter pairs from several donors into every layer's paged cache in one pass.
 
@@ -124,6 +125,9 @@ def composite_scatter_paged_layers(
     donor_first_positions: per donor, the sequence position its tensors' row 0 holds
         (default 0): a tensor holding only a window ``[f, f + S_k)`` of a donor (one staged
         chunk) is read at ``donor_positions[i] - f`` and rotated by the true delta.
+    repeated_donor_rows: whether one donor row may be the source of several pairs (the
+        donors are then read through the caches); None decides from host positions and
+        takes device positions as distinct. It changes speed, not results.
     """
     num_pairs = len(target_positions)
     if num_pairs == 0 or not kv_caches or not donor_kvs:
@@ -161,6 +165,8 @@ def composite_scatter_paged_layers(
     tpos = _lib.as_index(_as_tensor(target_positions), dev)
     if not (didx.shape[0] == dpos.shape[0] == tpos.shape[0]):
         raise ValueError("donor_index, donor_positions and target_positions differ in length")
+    if repeated_donor_rows is None:
+        repeated_donor_rows = _lib.rows_repeat(donor_positions, donor_index)
     inv_freq = inv_freq_table(rope_base, head_dim, dev) if rope else None
     with torch.cuda.device(dev):
         _lib.call(
@@ -169,7 +175,8 @@ def composite_scatter_paged_layers(
             _lib.i64_array(strides), didx.data_ptr(), dpos.data_ptr(), tpos.data_ptr(),
             inv_freq.data_ptr() if inv_freq is not None else None, num_pairs, num_heads,
             block_size, head_dim, bt.data_ptr(), nb_total, bt.shape[0], _lib.strides(ref),
-            _lib.dtype_code(ref), _lib.stream_handle(dev),
+            _lib.dtype_code(ref), _lib.scatter_flags(repeated_donor_rows),
+            _lib.stream_handle(dev),
         )
     return kv_caches
 

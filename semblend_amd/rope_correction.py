@@ -126,16 +126,21 @@ def rope_correct_scatter_paged_layers(
     donor_positions: torch.Tensor,
     target_positions: torch.Tensor,
     rope_base: float = 10000.0,
+    repeated_donor_rows: bool | None = None,
 ) -> list[torch.Tensor]:
     """``rope_correct_scatter_paged`` over many layers in one launch.
 
     kv_caches / donor_kvs: one tensor per layer, all with the same shape, strides and dtype.
-    cos/sin of each pair are evaluated once and reused for every layer and head. Extension
+    cos/sin of each pair are evaluated once and reused for every layer and head.
+    repeated_donor_rows: as in ``prepare_scatter_paged_layers``, except that None takes
+    device positions as distinct (no synchronisation per call). Extension
     with no reference counterpart; it replaces a per-layer loop around
     ``rope_correct_scatter_paged`` (semblend/integration/trtllm/pytorch_backend.py:106-154).
     """
+    if repeated_donor_rows is None:
+        repeated_donor_rows = _lib.rows_repeat(donor_positions)
     call = prepare_scatter_paged_layers(kv_caches, donor_kvs, block_table, donor_positions,
-                                        target_positions, rope_base)
+                                        target_positions, rope_base, repeated_donor_rows)
     if call is not None:
         call()
     return kv_caches
@@ -169,12 +174,20 @@ def prepare_scatter_paged_layers(
     donor_positions: torch.Tensor,
     target_positions: torch.Tensor,
     rope_base: float | None = 10000.0,
+    repeated_donor_rows: bool | None = None,
 ) -> PreparedScatter | None:
     """Check the inputs of the multi-layer paged scatter once and bind them: K is rotated by
     ``target - donor`` with RoPE base ``rope_base``, or copied unrotated (with V) when
     ``rope_base`` is None. Returns None when there are no pairs. For callers that repeat the
     same scatter every step: the host work of validation, address tables and index uploads
-    is done here, not per launch; the tensors must keep their storage afterwards."""
+    is done here, not per launch; the tensors must keep their storage afterwards.
+
+    repeated_donor_rows: whether a donor position may be the source of several pairs (e.g.
+    chunks whose deltas make their donor windows overlap). The launch then reads donors
+    through the caches, which serves the repeats from L2 / Infinity Cache; otherwise it reads
+    them with nontemporal loads, faster when each donor row is read once. None finds out
+    from the positions (one device-to-host read for device positions, here only). Results
+    are the same either way."""
     if len(kv_caches) != len(donor_kvs):
         raise ValueError("kv_caches and donor_kvs must have the same length")
     num_pairs = len(donor_positions)
@@ -192,13 +205,16 @@ def prepare_scatter_paged_layers(
     _check_uniform(donor_kvs, "donor_kvs")
     if dref.dtype != ref.dtype:
         raise TypeError("donor_kvs and kv_caches must share a dtype")
+    if repeated_donor_rows is None:
+        repeated_donor_rows = _lib.rows_repeat(donor_positions, sync=True)
     kv_tab = _layer_table(kv_caches, dev)
     d_tab = _layer_table(donor_kvs, dev)
     bt = _lib.as_index(block_table, dev)
     dpos = _lib.as_index(donor_positions, dev)
     tpos = _lib.as_index(target_positions, dev)
     tail = (num_pairs, num_heads, block_size, head_dim, dref.shape[2], nb_total, bt.shape[0],
-            _lib.strides(ref), _lib.strides(dref), _lib.dtype_code(ref))
+            _lib.strides(ref), _lib.strides(dref), _lib.dtype_code(ref),
+            _lib.scatter_flags(repeated_donor_rows))
     head = (kv_tab.data_ptr(), d_tab.data_ptr(), len(kv_caches), bt.data_ptr(),
             dpos.data_ptr(), tpos.data_ptr())
     if rope:

@@ -153,12 +153,16 @@ def scatter_donor_kv_paged_layers(
     block_table: torch.Tensor,
     donor_positions: torch.Tensor,
     target_positions: torch.Tensor,
+    repeated_donor_rows: bool | None = None,
 ) -> list[torch.Tensor]:
     """``scatter_donor_kv_paged`` for every layer in a single launch.
 
     kv_caches / donor_kvs: one tensor per layer (same shape, strides and dtype across
-    layers, 16-byte aligned bases). Extension with no reference counterpart; it replaces the
-    per-layer Python loop of callers such as synapse_kv_connector/model_runner_hook.py:215-276.
+    layers, 16-byte aligned bases). repeated_donor_rows: whether a donor position may be the
+    source of several pairs (the donor is then read through the caches); None decides from
+    host positions and takes device positions as distinct. It changes speed, not results.
+    Extension with no reference counterpart; it replaces the per-layer Python loop of callers
+    such as synapse_kv_connector/model_runner_hook.py:215-276.
     """
     if len(kv_caches) != len(donor_kvs):
         raise ValueError("kv_caches and donor_kvs must have the same length")
@@ -177,6 +181,8 @@ def scatter_donor_kv_paged_layers(
     if ref.dtype != dref.dtype:
         raise TypeError("kv_caches and donor_kvs must share a dtype")
     nb_total, _, num_heads, block_size, head_dim = ref.shape
+    if repeated_donor_rows is None:
+        repeated_donor_rows = _lib.rows_repeat(donor_positions)
     kv_tab = _lib.address_table(kv_caches, dev)
     d_tab = _lib.address_table(donor_kvs, dev)
     bt = _lib.as_index(block_table, dev)
@@ -188,7 +194,8 @@ def scatter_donor_kv_paged_layers(
             kv_tab.data_ptr(), d_tab.data_ptr(), len(kv_caches), bt.data_ptr(),
             dpos.data_ptr(), tpos.data_ptr(), num_pairs, num_heads, block_size, head_dim,
             dref.shape[2], nb_total, bt.shape[0], _lib.strides(ref), _lib.strides(dref),
-            _lib.dtype_code(ref), _lib.stream_handle(dev),
+            _lib.dtype_code(ref), _lib.scatter_flags(repeated_donor_rows),
+            _lib.stream_handle(dev),
         )
     return kv_caches
 

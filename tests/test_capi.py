@@ -81,6 +81,14 @@ def test_invalid_arguments_are_rejected_without_launch():
                                           0.1, _i64(1, 1, 1), _i64(1, 1, 1), _i64(1, 1, 1),
                                           _i64(1, 1, 1), 2, None)
     assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"workspace" in lib.sb_last_error_string()
+    # unknown scatter flags (bit 0 is the only one defined)
+    rc = lib.sb_scatter_donor_kv_paged_layers(fake, fake, 2, fake, fake, fake, 4, 1, 16, 8, 4,
+                                              4, 1, st, _i64(1, 1, 1, 1), 2, 2, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"flags" in lib.sb_last_error_string()
+    rc = lib.sb_composite_scatter_paged_layers(fake, 2, fake, 1, _i64(1, 1, 1, 4, 0), fake,
+                                               fake, fake, None, 4, 1, 16, 8, fake, 4, 1, st,
+                                               2, 4, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"flags" in lib.sb_last_error_string()
 
 
 def test_empty_calls_are_no_ops():

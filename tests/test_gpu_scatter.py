@@ -10,8 +10,9 @@ import pytest
 import torch
 
 from oracle import ref_cpu as ref
+from semblend_amd import rope_correction as rc
 from semblend_amd import triton_kernels as tk
-from tests.helpers import assert_bit_exact, gen, randn
+from tests.helpers import assert_bit_exact, assert_rope_close, gen, randn
 
 pytestmark = pytest.mark.gpu
 
@@ -171,6 +172,47 @@ def test_paged_layers_matches_per_layer(dev, dtype):
                                      dp.to(dev), tp.to(dev))
     for g, w in zip(kvs_dev, want):
         assert_bit_exact(g, w)
+
+
+@pytest.mark.parametrize("rope", [False, True])
+def test_paged_layers_repeated_donor_rows(dev, rope):
+    """Donor rows that feed several targets (chunk deltas whose donor windows overlap): the
+    cached-load policy, the nontemporal one and the automatic choice give the same bits, and
+    every layer meets the oracle (copies bit-exact, rotated K within the RoPE bar)."""
+    L, nb, h, bs, d = 3, 48, 2, 16, 128
+    kvs = [randn((nb, 2, h, bs, d), torch.bfloat16, 300 + i) for i in range(L)]
+    donors = [randn((2, h, 256, d), torch.bfloat16, 310 + i) for i in range(L)]
+    bt = torch.randperm(nb, generator=gen(320))[:40].to(torch.int32)
+    tp = torch.arange(0, 600, dtype=torch.int32)
+    dp = (tp % 200 + 20).to(torch.int32)  # each donor row is read by three targets
+    if rope:
+        want = [ref.rope_correct_scatter_paged(k.clone(), dn, bt, dp, tp, 5e5)
+                for k, dn in zip(kvs, donors)]
+    else:
+        want = [ref.scatter_donor_kv_paged(k.clone(), dn, bt, dp, tp)
+                for k, dn in zip(kvs, donors)]
+    dd = [dn.to(dev) for dn in donors]
+    results = {}
+    for repeated in (False, True, None):
+        got = [k.to(dev) for k in kvs]
+        if rope:
+            call = rc.prepare_scatter_paged_layers(got, dd, bt.to(dev), dp.to(dev),
+                                                   tp.to(dev), 5e5, repeated_donor_rows=repeated)
+            assert (call.args[-1] == 1) == (repeated is not False)
+            call()
+        else:
+            tk.scatter_donor_kv_paged_layers(got, dd, bt.to(dev), dp, tp,
+                                             repeated_donor_rows=repeated)
+        results[repeated] = [g.cpu() for g in got]
+    for repeated in (True, None):
+        for a, b in zip(results[repeated], results[False]):
+            assert_bit_exact(a, b)
+    for g, w in zip(results[False], want):
+        if rope:
+            assert_bit_exact(g[:, 1], w[:, 1])
+            assert_rope_close(g, w)
+        else:
+            assert_bit_exact(g, w)
 
 
 def test_paged_layers_full_size_7b(dev):

@@ -292,6 +292,25 @@ def test_prepare_scatter_paged_layers_host_checks():
         rc.prepare_scatter_paged_layers(kv, donors, bt, d, d)
 
 
+def test_rows_repeat():
+    """The load-policy hint of the multi-layer scatters: a donor row used by two pairs, per
+    donor when donor indices are given; host sequences, numpy and CPU tensors alike."""
+    from semblend_amd import _lib
+    assert not _lib.rows_repeat([3, 1, 2])
+    assert _lib.rows_repeat([3, 1, 3])
+    assert not _lib.rows_repeat([])
+    assert not _lib.rows_repeat(np.array([7]))
+    assert _lib.rows_repeat(np.array([0, 5, 9, 5], dtype=np.int32))
+    assert _lib.rows_repeat(torch.tensor([2, 2], dtype=torch.int32))
+    # the same position of two donors is two rows; of one donor, one row
+    assert not _lib.rows_repeat([4, 4], donor_index=[0, 1])
+    assert _lib.rows_repeat([4, 4, 4], donor_index=[0, 1, 1])
+    # negative positions (skipped pairs) and large positions keep distinct keys
+    assert not _lib.rows_repeat([-1, 2**31 - 1], donor_index=[1, 0])
+    assert _lib.scatter_flags(True) == _lib.SB_SCATTER_REPEATED_DONOR_ROWS == 1
+    assert _lib.scatter_flags(False) == 0
+
+
 def test_pair_length_mismatch_is_rejected_before_launch():
     """A target list shorter than the donor list would make the kernels read past it: every
     scatter entry refuses it with ValueError before looking at the device (CPU tensors here,
