@@ -440,18 +440,31 @@ struct RopeRowsArgs {
   int tpr_log2;
 };
 
-template <int DT, int VB>
-__global__ __launch_bounds__(kThreads) void rope_rows_kernel(RopeRowsArgs a) {
+// The pair-centric form (donor positions distinct) has no multi-pair path (90 VGPRs, 5 waves
+// per SIMD, against 97 and 4 with it). Its knobs: waves per SIMD (1: the compiler's choice)
+// and rows per batch. On the 7B workload (28 x 4 x 8192 rows) the defaults take 86 us; 8 waves
+// 107 us (46 registers spilled), 4-row batches 88 us, 4-row batches at 8 waves 95 us.
+#ifndef SB_ROPE_DISTINCT_WAVES
+#define SB_ROPE_DISTINCT_WAVES 1
+#endif
+#ifndef SB_ROPE_DISTINCT_BATCH
+#define SB_ROPE_DISTINCT_BATCH SB_ROPE_BATCH
+#endif
+template <int DT, int VB, bool INDEXED>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(INDEXED ? 1 : SB_ROPE_DISTINCT_WAVES)))
+void rope_rows_kernel(RopeRowsArgs a) {
   constexpr int W = VB / 4;
   constexpr int E = (DT == SB_DTYPE_F32) ? W : 2 * W;
   constexpr int NP = E / 2;
+  constexpr int kRows = INDEXED ? kRopeBatch : SB_ROPE_DISTINCT_BATCH;
   const int tpr = 1 << a.tpr_log2;
   const int lane = threadIdx.x & (tpr - 1);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * (kThreads >> a.tpr_log2) +
                     (threadIdx.x >> a.tpr_log2);
   int64_t s, first;
   int cnt;
-  if (a.ws) {
+  if (INDEXED) {
     // Row-centric: thread t owns position t; the index names its pairs.
     s = t;
     if (s >= a.seq_len) return;
@@ -482,7 +495,7 @@ __global__ __launch_bounds__(kThreads) void rope_rows_kernel(RopeRowsArgs a) {
     return a.out + l * a.o_s_layer + h * a.o_s_head + s * a.o_s_seq;
   };
 
-  if (cnt > 1) {
+  if (INDEXED && cnt > 1) {
     // Several pairs rotate this row (rare): apply them in pair order, rounding to the tensor
     // dtype after each one, as the reference's sequential loop does. One row at a time.
     for (int j = lane; j < a.vpr; j += tpr) {
@@ -522,13 +535,13 @@ __global__ __launch_bounds__(kThreads) void rope_rows_kernel(RopeRowsArgs a) {
 #pragma unroll
       for (int k = 0; k < NP; ++k) sincos_rn(delta * a.inv_freq[j * NP + k], &sn[k], &c[k]);
     }
-    for (int r0 = r_begin; r0 < r_end; r0 += kRopeBatch) {
-      uint32_t w[kRopeBatch][W];
+    for (int r0 = r_begin; r0 < r_end; r0 += kRows) {
+      uint32_t w[kRows][W];
 #pragma unroll
-      for (int b = 0; b < kRopeBatch; ++b)
+      for (int b = 0; b < kRows; ++b)
         if (r0 + b < r_end) load_vec<VB, true>(k_row(r0 + b) + vofs, w[b]);
 #pragma unroll
-      for (int b = 0; b < kRopeBatch; ++b) {
+      for (int b = 0; b < kRows; ++b) {
         if (r0 + b >= r_end) continue;
         if (cnt == 1) {
           float f[E];
@@ -1040,7 +1053,11 @@ int rope_k_impl(const char* fn, void* out, const void* k, const int32_t* donor_p
   dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
 #define SB_ROWS_CASE(DT, VB)                                                              \
   if (dtype == DT && g.vb == VB) {                                                        \
-    SB_LAUNCH("rope_rows", (rope_rows_kernel<DT, VB>), grid, dim3(kThreads), st, a);    \
+    if (ws)                                                                               \
+      SB_LAUNCH("rope_rows", (rope_rows_kernel<DT, VB, true>), grid, dim3(kThreads), st, a); \
+    else                                                                                  \
+      SB_LAUNCH("rope_rows", (rope_rows_kernel<DT, VB, false>), grid, dim3(kThreads), st,  \
+                a);                                                                       \
     return check_launch(fn);                                                              \
   }
   SB_ROWS_CASE(SB_DTYPE_F32, 16)
