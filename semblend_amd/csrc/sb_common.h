@@ -7,6 +7,7 @@
 #include <string>
 
 #include "../../include/semblend_hip.h"
+#include "sb_sincos.h"
 
 namespace sb {
 
@@ -173,9 +174,11 @@ template <> struct ByteVec<1> { using T = uint8_t; };
 // values a correctly rounded libm returns, which torch's CPU kernels also produce for all but
 // rare arguments. Matching them matters where e*c - o*s cancels: for an output of ~1e-6 from
 // O(1) inputs, a one-ulp difference in cos or sin is several bf16 ulps of the result.
+// x is a RoPE angle (an int32 position or position difference times an inverse frequency
+// <= 1), so |x| < 2^31, the range of sincos_cw.
 __device__ __forceinline__ void sincos_rn(float x, float* s, float* c) {
   double sd, cd;
-  sincos(static_cast<double>(x), &sd, &cd);
+  sincos_cw(static_cast<double>(x), &sd, &cd);
   *s = static_cast<float>(sd);
   *c = static_cast<float>(cd);
 }

@@ -258,11 +258,11 @@ __device__ __forceinline__ void nope_pairs(float* f, const float* cs, const floa
   }
 }
 
-// Waves per SIMD that the delta-rotating movers are compiled for. Left to itself the
-// compiler gives them 74-80 VGPRs (6 waves); capped at 64 (8 waves, a few spilled registers
-// in the once-per-pair cos/sin code) the fused RoPE scatter of Qwen2.5-7B runs 331 -> 288 us
-// and of the Llama-3-8B batch 3.38 -> 2.93 ms. Plain copies already fit 8 waves; the other
-// rotation forms keep the compiler's choice (two cos/sin sets would spill in the row loop).
+// Waves per SIMD that the delta-rotating movers are compiled for. Occupancy decides their
+// speed: with a general-purpose double sincos they took 74-80 VGPRs (6 waves) and the fused
+// RoPE scatter of Qwen2.5-7B ran at 331 us; capped at 64 VGPRs (8 waves, spilling) at 288 us.
+// With sincos_cw the cap costs no spills (45-51 VGPRs; left alone the scheduler takes 58-64)
+// and the scatter takes 272 us. The other rotation forms keep the compiler's choice.
 #ifndef SB_MOVE_ROT_WAVES
 #define SB_MOVE_ROT_WAVES 8
 #endif
