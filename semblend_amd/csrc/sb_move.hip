@@ -61,11 +61,18 @@ enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3 };
 #ifndef SB_MOVE_NT_STORE
 #define SB_MOVE_NT_STORE 1
 #endif
+// Layers per thread of the multi-layer pair movers (with at least 8192 pairs): plain copies,
+// and the K and V planes of rotating launches. On the 7B workload (28 layers, 13926 pairs):
+// plain copies 1 layer 274-276 us, 2 layers 280-281; the V plane of the rotating launches
+// 2 layers (four-donor composite 290 us) against 1 (305 us).
 #ifndef SB_SCATTER_LPG
-#define SB_SCATTER_LPG 2
+#define SB_SCATTER_LPG 1
 #endif
 #ifndef SB_ROPE_SCATTER_LPG
 #define SB_ROPE_SCATTER_LPG 8
+#endif
+#ifndef SB_ROPE_V_LPG
+#define SB_ROPE_V_LPG 2
 #endif
 constexpr int kThreads = SB_MOVE_THREADS;
 constexpr int kBatch = SB_MOVE_BATCH;      // pair movers: rows loaded before the first store
@@ -666,24 +673,27 @@ RowSide side_index(void* base, int64_t num_heads, int64_t head_dim, int64_t es, 
   return s;
 }
 
-int layers_per_group_for(int64_t num_layers, int64_t num_pairs, bool rope);
+enum LayerGroupKind { kGroupCopy, kGroupRotK, kGroupRotV };
+int layers_per_group_for(int64_t num_layers, int64_t num_pairs, LayerGroupKind kind);
 
 // Grid slices of a rotating launch over both planes: K in the rotating path's long layer
 // groups (cos/sin once per group), V in the plain copy's short ones (more slices in flight).
 int split_rope_planes(MoveArgs& a, int64_t num_layers, int64_t num_pairs) {
-  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, true);
-  a.v_layers_per_group = layers_per_group_for(num_layers, num_pairs, false);
+  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, kGroupRotK);
+  a.v_layers_per_group = layers_per_group_for(num_layers, num_pairs, kGroupRotV);
   a.k_slices = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
   return a.k_slices +
          static_cast<int>((num_layers + a.v_layers_per_group - 1) / a.v_layers_per_group);
 }
 
-int layers_per_group_for(int64_t num_layers, int64_t num_pairs, bool rope) {
+int layers_per_group_for(int64_t num_layers, int64_t num_pairs, LayerGroupKind kind) {
   // Enough grid.y slices to fill the chip when there are few pairs; otherwise walk several
   // layers per thread so index work (and, when rotating, the fp64 cos/sin) is amortised.
   // Plain copies stay at short groups (more independent slices in flight); the rotating
   // path computes cos/sin once per group, so longer groups pay for themselves there.
-  const int64_t lpg = rope ? SB_ROPE_SCATTER_LPG : SB_SCATTER_LPG;
+  const int64_t lpg = kind == kGroupRotK   ? SB_ROPE_SCATTER_LPG
+                     : kind == kGroupRotV ? SB_ROPE_V_LPG
+                                          : SB_SCATTER_LPG;
   if (num_pairs >= 8192) return static_cast<int>(num_layers < lpg ? num_layers : lpg);
   return 1;
 }
@@ -723,7 +733,7 @@ extern "C" int sb_scatter_donor_kv(void* target, const void* donor, const int32_
   a.num_pairs = num_pairs;
   a.num_heads = static_cast<int>(num_heads);
   a.num_layers = static_cast<int>(num_layers);
-  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, false);
+  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, kGroupCopy);
   a.kv_first = 0;
   a.num_kv = 2;
   const int groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
@@ -775,7 +785,8 @@ static int paged_scatter_impl(const char* fn, void* kv_base, const uint64_t* kv_
   a.num_pairs = num_pairs;
   a.num_heads = static_cast<int>(num_heads);
   a.num_layers = static_cast<int>(num_layers);
-  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, rope);
+  a.layers_per_group =
+      layers_per_group_for(num_layers, num_pairs, rope ? kGroupRotK : kGroupCopy);
   a.kv_first = 0;
   a.num_kv = 2;
   a.cached_loads = (flags & SB_SCATTER_REPEATED_DONOR_ROWS) ? 1 : 0;
@@ -912,7 +923,8 @@ extern "C" int sb_composite_scatter_paged_layers(
   a.num_pairs = num_pairs;
   a.num_heads = static_cast<int>(num_heads);
   a.num_layers = static_cast<int>(num_layers);
-  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, rope);
+  a.layers_per_group =
+      layers_per_group_for(num_layers, num_pairs, rope ? kGroupRotK : kGroupCopy);
   a.kv_first = 0;
   a.num_kv = 2;
   a.cached_loads = (flags & SB_SCATTER_REPEATED_DONOR_ROWS) ? 1 : 0;
