@@ -45,6 +45,7 @@ import os
 import sys
 import time
 
+import numpy as np
 import torch
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, GB/s
@@ -118,11 +119,13 @@ def qwen05b_pipeline_inputs(seed: int = 0) -> dict:
 def delta_groups(deltas: torch.Tensor) -> list[tuple[int, list[int]]]:
     """(delta, positions) for every distinct nonzero per-token delta, in ascending delta
     order: one in-place RoPE call per group."""
-    out = []
-    for dl in torch.unique(deltas).tolist():
-        if dl != 0:
-            out.append((int(dl), (deltas == dl).nonzero().flatten().tolist()))
-    return out
+    d = deltas.numpy()
+    order = np.argsort(d, kind="stable")  # positions stay ascending within a group
+    sd = d[order]
+    bounds = (np.flatnonzero(np.diff(sd)) + 1).tolist()
+    pos, val = order.tolist(), sd.tolist()
+    return [(int(val[s]), pos[s:e]) for s, e in zip([0] + bounds, bounds + [len(pos)])
+            if val[s] != 0]
 
 
 def qwen05b_pipeline(mod_tk, mod_rc, inp: dict, device=None):

@@ -45,6 +45,9 @@ extern "C" {
 #define SB_SCATTER_REPEATED_DONOR_ROWS 1
 #define SB_SCATTER_FLAGS_ALL 1
 
+/* Most positions sb_apply_rope_delta_inplace_host takes (they travel inside the launch). */
+#define SB_INLINE_POSITIONS_MAX 256
+
 /* Library version string, e.g. "semblend_hip 0.1.0 gfx950". */
 const char* sb_version(void);
 
@@ -252,6 +255,22 @@ int sb_apply_rope_delta_inplace(void* k_plane, const int32_t* block_table,
                                 int64_t num_heads, int64_t block_size, int64_t head_dim,
                                 int64_t num_blocks_total, int64_t num_blocks_per_seq,
                                 const int64_t* k_strides, int32_t dtype, void* stream);
+
+/* sb_apply_rope_delta_inplace with positions (and repeat, or NULL) in HOST memory, at most
+ * SB_INLINE_POSITIONS_MAX of them: they are copied into the launch's own argument block, so
+ * a short list needs no device buffer and no host-to-device copy (the per-call cost of the
+ * reference's caller pattern, one call per distinct delta). Same results as
+ * sb_apply_rope_delta_inplace; more positions are rejected with SB_ERR_INVALID_ARGUMENT.
+ * The host arrays may be reused as soon as the call returns.
+ * Replaces semblend_core/rope_correction.py:699-783 (apply_rope_delta_inplace) for short
+ * position lists. */
+int sb_apply_rope_delta_inplace_host(void* k_plane, const int32_t* block_table,
+                                     const int32_t* positions, const int32_t* repeat,
+                                     int64_t num_positions, int64_t delta,
+                                     const float* inv_freq, int64_t num_heads,
+                                     int64_t block_size, int64_t head_dim,
+                                     int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                                     const int64_t* k_strides, int32_t dtype, void* stream);
 
 /* Permutation inside a paged cache with snapshot semantics: every source row (K and V) is
  * read before any target row is written; V is copied, K rotated by (tgt - src).

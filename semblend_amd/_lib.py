@@ -21,6 +21,8 @@ SB_OK = 0
 SB_ERR_INVALID_ARGUMENT = 100001
 # Flag of the multi-layer scatters: a donor row may be the source of several pairs.
 SB_SCATTER_REPEATED_DONOR_ROWS = 1
+# Most positions the in-place delta RoPE takes by value in its launch (host arrays).
+SB_INLINE_POSITIONS_MAX = 256
 SB_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 _vp = ctypes.c_void_p
@@ -28,6 +30,7 @@ _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 _f32 = ctypes.c_float
 _i64p = ctypes.POINTER(ctypes.c_int64)
+_i32p = ctypes.POINTER(ctypes.c_int32)
 
 # Argument signatures of every exported function (order as in include/semblend_hip.h).
 SIGNATURES: dict[str, list] = {
@@ -51,6 +54,8 @@ SIGNATURES: dict[str, list] = {
                                    _i32, _vp],
     "sb_apply_rope_delta_inplace": [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                     _i64, _i64, _i64p, _i32, _vp],
+    "sb_apply_rope_delta_inplace_host": [_vp, _vp, _i32p, _i32p, _i64, _i64, _vp, _i64, _i64,
+                                         _i64, _i64, _i64, _i64p, _i32, _vp],
     "sb_permute_paged_kv_with_rope": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                       _i64, _i64, _i64p, _i32, _vp],
     "sb_nope_permute_paged_kv": [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64,
@@ -173,6 +178,11 @@ def ptr(t: torch.Tensor | None) -> int | None:
 def strides(t: torch.Tensor, dims: tuple[int, ...] | None = None):
     s = t.stride() if dims is None else tuple(t.stride(d) for d in dims)
     return (ctypes.c_int64 * len(s))(*s)
+
+
+def i32_array(values) -> ctypes.Array:
+    """Host int32 array for arguments the library reads on the host."""
+    return (ctypes.c_int32 * len(values))(*values)
 
 
 def i64_array(values) -> ctypes.Array:

@@ -20,6 +20,7 @@
 // elementwise ops.
 
 #include <algorithm>
+#include <cstring>
 
 #include "sb_common.h"
 
@@ -274,9 +275,7 @@ __device__ __forceinline__ void nope_pairs(float* f, const float* cs, const floa
 #define SB_MOVE_ROT_WAVES 8
 #endif
 template <int DT, int VB, int ROT, int SRCM, int DSTM>
-__global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(ROT == ROT_DELTA ? SB_MOVE_ROT_WAVES : 1)))
-void move_rows_kernel(MoveArgs a) {
+__device__ __forceinline__ void move_rows_body(const MoveArgs& a) {
   constexpr int W = VB / 4;
   constexpr int E = (DT == SB_DTYPE_F32) ? W : 2 * W;
   constexpr int NP = E / 2;
@@ -386,6 +385,34 @@ void move_rows_kernel(MoveArgs a) {
       }
     }
   }
+}
+
+template <int DT, int VB, int ROT, int SRCM, int DSTM>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(ROT == ROT_DELTA ? SB_MOVE_ROT_WAVES : 1)))
+void move_rows_kernel(MoveArgs a) {
+  move_rows_body<DT, VB, ROT, SRCM, DSTM>(a);
+}
+
+// In-place RoPE by one delta at positions passed by value in the launch itself (the kernel
+// argument block), so a short host list reaches the kernel without a host-to-device copy.
+// The rows are read through pointers into the argument block.
+constexpr int kInlinePositions = SB_INLINE_POSITIONS_MAX;
+struct InlineIndex {
+  int32_t pos[kInlinePositions];
+  int32_t rep[kInlinePositions];
+  int has_rep;
+};
+static_assert(sizeof(MoveArgs) + sizeof(InlineIndex) <= 4096, "kernel arguments over 4 KB");
+
+template <int DT, int VB>
+__global__ __launch_bounds__(kThreads) void rope_delta_inline_kernel(MoveArgs a0,
+                                                                     InlineIndex ix) {
+  MoveArgs a = a0;
+  a.src_pos = ix.pos;
+  a.dst_pos = ix.pos;
+  a.repeat = ix.has_rep ? ix.rep : nullptr;
+  move_rows_body<DT, VB, ROT_CONST, ROW_PAGED_POS, ROW_PAGED_POS>(a);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -624,6 +651,31 @@ int launch_move(const char* fn, const MoveArgs& a0, int32_t dtype, const Geometr
     SB_MOVE_CASE(SB_DTYPE_F16, 4)
   }
 #undef SB_MOVE_CASE
+  return fail(fn, "unsupported dtype / vector width combination");
+}
+
+int launch_rope_delta_inline(const char* fn, const MoveArgs& a0, const InlineIndex& ix,
+                             int32_t dtype, const Geometry& g, hipStream_t stream) {
+  MoveArgs a = a0;
+  a.vpr = g.vpr;
+  a.tpr_log2 = g.tpr_log2;
+  const int64_t rows_per_block = kThreads >> g.tpr_log2;
+  dim3 grid(static_cast<unsigned>((a.num_pairs + rows_per_block - 1) / rows_per_block));
+#define SB_INLINE_CASE(DT, VB)                                                            \
+  if (dtype == DT && g.vb == VB) {                                                        \
+    SB_LAUNCH("move_rows", (rope_delta_inline_kernel<DT, VB>), grid, dim3(kThreads),     \
+              stream, a, ix);                                                             \
+    return check_launch(fn);                                                              \
+  }
+  SB_INLINE_CASE(SB_DTYPE_F32, 16)
+  SB_INLINE_CASE(SB_DTYPE_F32, 8)
+  SB_INLINE_CASE(SB_DTYPE_BF16, 16)
+  SB_INLINE_CASE(SB_DTYPE_BF16, 8)
+  SB_INLINE_CASE(SB_DTYPE_BF16, 4)
+  SB_INLINE_CASE(SB_DTYPE_F16, 16)
+  SB_INLINE_CASE(SB_DTYPE_F16, 8)
+  SB_INLINE_CASE(SB_DTYPE_F16, 4)
+#undef SB_INLINE_CASE
   return fail(fn, "unsupported dtype / vector width combination");
 }
 
@@ -1086,37 +1138,30 @@ int rope_k_impl(const char* fn, void* out, const void* k, const int32_t* donor_p
 }  // namespace
 }  // namespace sb
 
-extern "C" int sb_apply_rope_delta_inplace(void* k_plane, const int32_t* block_table,
-                                           const int32_t* positions, const int32_t* repeat,
-                                           int64_t num_positions, int64_t delta,
-                                           const float* inv_freq, int64_t num_heads,
-                                           int64_t block_size, int64_t head_dim,
-                                           int64_t num_blocks_total,
-                                           int64_t num_blocks_per_seq, const int64_t* ks,
-                                           int32_t dtype, void* stream) {
-  const char* fn = "sb_apply_rope_delta_inplace";
-  clear_error();
-  if (num_positions == 0 || num_heads == 0 || head_dim == 0 || delta == 0) return SB_OK;
+namespace sb {
+namespace {
+// Checks and launch arguments shared by the two in-place delta RoPE entries; positions and
+// repeat are filled in by the caller.
+int rope_delta_setup(const char* fn, void* k_plane, const int32_t* block_table,
+                     int64_t num_positions, int64_t delta, const float* inv_freq,
+                     int64_t num_heads, int64_t block_size, int64_t head_dim,
+                     int64_t num_blocks_total, int64_t num_blocks_per_seq, const int64_t* ks,
+                     int32_t dtype, MoveArgs* out, Geometry* g) {
   if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
-  if (!k_plane || !block_table || !positions || !inv_freq || !ks)
-    return fail(fn, "null pointer argument");
+  if (!k_plane || !block_table || !inv_freq || !ks) return fail(fn, "null pointer argument");
   if ((head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
   if (block_size <= 0) return fail(fn, "block_size must be positive");
   if (ks[3] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
   const int64_t es = elem_size(dtype);
-  Geometry g;
   if (!make_geometry(head_dim, es,
                      {reinterpret_cast<int64_t>(k_plane), ks[0] * es, ks[1] * es, ks[2] * es},
-                     true, &g))
+                     true, g))
     return fail(fn, "rows are not aligned for vector access");
   // k_strides = (block, head, pos, dim); expressed as a paged side with a single kv plane.
   const int64_t st5[5] = {ks[0], 0, ks[1], ks[2], ks[3]};
   MoveArgs a{};
   a.src = side_paged(k_plane, nullptr, st5, es);
   a.dst = a.src;
-  a.src_pos = positions;
-  a.dst_pos = positions;
-  a.repeat = repeat;
   a.block_table = block_table;
   a.block_size = block_size;
   a.nb_total = num_blocks_total;
@@ -1129,8 +1174,65 @@ extern "C" int sb_apply_rope_delta_inplace(void* k_plane, const int32_t* block_t
   a.layers_per_group = 1;
   a.kv_first = 0;
   a.num_kv = 1;
+  *out = a;
+  return SB_OK;
+}
+}  // namespace
+}  // namespace sb
+
+extern "C" int sb_apply_rope_delta_inplace(void* k_plane, const int32_t* block_table,
+                                           const int32_t* positions, const int32_t* repeat,
+                                           int64_t num_positions, int64_t delta,
+                                           const float* inv_freq, int64_t num_heads,
+                                           int64_t block_size, int64_t head_dim,
+                                           int64_t num_blocks_total,
+                                           int64_t num_blocks_per_seq, const int64_t* ks,
+                                           int32_t dtype, void* stream) {
+  const char* fn = "sb_apply_rope_delta_inplace";
+  clear_error();
+  if (num_positions == 0 || num_heads == 0 || head_dim == 0 || delta == 0) return SB_OK;
+  if (!positions) return fail(fn, "null pointer argument");
+  MoveArgs a;
+  Geometry g;
+  const int rc = rope_delta_setup(fn, k_plane, block_table, num_positions, delta, inv_freq,
+                                  num_heads, block_size, head_dim, num_blocks_total,
+                                  num_blocks_per_seq, ks, dtype, &a, &g);
+  if (rc) return rc;
+  a.src_pos = positions;
+  a.dst_pos = positions;
+  a.repeat = repeat;
   return launch_move<ROT_CONST, ROW_PAGED_POS, ROW_PAGED_POS>(fn, a, dtype, g, 1,
                                                               static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sb_apply_rope_delta_inplace_host(void* k_plane, const int32_t* block_table,
+                                                const int32_t* positions,
+                                                const int32_t* repeat, int64_t num_positions,
+                                                int64_t delta, const float* inv_freq,
+                                                int64_t num_heads, int64_t block_size,
+                                                int64_t head_dim, int64_t num_blocks_total,
+                                                int64_t num_blocks_per_seq, const int64_t* ks,
+                                                int32_t dtype, void* stream) {
+  const char* fn = "sb_apply_rope_delta_inplace_host";
+  clear_error();
+  if (num_positions == 0 || num_heads == 0 || head_dim == 0 || delta == 0) return SB_OK;
+  if (!positions) return fail(fn, "null pointer argument");
+  if (num_positions < 0 || num_positions > kInlinePositions)
+    return fail(fn, "more positions than SB_INLINE_POSITIONS_MAX");
+  MoveArgs a;
+  Geometry g;
+  const int rc = rope_delta_setup(fn, k_plane, block_table, num_positions, delta, inv_freq,
+                                  num_heads, block_size, head_dim, num_blocks_total,
+                                  num_blocks_per_seq, ks, dtype, &a, &g);
+  if (rc) return rc;
+  InlineIndex ix;
+  std::memset(&ix, 0, sizeof(ix));
+  std::memcpy(ix.pos, positions, static_cast<size_t>(num_positions) * sizeof(int32_t));
+  if (repeat) {
+    std::memcpy(ix.rep, repeat, static_cast<size_t>(num_positions) * sizeof(int32_t));
+    ix.has_rep = 1;
+  }
+  return launch_rope_delta_inline(fn, a, ix, dtype, g, static_cast<hipStream_t>(stream));
 }
 
 namespace sb {

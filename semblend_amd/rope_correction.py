@@ -474,36 +474,40 @@ def apply_rope_delta_inplace(
     if delta == 0 or not positions:
         return 0
     dev = _lib.require_device(kv_cache)
-    is_vllm_layout = kv_cache.shape[0] == 2 and (kv_cache.ndim == 5 and kv_cache.shape[1] != 2)
-    if is_vllm_layout:
-        head_dim = kv_cache.shape[4]
-        block_size = kv_cache.shape[2]
-        num_heads = kv_cache.shape[3]
-        nb_total = kv_cache.shape[1]
-        k_plane = kv_cache[0]                     # [NB, bs, H, D]
-        kst = (k_plane.stride(0), k_plane.stride(2), k_plane.stride(1), k_plane.stride(3))
-    else:
-        head_dim = kv_cache.shape[4]
-        block_size = kv_cache.shape[3]
-        num_heads = kv_cache.shape[2]
-        nb_total = kv_cache.shape[0]
-        k_plane = kv_cache[:, 0]                  # [NB, H, bs, D]
-        kst = (k_plane.stride(0), k_plane.stride(1), k_plane.stride(2), k_plane.stride(3))
+    shape, st = kv_cache.shape, kv_cache.stride()
+    # The K plane starts at the tensor's own address in both layouts (kv index 0); strides
+    # (block, head, pos, dim) are read off the full tensor, so no view is made.
+    if kv_cache.ndim == 5 and shape[0] == 2 and shape[1] != 2:  # vLLM [2, NB, bs, H, D]
+        nb_total, block_size, num_heads, head_dim = shape[1], shape[2], shape[3], shape[4]
+        kst = (st[1], st[3], st[2], st[4])
+    else:                                                        # [NB, 2, H, bs, D]
+        nb_total, num_heads, block_size, head_dim = shape[0], shape[2], shape[3], shape[4]
+        kst = (st[0], st[2], st[3], st[4])
     _check_head_dim(head_dim, head_dim, "apply_rope_delta_inplace")
     nbs = block_table.shape[0]
     counts, modified = _rotation_counts(positions, block_size, nbs)
     if not counts:
         return 0
-    pos_t = _lib.upload_index(torch.tensor(list(counts.keys()), dtype=torch.int32), dev)
-    rep_t = None
-    if any(c != 1 for c in counts.values()):
-        rep_t = _lib.upload_index(torch.tensor(list(counts.values()), dtype=torch.int32), dev)
     bt = _lib.as_index(block_table, dev)
     inv_freq = inv_freq_table(rope_base, head_dim, dev)
+    reps = list(counts.values())
+    repeated = any(c != 1 for c in reps)
     with torch.cuda.device(dev):
+        if len(counts) <= _lib.SB_INLINE_POSITIONS_MAX:
+            # Short lists travel inside the launch: no index upload.
+            _lib.call(
+                "sb_apply_rope_delta_inplace_host",
+                kv_cache.data_ptr(), bt.data_ptr(), _lib.i32_array(list(counts.keys())),
+                _lib.i32_array(reps) if repeated else None, len(counts), int(delta),
+                inv_freq.data_ptr(), num_heads, block_size, head_dim, nb_total, nbs,
+                _lib.i64_array(kst), _lib.dtype_code(kv_cache), _lib.stream_handle(dev),
+            )
+            return modified
+        pos_t = _lib.upload_index(torch.tensor(list(counts.keys()), dtype=torch.int32), dev)
+        rep_t = _lib.upload_index(torch.tensor(reps, dtype=torch.int32), dev) if repeated else None
         _lib.call(
             "sb_apply_rope_delta_inplace",
-            k_plane.data_ptr(), bt.data_ptr(), pos_t.data_ptr(),
+            kv_cache.data_ptr(), bt.data_ptr(), pos_t.data_ptr(),
             None if rep_t is None else rep_t.data_ptr(), len(counts), int(delta),
             inv_freq.data_ptr(), num_heads, block_size, head_dim, nb_total, nbs,
             _lib.i64_array(kst), _lib.dtype_code(kv_cache), _lib.stream_handle(dev),

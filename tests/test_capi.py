@@ -81,6 +81,12 @@ def test_invalid_arguments_are_rejected_without_launch():
                                           0.1, _i64(1, 1, 1), _i64(1, 1, 1), _i64(1, 1, 1),
                                           _i64(1, 1, 1), 2, None)
     assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"workspace" in lib.sb_last_error_string()
+    # more host positions than the launch carries
+    many = (ctypes.c_int32 * 257)()
+    rc = lib.sb_apply_rope_delta_inplace_host(fake, fake, many, None, 257, 5, fake, 1, 16, 8,
+                                              4, 1, _i64(1, 1, 1, 1), 2, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT
+    assert b"SB_INLINE_POSITIONS_MAX" in lib.sb_last_error_string()
     # unknown scatter flags (bit 0 is the only one defined)
     rc = lib.sb_scatter_donor_kv_paged_layers(fake, fake, 2, fake, fake, fake, 4, 1, 16, 8, 4,
                                               4, 1, st, _i64(1, 1, 1, 1), 2, 2, None)

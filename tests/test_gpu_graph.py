@@ -102,6 +102,31 @@ def test_graph_rope_inplace(dev):
         assert torch.equal(k.view(torch.int16), want.view(torch.int16))
 
 
+@pytest.mark.parametrize("layout", ["standard", "vllm"])
+def test_graph_apply_rope_delta_short_list(dev, layout):
+    """apply_rope_delta_inplace with a short position list passes the positions inside the
+    launch (no upload), so the call can be captured; every replay of the in-place rotation
+    (from the same starting cache) equals the eager call."""
+    nb, h, bs, d = 24, 2, 16, 64
+    shape = (nb, 2, h, bs, d) if layout == "standard" else (2, nb, bs, h, d)
+    kv0 = randn(shape, torch.bfloat16, 30).to(dev)
+    bt = torch.randperm(nb, generator=gen(31))[:16].to(torch.int32).to(dev)
+    pos = torch.randperm(256, generator=gen(32))[:40].tolist() + [7, 7, 200]
+    kv = kv0.clone()
+    rc.apply_rope_delta_inplace(kv, bt, pos, 37, rope_base=1e6)
+    torch.cuda.synchronize()
+    want = kv.clone()
+    kv.copy_(kv0)
+    g = _capture(lambda: rc.apply_rope_delta_inplace(kv, bt, pos, 37, rope_base=1e6))
+    for _ in range(3):
+        kv.copy_(kv0)
+        _noise(dev)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(kv.view(torch.int16), want.view(torch.int16))
+
+
 @pytest.mark.parametrize("nope", [False, True])
 def test_graph_prepared_permute_layers(dev, nope):
     """The prepared multi-layer permutation (the RoPE hook's per-request call) replays the

@@ -251,6 +251,64 @@ def test_apply_rope_delta_inplace(dev, dtype, layout):
     assert rc.apply_rope_delta_inplace(kd, bt.to(dev), [], 5) == 0
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("layout", ["standard", "vllm"])
+@pytest.mark.parametrize("n", [7, 256, 400])
+def test_apply_rope_delta_host_and_device_positions(dev, dtype, layout, n):
+    """The two C entries behind apply_rope_delta_inplace: positions by value in the launch
+    (host arrays, at most SB_INLINE_POSITIONS_MAX) and positions in device memory give the
+    same bits, with and without repeats; the Python function picks the first for short lists
+    and the second for longer ones (n = 300), and both meet the oracle."""
+    from semblend_amd import _lib
+    nb, h, bs, d = 40, 2, 16, 64
+    shape = (nb, 2, h, bs, d) if layout == "standard" else (2, nb, bs, h, d)
+    kv = randn(shape, dtype, 70 + n)
+    bt = torch.randperm(nb, generator=gen(71))[:32].to(torch.int32)
+    g = gen(72 + n)
+    pos = torch.randperm(32 * bs, generator=g)[:n].tolist()
+    if n != 256:  # 256: exactly the most positions one launch carries, no repeats
+        q = max(n // 4, 1)
+        pos[:q] = pos[q: 2 * q]  # repeats
+    want = kv.clone()
+    n_ref = ref.apply_rope_delta_inplace(want, bt, pos, -45, rope_base=1e6)
+    got = kv.to(dev)
+    assert rc.apply_rope_delta_inplace(got, bt.to(dev), pos, -45, rope_base=1e6) == n_ref
+    assert_bit_exact(got[:, 1] if layout == "standard" else got[1],
+                     want[:, 1] if layout == "standard" else want[1])
+    assert_rope_close(got, want)
+    counts, _ = rc._rotation_counts(pos, bs, bt.shape[0])
+    keys, reps = list(counts.keys()), list(counts.values())
+    if len(keys) > _lib.SB_INLINE_POSITIONS_MAX:
+        with pytest.raises(RuntimeError, match="SB_INLINE_POSITIONS_MAX"):
+            _lib.call("sb_apply_rope_delta_inplace_host", got.data_ptr(), 0,
+                      _lib.i32_array(keys), None, len(keys), 1, 0, h, bs, d, nb, 32,
+                      _lib.i64_array([1, 1, 1, 1]), _lib.dtype_code(got), 0)
+        return
+    st = got.stride()
+    kst = (st[0], st[2], st[3], st[4]) if layout == "standard" else (st[1], st[3], st[2], st[4])
+    inv = rc.inv_freq_table(1e6, d, dev)
+    btd = bt.to(dev)
+    results = []
+    for host in (True, False):
+        for with_rep in (True, False):
+            x = kv.to(dev)
+            args_tail = (len(keys), -45, inv.data_ptr(), h, bs, d, nb, 32, _lib.i64_array(kst),
+                         _lib.dtype_code(x), _lib.stream_handle(dev))
+            if host:
+                _lib.call("sb_apply_rope_delta_inplace_host", x.data_ptr(), btd.data_ptr(),
+                          _lib.i32_array(keys), _lib.i32_array(reps) if with_rep else None,
+                          *args_tail)
+            else:
+                kd = torch.tensor(keys, dtype=torch.int32, device=dev)
+                rd = torch.tensor(reps, dtype=torch.int32, device=dev)
+                _lib.call("sb_apply_rope_delta_inplace", x.data_ptr(), btd.data_ptr(),
+                          kd.data_ptr(), rd.data_ptr() if with_rep else None, *args_tail)
+            results.append(x.cpu())
+    assert_bit_exact(results[0], results[2])  # with repeats: host == device positions
+    assert_bit_exact(results[1], results[3])  # once each
+    assert_bit_exact(results[0], got)
+
+
 def test_apply_rope_delta_round_trip(dev):
     """Δ then -Δ is the identity up to rounding (semblend_connector.py:609-616 relies on it)."""
     kv = randn((8, 2, 4, 16, 64), torch.float32, 52)
