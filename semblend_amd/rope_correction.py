@@ -186,8 +186,8 @@ def prepare_scatter_paged_layers(
     chunks whose deltas make their donor windows overlap). The launch then reads donors
     through the caches, which serves the repeats from L2 / Infinity Cache; otherwise it reads
     them with nontemporal loads, faster when each donor row is read once. None finds out
-    from the positions (one device-to-host read for device positions, here only). Results
-    are the same either way."""
+    from the positions (one device-to-host read for device positions, here only; under HIP
+    graph capture device positions count as distinct). Results are the same either way."""
     if len(kv_caches) != len(donor_kvs):
         raise ValueError("kv_caches and donor_kvs must have the same length")
     num_pairs = len(donor_positions)
@@ -206,7 +206,9 @@ def prepare_scatter_paged_layers(
     if dref.dtype != ref.dtype:
         raise TypeError("donor_kvs and kv_caches must share a dtype")
     if repeated_donor_rows is None:
-        repeated_donor_rows = _lib.rows_repeat(donor_positions, sync=True)
+        # one device-to-host read for device positions, except under graph capture
+        repeated_donor_rows = _lib.rows_repeat(
+            donor_positions, sync=not torch.cuda.is_current_stream_capturing())
     kv_tab = _layer_table(kv_caches, dev)
     d_tab = _layer_table(donor_kvs, dev)
     bt = _lib.as_index(block_table, dev)

@@ -102,6 +102,37 @@ def test_graph_rope_inplace(dev):
         assert torch.equal(k.view(torch.int16), want.view(torch.int16))
 
 
+def test_graph_prepare_scatter_inside_capture(dev):
+    """A multi-layer RoPE scatter prepared while the stream is capturing (no eager warm-up
+    of this call): preparation reads nothing back from the device then (the load policy
+    takes device positions as distinct), and every replay equals the eager launch."""
+    L, nb, h, bs, d = 3, 48, 2, 16, 128
+    caches0 = [randn((nb, 2, h, bs, d), torch.bfloat16, 40 + i).to(dev) for i in range(L)]
+    donors = [randn((2, h, 512, d), torch.bfloat16, 50 + i).to(dev) for i in range(L)]
+    bt = torch.randperm(nb, generator=gen(60))[:40].to(torch.int32).to(dev)
+    tp = torch.arange(0, 600, dtype=torch.int32, device=dev)
+    dp = (tp % 300 + 10).to(torch.int32)  # donor rows repeat
+    rc.inv_freq_table(5e5, d, dev)  # the table exists before capture, as after any warm-up
+    want = [c.clone() for c in caches0]
+    rc.prepare_scatter_paged_layers(want, donors, bt, dp, tp, 5e5)()
+    caches = [c.clone() for c in caches0]
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call = rc.prepare_scatter_paged_layers(caches, donors, bt, dp, tp, 5e5)
+        call()
+    assert call.args[-1] == 0  # distinct assumed under capture
+    for _ in range(3):
+        for c, c0 in zip(caches, caches0):
+            c.copy_(c0)
+        _noise(dev)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for c, w in zip(caches, want):
+            assert torch.equal(c.view(torch.int16), w.view(torch.int16))
+
+
 @pytest.mark.parametrize("layout", ["standard", "vllm"])
 def test_graph_apply_rope_delta_short_list(dev, layout):
     """apply_rope_delta_inplace with a short position list passes the positions inside the
