@@ -57,6 +57,12 @@ constexpr int kWaveRows = 32;   // flattened query rows per MFMA row group
 #ifndef SB_ATTN_PV_PRIO
 #define SB_ATTN_PV_PRIO 1
 #endif
+// Score-to-P work of the QK block skewed over the MFMA steps (fma one step ahead, packing one
+// step behind the exp2), or (0) each pair's dependent chain within its own step. Skewed:
+// 350.6 / 351.9 us against 354.8 / 358.9 on the 7B workload (alternating runs, one box).
+#ifndef SB_ATTN_VALU_SKEW
+#define SB_ATTN_VALU_SKEW 1
+#endif
 // LDS fragment reads issued ahead of the MFMA that consumes them, through rings of kRing
 // fragments (a power of two above kFragAhead).
 #ifndef SB_ATTN_FRAG_AHEAD
@@ -683,6 +689,26 @@ attn_mfma_kernel(const AttnBatch batch) {
       for (int n = 0; n < kFragAhead; ++n) ring[n] = kfrag(ks, n);
       uint32_t pw[RG][kHalves][2][4];  // P words: [group][half][8-element pack][word]
       float acc[RG][kHalves][2];
+#if SB_ATTN_VALU_SKEW
+      // element e (0, 1) of P pair q
+      auto s_at = [&](int q, int e) -> float {
+        const int g = q / (kHalves * 8), r = q % (kHalves * 8);
+        return s_cur[g][r / 8][8 * ((r / 4) % 2) + 2 * (r % 4) + e];
+      };
+      auto pack_pair = [&](int q, float e0, float e1) {
+        const int g = q / (kHalves * 8), r = q % (kHalves * 8);
+        const int hj = r / 8, h = (r / 4) % 2, w = r % 4;
+        const auto pr = M::cvt2(e0, e1);
+        pw[g][hj][h][w] = __builtin_bit_cast(uint32_t, pr);
+        acc[g][hj][h] = M::sum2(pr, w == 0 ? 0.f : acc[g][hj][h]);
+      };
+      float fa0[NPAIR], fa1[NPAIR], ea0[NPAIR], ea1[NPAIR];
+#pragma unroll
+      for (int q = 0; q < PPS; ++q) {
+        fa0[q] = __builtin_fmaf(c_log2, s_at(q, 0), negm[q / (kHalves * 8)]);
+        fa1[q] = __builtin_fmaf(c_log2, s_at(q, 1), negm[q / (kHalves * 8)]);
+      }
+#endif
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int n = 0; n < NQ; ++n) {
@@ -692,6 +718,22 @@ attn_mfma_kernel(const AttnBatch batch) {
         for (int g = 0; g < RG; ++g)
           s_nxt[g][j] =
               M::mma(ring[n % kRing], qf[g][n / kHalves], n < kHalves ? f32x16_t{} : s_nxt[g][j]);
+#if SB_ATTN_VALU_SKEW
+        // Three-stage VALU pipeline over the pairs: the fmas of pair n + 1, the exp2 of pair
+        // n and the packing and sum of pair n - 1 share step n, so no instruction of a step
+        // waits for another of the same step.
+#pragma unroll
+        for (int pp = 0; pp < PPS; ++pp) {
+          const int q = n * PPS + pp;
+          if (q + PPS < NPAIR) {
+            fa0[q + PPS] = __builtin_fmaf(c_log2, s_at(q + PPS, 0), negm[(q + PPS) / (kHalves * 8)]);
+            fa1[q + PPS] = __builtin_fmaf(c_log2, s_at(q + PPS, 1), negm[(q + PPS) / (kHalves * 8)]);
+          }
+          ea0[q] = __builtin_amdgcn_exp2f(fa0[q]);
+          ea1[q] = __builtin_amdgcn_exp2f(fa1[q]);
+          if (q >= PPS) pack_pair(q - PPS, ea0[q - PPS], ea1[q - PPS]);
+        }
+#else
 #pragma unroll
         for (int pp = 0; pp < PPS; ++pp) {
           const int q = n * PPS + pp;
@@ -705,8 +747,13 @@ attn_mfma_kernel(const AttnBatch batch) {
           pw[g][hj][h][w] = __builtin_bit_cast(uint32_t, pr);
           acc[g][hj][h] = M::sum2(pr, w == 0 ? 0.f : acc[g][hj][h]);
         }
+#endif
         __builtin_amdgcn_sched_barrier(0);
       }
+#if SB_ATTN_VALU_SKEW
+#pragma unroll
+      for (int q = NPAIR - PPS; q < NPAIR; ++q) pack_pair(q, ea0[q], ea1[q]);
+#endif
 #pragma unroll
       for (int g = 0; g < RG; ++g) {
         float t = 0.f;
