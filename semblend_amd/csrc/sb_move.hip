@@ -266,6 +266,18 @@ __device__ __forceinline__ void nope_pairs(float* f, const float* cs, const floa
   }
 }
 
+// In-place RoPE by one delta at positions passed by value in the launch itself (the kernel
+// argument block), so a short host list reaches the kernel without a host-to-device copy.
+// Other launches pass the empty InlineArg<false>.
+constexpr int kInlinePositions = SB_INLINE_POSITIONS_MAX;
+template <bool INLINE> struct InlineArg {};
+template <> struct InlineArg<true> {
+  int32_t pos[kInlinePositions];
+  int32_t rep[kInlinePositions];
+  int has_rep;
+};
+static_assert(sizeof(MoveArgs) + sizeof(InlineArg<true>) <= 4096, "kernel arguments over 4 KB");
+
 // Waves per SIMD that the delta-rotating movers are compiled for. Occupancy decides their
 // speed: with a general-purpose double sincos they took 74-80 VGPRs (6 waves) and the fused
 // RoPE scatter of Qwen2.5-7B ran at 331 us; capped at 64 VGPRs (8 waves, spilling) at 288 us.
@@ -274,8 +286,10 @@ __device__ __forceinline__ void nope_pairs(float* f, const float* cs, const floa
 #ifndef SB_MOVE_ROT_WAVES
 #define SB_MOVE_ROT_WAVES 8
 #endif
-template <int DT, int VB, int ROT, int SRCM, int DSTM>
-__device__ __forceinline__ void move_rows_body(const MoveArgs& a) {
+template <int DT, int VB, int ROT, int SRCM, int DSTM, bool INLINE>
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(ROT == ROT_DELTA ? SB_MOVE_ROT_WAVES : 1)))
+void move_rows_kernel(MoveArgs a, InlineArg<INLINE> ix) {
   constexpr int W = VB / 4;
   constexpr int E = (DT == SB_DTYPE_F32) ? W : 2 * W;
   constexpr int NP = E / 2;
@@ -285,6 +299,17 @@ __device__ __forceinline__ void move_rows_body(const MoveArgs& a) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * (kThreads >> a.tpr_log2) +
                     (threadIdx.x >> a.tpr_log2);
   if (i >= a.num_pairs) return;
+  // Positions (and repeat counts) from device arrays, or from the launch's own argument block.
+  // Read through local pointers: the argument `a` is only ever read member by member, which
+  // keeps its arrays (the donor table) in the argument segment rather than in scratch.
+  const int32_t* src_pos = a.src_pos;
+  const int32_t* dst_pos = a.dst_pos;
+  const int32_t* repeat = a.repeat;
+  if constexpr (INLINE) {
+    src_pos = ix.pos;
+    dst_pos = ix.pos;
+    repeat = ix.has_rep ? ix.rep : nullptr;
+  }
 
   int kv, l0, lpg;
   if (ROT != ROT_NONE && a.k_slices > 0) {
@@ -310,27 +335,27 @@ __device__ __forceinline__ void move_rows_body(const MoveArgs& a) {
     src.s_head = a.donors.s_head[dn];
     // Rows are addressed relative to the donor tensor's first position; the rotation below
     // still uses the pair's sequence positions.
-    const int64_t p = static_cast<int64_t>(a.src_pos[i]) - a.donors.first_pos[dn];
+    const int64_t p = static_cast<int64_t>(src_pos[i]) - a.donors.first_pos[dn];
     if (p < 0 || p >= a.donors.bound[dn]) return;
     src_off = p * a.donors.s_seq[dn];
-  } else if (!resolve_row<SRCM>(a, src, a.src_pos, i, &src_off)) {
+  } else if (!resolve_row<SRCM>(a, src, src_pos, i, &src_off)) {
     return;
   }
-  if (!resolve_row<DSTM>(a, a.dst, a.dst_pos, i, &dst_off)) return;
+  if (!resolve_row<DSTM>(a, a.dst, dst_pos, i, &dst_off)) return;
   if (SRCM == ROW_INDEX && a.src_index_check) {
     int64_t unused;
-    if (!paged_slot(a, a.src_pos[i], 0, 0, &unused)) return;
+    if (!paged_slot(a, src_pos[i], 0, 0, &unused)) return;
   }
   const bool rotate = (ROT != ROT_NONE) && kv == 0;
   int reps = 1;
-  if (ROT == ROT_CONST && a.repeat) reps = a.repeat[i];
+  if (ROT == ROT_CONST && repeat) reps = repeat[i];
 
   float ang_a = 0.f, ang_b = 0.f;  // angle multipliers (fp32, as torch computes them)
-  if (ROT == ROT_DELTA) ang_a = static_cast<float>(a.dst_pos[i] - a.src_pos[i]);
+  if (ROT == ROT_DELTA) ang_a = static_cast<float>(dst_pos[i] - src_pos[i]);
   if (ROT == ROT_CONST) ang_a = static_cast<float>(a.const_delta);
   if (ROT == ROT_NOPE) {
-    ang_a = static_cast<float>(a.src_pos[i]);
-    ang_b = static_cast<float>(a.dst_pos[i]);
+    ang_a = static_cast<float>(src_pos[i]);
+    ang_b = static_cast<float>(dst_pos[i]);
   }
 
   const int nrows = (l1 - l0) * a.num_heads;
@@ -385,34 +410,6 @@ __device__ __forceinline__ void move_rows_body(const MoveArgs& a) {
       }
     }
   }
-}
-
-template <int DT, int VB, int ROT, int SRCM, int DSTM>
-__global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(ROT == ROT_DELTA ? SB_MOVE_ROT_WAVES : 1)))
-void move_rows_kernel(MoveArgs a) {
-  move_rows_body<DT, VB, ROT, SRCM, DSTM>(a);
-}
-
-// In-place RoPE by one delta at positions passed by value in the launch itself (the kernel
-// argument block), so a short host list reaches the kernel without a host-to-device copy.
-// The rows are read through pointers into the argument block.
-constexpr int kInlinePositions = SB_INLINE_POSITIONS_MAX;
-struct InlineIndex {
-  int32_t pos[kInlinePositions];
-  int32_t rep[kInlinePositions];
-  int has_rep;
-};
-static_assert(sizeof(MoveArgs) + sizeof(InlineIndex) <= 4096, "kernel arguments over 4 KB");
-
-template <int DT, int VB>
-__global__ __launch_bounds__(kThreads) void rope_delta_inline_kernel(MoveArgs a0,
-                                                                     InlineIndex ix) {
-  MoveArgs a = a0;
-  a.src_pos = ix.pos;
-  a.dst_pos = ix.pos;
-  a.repeat = ix.has_rep ? ix.rep : nullptr;
-  move_rows_body<DT, VB, ROT_CONST, ROW_PAGED_POS, ROW_PAGED_POS>(a);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -630,8 +627,8 @@ int launch_move(const char* fn, const MoveArgs& a0, int32_t dtype, const Geometr
   dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(grid_y));
 #define SB_MOVE_CASE(DT, VB)                                                              \
   if (dtype == DT && g.vb == VB) {                                                        \
-    SB_LAUNCH("move_rows", (move_rows_kernel<DT, VB, ROT, SRCM, DSTM>), grid,            \
-              dim3(kThreads), stream, a);                                                 \
+    SB_LAUNCH("move_rows", (move_rows_kernel<DT, VB, ROT, SRCM, DSTM, false>), grid,     \
+              dim3(kThreads), stream, a, InlineArg<false>{});                             \
     return check_launch(fn);                                                              \
   }
   if (ROT == ROT_NONE) {
@@ -654,7 +651,7 @@ int launch_move(const char* fn, const MoveArgs& a0, int32_t dtype, const Geometr
   return fail(fn, "unsupported dtype / vector width combination");
 }
 
-int launch_rope_delta_inline(const char* fn, const MoveArgs& a0, const InlineIndex& ix,
+int launch_rope_delta_inline(const char* fn, const MoveArgs& a0, const InlineArg<true>& ix,
                              int32_t dtype, const Geometry& g, hipStream_t stream) {
   MoveArgs a = a0;
   a.vpr = g.vpr;
@@ -663,8 +660,9 @@ int launch_rope_delta_inline(const char* fn, const MoveArgs& a0, const InlineInd
   dim3 grid(static_cast<unsigned>((a.num_pairs + rows_per_block - 1) / rows_per_block));
 #define SB_INLINE_CASE(DT, VB)                                                            \
   if (dtype == DT && g.vb == VB) {                                                        \
-    SB_LAUNCH("move_rows", (rope_delta_inline_kernel<DT, VB>), grid, dim3(kThreads),     \
-              stream, a, ix);                                                             \
+    SB_LAUNCH("move_rows",                                                                \
+              (move_rows_kernel<DT, VB, ROT_CONST, ROW_PAGED_POS, ROW_PAGED_POS, true>), grid, \
+              dim3(kThreads), stream, a, ix);                                             \
     return check_launch(fn);                                                              \
   }
   SB_INLINE_CASE(SB_DTYPE_F32, 16)
@@ -1225,7 +1223,7 @@ extern "C" int sb_apply_rope_delta_inplace_host(void* k_plane, const int32_t* bl
                                   num_heads, block_size, head_dim, num_blocks_total,
                                   num_blocks_per_seq, ks, dtype, &a, &g);
   if (rc) return rc;
-  InlineIndex ix;
+  InlineArg<true> ix;
   std::memset(&ix, 0, sizeof(ix));
   std::memcpy(ix.pos, positions, static_cast<size_t>(num_positions) * sizeof(int32_t));
   if (repeat) {

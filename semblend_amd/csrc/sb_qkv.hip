@@ -518,16 +518,17 @@ int qkv_common(const char* fn, QkvArgs* a, const void* hidden, const void* weigh
   return SB_OK;
 }
 
-// Tile shape. 256 features x 64 BJ rows (one workgroup per CU) with BJ in {4, 3, 2} chosen to
+// Tile shape. 256 features x 64 BJ rows (one workgroup per CU) with BJ in {3, 2} chosen to
 // minimise the work of the busiest CU, rounds x BJ (ties: larger tiles); 128 x 128 (two per
-// CU) when even BJ = 2 leaves more than half the CUs without a tile.
+// CU) when even BJ = 2 leaves more than half the CUs without a tile. (BJ = 4 spilled 5-6
+// VGPRs and never cost less than BJ = 2 in this model: at most a tie.)
 constexpr int64_t kCus = 256;
 template <int MODE>
 int launch_qkv(const char* fn, const QkvArgs& a, int32_t dtype, hipStream_t st) {
   const int64_t nft = (a.num_features + 255) / 256;
   int bj = 0;
   int64_t best = 0, tiles = 0;
-  for (int c = 4; c >= 2; --c) {
+  for (int c = 3; c >= 2; --c) {
     const int64_t t = nft * ((a.num_rows + 64 * c - 1) / (64 * c));
     const int64_t cost = ((t + kCus - 1) / kCus) * c;
     if (bj == 0 || cost < best) {
@@ -546,7 +547,6 @@ int launch_qkv(const char* fn, const QkvArgs& a, int32_t dtype, hipStream_t st) 
   SB_LAUNCH("qkv_mfma", (qkv_mfma_kernel<DT, MODE, BI, BJ>), grid, dim3(kQThreads), st, a)
 #define SB_QKV_DT(DT)                   \
   switch (bj) {                         \
-    case 4: SB_QKV_CASE(DT, 4, 4); break; \
     case 3: SB_QKV_CASE(DT, 4, 3); break; \
     case 2: SB_QKV_CASE(DT, 4, 2); break; \
     default: SB_QKV_CASE(DT, 2, 2); break; \
