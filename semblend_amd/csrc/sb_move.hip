@@ -471,10 +471,11 @@ struct RopeRowsArgs {
   int tpr_log2;
 };
 
-// The pair-centric form (donor positions distinct) has no multi-pair path (90 VGPRs, 5 waves
-// per SIMD, against 97 and 4 with it). Its knobs: waves per SIMD (1: the compiler's choice)
-// and rows per batch. On the 7B workload (28 x 4 x 8192 rows) the defaults take 86 us; 8 waves
-// 107 us (46 registers spilled), 4-row batches 88 us, 4-row batches at 8 waves 95 us.
+// The pair-centric form (donor positions distinct) has no multi-pair path. Its knobs: waves
+// per SIMD (1: the compiler's choice, 67 VGPRs and 7 waves with sincos_cw) and rows per batch.
+// On the 7B workload (28 x 4 x 8192 rows) the defaults take 85-86 us; 8 waves 86 us (61
+// VGPRs), 4-row batches at 8 waves 91 us. (With the general-purpose double sincos it held
+// 90 VGPRs, and 8 waves spilled 46 registers: 107 us.)
 #ifndef SB_ROPE_DISTINCT_WAVES
 #define SB_ROPE_DISTINCT_WAVES 1
 #endif
