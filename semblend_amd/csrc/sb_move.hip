@@ -62,18 +62,21 @@ enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3 };
 #ifndef SB_MOVE_NT_STORE
 #define SB_MOVE_NT_STORE 1
 #endif
-// Layers per thread of the multi-layer pair movers (with at least 8192 pairs): plain copies,
-// and the K and V planes of rotating launches. On the 7B workload (28 layers, 13926 pairs):
-// plain copies 1 layer 274-276 us, 2 layers 280-281; the V plane of the rotating launches
-// 2 layers (four-donor composite 290 us) against 1 (305 us).
+// Layers per thread of the pair movers (with at least 8192 pairs). Multi-layer paged launches
+// slice the K plane and the V plane separately (grid.y): K in groups of SB_K_PLANE_LPG layers
+// (a rotating launch evaluates cos/sin once per group), V in groups of SB_V_PLANE_LPG. On the
+// 7B workload (28 layers, 13926 pairs, graph replays on one box): plain scatter K 8 / V 2
+// 279 us against one interleaved group of 1 layer 284-288 us (2: 280-281 us on another box,
+// 1: 274-276); rotating launches V 2 layers (four-donor composite 290 us) against 1 (305 us).
+// Single-plane-pair launches (the flat scatter) use SB_SCATTER_LPG for both planes.
 #ifndef SB_SCATTER_LPG
 #define SB_SCATTER_LPG 1
 #endif
-#ifndef SB_ROPE_SCATTER_LPG
-#define SB_ROPE_SCATTER_LPG 8
+#ifndef SB_K_PLANE_LPG
+#define SB_K_PLANE_LPG 8
 #endif
-#ifndef SB_ROPE_V_LPG
-#define SB_ROPE_V_LPG 2
+#ifndef SB_V_PLANE_LPG
+#define SB_V_PLANE_LPG 2
 #endif
 constexpr int kThreads = SB_MOVE_THREADS;
 constexpr int kBatch = SB_MOVE_BATCH;      // pair movers: rows loaded before the first store
@@ -125,9 +128,9 @@ struct MoveArgs {
   int layers_per_group;
   int kv_first;            // first kv plane (0 = K, 1 = V)
   int num_kv;              // 1 or 2 planes
-  // Rotating launches over both planes: grid.y slices [0, k_slices) rotate K in groups of
-  // layers_per_group layers, the rest copy V in groups of v_layers_per_group (0: one
-  // interleaved decode with layers_per_group for both planes).
+  // Launches over both planes of many layers: grid.y slices [0, k_slices) move (and, when
+  // rotating, rotate) K in groups of layers_per_group layers, the rest copy V in groups of
+  // v_layers_per_group (0: one interleaved decode with layers_per_group for both planes).
   int k_slices;
   int v_layers_per_group;
   int src_index_check;     // ROW_INDEX source: also require src_pos to be a valid paged slot
@@ -312,7 +315,7 @@ void move_rows_kernel(MoveArgs a, InlineArg<INLINE> ix) {
   }
 
   int kv, l0, lpg;
-  if (ROT != ROT_NONE && a.k_slices > 0) {
+  if (a.k_slices > 0) {
     const int y = static_cast<int>(blockIdx.y);
     const bool k_slice = y < a.k_slices;
     kv = k_slice ? 0 : 1;
@@ -724,14 +727,14 @@ RowSide side_index(void* base, int64_t num_heads, int64_t head_dim, int64_t es, 
   return s;
 }
 
-enum LayerGroupKind { kGroupCopy, kGroupRotK, kGroupRotV };
+enum LayerGroupKind { kGroupCopy, kGroupK, kGroupV };
 int layers_per_group_for(int64_t num_layers, int64_t num_pairs, LayerGroupKind kind);
 
-// Grid slices of a rotating launch over both planes: K in the rotating path's long layer
-// groups (cos/sin once per group), V in the plain copy's short ones (more slices in flight).
-int split_rope_planes(MoveArgs& a, int64_t num_layers, int64_t num_pairs) {
-  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, kGroupRotK);
-  a.v_layers_per_group = layers_per_group_for(num_layers, num_pairs, kGroupRotV);
+// Grid slices of a launch over both planes of many layers: K in long layer groups (cos/sin
+// once per group when rotating), V in short ones (more slices in flight).
+int split_planes(MoveArgs& a, int64_t num_layers, int64_t num_pairs) {
+  a.layers_per_group = layers_per_group_for(num_layers, num_pairs, kGroupK);
+  a.v_layers_per_group = layers_per_group_for(num_layers, num_pairs, kGroupV);
   a.k_slices = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
   return a.k_slices +
          static_cast<int>((num_layers + a.v_layers_per_group - 1) / a.v_layers_per_group);
@@ -740,11 +743,9 @@ int split_rope_planes(MoveArgs& a, int64_t num_layers, int64_t num_pairs) {
 int layers_per_group_for(int64_t num_layers, int64_t num_pairs, LayerGroupKind kind) {
   // Enough grid.y slices to fill the chip when there are few pairs; otherwise walk several
   // layers per thread so index work (and, when rotating, the fp64 cos/sin) is amortised.
-  // Plain copies stay at short groups (more independent slices in flight); the rotating
-  // path computes cos/sin once per group, so longer groups pay for themselves there.
-  const int64_t lpg = kind == kGroupRotK   ? SB_ROPE_SCATTER_LPG
-                     : kind == kGroupRotV ? SB_ROPE_V_LPG
-                                          : SB_SCATTER_LPG;
+  const int64_t lpg = kind == kGroupK   ? SB_K_PLANE_LPG
+                     : kind == kGroupV ? SB_V_PLANE_LPG
+                                       : SB_SCATTER_LPG;
   if (num_pairs >= 8192) return static_cast<int>(num_layers < lpg ? num_layers : lpg);
   return 1;
 }
@@ -836,17 +837,14 @@ static int paged_scatter_impl(const char* fn, void* kv_base, const uint64_t* kv_
   a.num_pairs = num_pairs;
   a.num_heads = static_cast<int>(num_heads);
   a.num_layers = static_cast<int>(num_layers);
-  a.layers_per_group =
-      layers_per_group_for(num_layers, num_pairs, rope ? kGroupRotK : kGroupCopy);
   a.kv_first = 0;
   a.num_kv = 2;
   a.cached_loads = (flags & SB_SCATTER_REPEATED_DONOR_ROWS) ? 1 : 0;
-  const int groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
+  const int slices = split_planes(a, num_layers, num_pairs);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (rope)
-    return launch_move<ROT_DELTA, ROW_FLAT_POS, ROW_PAGED_POS>(
-        fn, a, dtype, g, split_rope_planes(a, num_layers, num_pairs), st);
-  return launch_move<ROT_NONE, ROW_FLAT_POS, ROW_PAGED_POS>(fn, a, dtype, g, 2 * groups, st);
+    return launch_move<ROT_DELTA, ROW_FLAT_POS, ROW_PAGED_POS>(fn, a, dtype, g, slices, st);
+  return launch_move<ROT_NONE, ROW_FLAT_POS, ROW_PAGED_POS>(fn, a, dtype, g, slices, st);
 }
 
 extern "C" int sb_scatter_donor_kv_paged(void* kv_cache, const void* donor_kv,
@@ -974,12 +972,10 @@ extern "C" int sb_composite_scatter_paged_layers(
   a.num_pairs = num_pairs;
   a.num_heads = static_cast<int>(num_heads);
   a.num_layers = static_cast<int>(num_layers);
-  a.layers_per_group =
-      layers_per_group_for(num_layers, num_pairs, rope ? kGroupRotK : kGroupCopy);
   a.kv_first = 0;
   a.num_kv = 2;
   a.cached_loads = (flags & SB_SCATTER_REPEATED_DONOR_ROWS) ? 1 : 0;
-  const int groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
+  const int slices = split_planes(a, num_layers, num_pairs);
   hipStream_t st = static_cast<hipStream_t>(stream);
   for (int64_t first = 0; first < num_donors; first += kMaxDonors) {
     const int count = static_cast<int>(std::min<int64_t>(kMaxDonors, num_donors - first));
@@ -994,9 +990,8 @@ extern "C" int sb_composite_scatter_paged_layers(
       a.donors.first_pos[k] = d[4];
     }
     const int rc =
-        rope ? launch_move<ROT_DELTA, ROW_DONOR_POS, ROW_PAGED_POS>(
-                   fn, a, dtype, g, split_rope_planes(a, num_layers, num_pairs), st)
-             : launch_move<ROT_NONE, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, 2 * groups, st);
+        rope ? launch_move<ROT_DELTA, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, slices, st)
+             : launch_move<ROT_NONE, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, slices, st);
     if (rc) return rc;
   }
   return SB_OK;
