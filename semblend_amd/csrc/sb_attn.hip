@@ -996,6 +996,7 @@ template <int DT>
 __global__ __launch_bounds__(64) void attn_valu_kernel(AttnArgs a) {
   __shared__ float qs[kValuMaxDim];
   __shared__ float ps[64];
+  __shared__ const char* vrow[64];
   const int lane = threadIdx.x;
   const int64_t pi = blockIdx.x;
   const int qh = static_cast<int>(blockIdx.y);
@@ -1018,12 +1019,23 @@ __global__ __launch_bounds__(64) void attn_valu_kernel(AttnArgs a) {
   for (int t0 = 0; t0 <= p; t0 += 64) {
     const int key = t0 + lane;
     float sc = -INFINITY;
+    // Each lane resolves its key's K and V rows once per chunk (block-table lookup); the V
+    // row addresses go through LDS to the lanes that sum over keys.
+    const char* vp = nullptr;
     if (key <= p) {
       const char* kp = key_row(a, a.k, a.k_s_head, a.k_s_seq, key, kvh);
-      float dot = 0.f;
-      for (int d = 0; d < D; ++d) dot += qs[d] * load_elem<DT>(kp, d);
-      sc = dot * a.scale;
+      vp = key_row(a, a.v, a.v_s_head, a.v_s_seq, key, kvh);
+      // four independent partial dot products (d, d + 1, d + 2, d + 3), summed at the end
+      float dot[4] = {0.f, 0.f, 0.f, 0.f};
+      int d = 0;
+      for (; d + 4 <= D; d += 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dot[j] += qs[d + j] * load_elem<DT>(kp, d + j);
+      }
+      for (; d < D; ++d) dot[0] += qs[d] * load_elem<DT>(kp, d);
+      sc = ((dot[0] + dot[1]) + (dot[2] + dot[3])) * a.scale;
     }
+    vrow[lane] = vp;
     const float m_new = fmaxf(m_run, wave_max(sc));
     const float alpha = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
     const float pk = key <= p ? expf(sc - m_new) : 0.f;
@@ -1036,10 +1048,14 @@ __global__ __launch_bounds__(64) void attn_valu_kernel(AttnArgs a) {
     for (int u = 0; u < kU; ++u) {
       const int d = lane + 64 * u;
       if (d < D) {
-        float sum = 0.f;
-        for (int kk = 0; kk < nk; ++kk)
-          sum += ps[kk] * load_elem<DT>(key_row(a, a.v, a.v_s_head, a.v_s_seq, t0 + kk, kvh), d);
-        acc[u] = acc[u] * alpha + sum;
+        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+        int kk = 0;
+        for (; kk + 4 <= nk; kk += 4) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sum[j] += ps[kk + j] * load_elem<DT>(vrow[kk + j], d);
+        }
+        for (; kk < nk; ++kk) sum[0] += ps[kk] * load_elem<DT>(vrow[kk], d);
+        acc[u] = acc[u] * alpha + ((sum[0] + sum[1]) + (sum[2] + sum[3]));
       }
     }
     __syncthreads();
