@@ -90,6 +90,33 @@ def test_composite_matches_oracle(dev, dtype, rope):
         _check(got[l], want, rope)
 
 
+@pytest.mark.parametrize("rope", [True, False], ids=["rope", "copy"])
+def test_composite_load_policy_same_bits(dev, rope):
+    """Donor windows of different chunks overlap in this plan (donor rows read by several
+    pairs): the cached-load policy, the nontemporal one and the choice made from host
+    positions give the same bits."""
+    from semblend_amd import _lib
+    layers, h, bs, d, dtype = 2, 4, 16, 128, torch.bfloat16
+    lens = [300, 517]
+    donors = [[_donor(n, h, d, dtype, 300 + 10 * k + l).to(dev) for l in range(layers)]
+              for k, n in enumerate(lens)]
+    nb, nb_seq = 96, 80
+    bt = torch.randperm(nb, generator=gen(8))[:nb_seq].to(torch.int32)
+    didx, dpos, tpos = _plan(lens, nb_seq, bs, 64, 9, skip_frac=0.0)
+    assert _lib.rows_repeat(dpos, didx)
+    caches = _caches(layers, nb, h, bs, d, dtype, 11)
+    outs = []
+    for policy, host in ((False, False), (True, False), (None, True)):
+        got = [c.to(dev) for c in caches]
+        idx = (didx, dpos, tpos) if host else (didx.to(dev), dpos.to(dev), tpos.to(dev))
+        composite_scatter_paged_layers(got, donors, bt.to(dev), *idx, rope=rope,
+                                       rope_base=1e6, repeated_donor_rows=policy)
+        outs.append([g.cpu() for g in got])
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+
+
 def test_composite_single_donor_equals_layers_entries(dev):
     layers, h, bs, d, dtype = 4, 4, 16, 128, torch.bfloat16
     donor = [randn((2, h, 700, d), dtype, 30 + l).to(dev) for l in range(layers)]
