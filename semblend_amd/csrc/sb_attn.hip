@@ -74,6 +74,10 @@ constexpr int kWaveRows = 32;   // flattened query rows per MFMA row group
 constexpr int kFragAhead = SB_ATTN_FRAG_AHEAD;
 constexpr int kRing = SB_ATTN_FRAG_RING;
 static_assert(kRing > kFragAhead && (kRing & (kRing - 1)) == 0, "fragment ring");
+// Tile loop unrolled by two (stage parity and score-buffer roles fixed per copy).
+#ifndef SB_ATTN_UNROLL2
+#define SB_ATTN_UNROLL2 1
+#endif
 #ifndef SB_ATTN_ROW_GROUPS
 #define SB_ATTN_ROW_GROUPS 1
 #endif
@@ -558,27 +562,40 @@ attn_mfma_kernel(const AttnBatch batch) {
 
   // K fragment of (half n % kHalves, k-step n / kHalves): key row 32 * half + lq, 16-byte
   // chunk 2 * kstep + lg.
+  // The swizzle depends on the row modulo 16 only, so the byte offset is kl[kstep] (this
+  // lane's part, half 0, stage 0) plus a constant per (stage, half).
+  int kl[NKS];
+#pragma unroll
+  for (int k = 0; k < NKS; ++k) kl[k] = 2 * (lq * D + 8 * kswz<CH>(lq, 2 * k + lg));
   auto kfrag = [&](int stage, int n) -> vec8 {
-    const int r = 32 * (n % kHalves) + lq;
-    const int c = 2 * (n / kHalves) + lg;
-    return *reinterpret_cast<const vec8*>(&Ks[stage][r * D + 8 * kswz<CH>(r, c)]);
+    const char* base = reinterpret_cast<const char*>(&Ks[0][0]) +
+                       stage * (kTileKeys * D * 2) + (n % kHalves) * (32 * D * 2);
+    return *reinterpret_cast<const vec8*>(base + kl[n / kHalves]);
   };
   // V^T fragment of (d-tile t, step st, half j) for the A operand: lane (lq, lg) needs
   // d = 32t + lq at keys 32j + 16st + {4lg..4lg+3, 8+4lg..8+4lg+3} (the key order of the
   // P^T accumulator elements). Two ds_read_b64_tr_b16: in each group of 16 lanes, lane i
   // reads 4 consecutive d of key row kb + i/4, and the transpose hands lane i the 4 keys
   // kb..kb+3 of column d0 + i.
+  // The V swizzle depends on the row modulo 4 only, which is (gi >> 2) mod 4 here: the byte
+  // offset is vl[t] (this lane's part for d-tile t) plus a constant per (stage, j, st, e).
   const int grp = lane >> 4, gi = lane & 15;
+  int vl[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) {
+    const int d = 32 * t + 16 * (grp & 1) + 4 * (gi & 3);
+    const int row = 4 * lg + (gi >> 2);
+    vl[t] = 2 * (row * D + 8 * vswz<CH>(row, d >> 3) + (d & 7));
+  }
   auto vfrag = [&](int stage, int n) -> vec8 {
     const int t = n % NDT, st = (n / NDT) & 1, j = n / (2 * NDT);
-    const int d = 32 * t + 16 * (grp & 1) + 4 * (gi & 3);
     u32x2_t h[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const int row = 32 * j + 16 * st + 4 * lg + 8 * e + (gi >> 2);
-      const int idx = row * D + 8 * vswz<CH>(row, d >> 3) + (d & 7);
-      h[e] = __builtin_bit_cast(
-          u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((SB_LDS s16x4_t*)&Vs[stage][idx]));
+      const char* base = reinterpret_cast<const char*>(&Vs[0][0]) +
+                         stage * (kTileKeys * D * 2) + (32 * j + 16 * st + 8 * e) * (D * 2);
+      h[e] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                              (SB_LDS s16x4_t*)(base + vl[t])));
     }
     const u32x4_t w = {h[0].x, h[0].y, h[1].x, h[1].y};
     return __builtin_bit_cast(vec8, w);
@@ -659,14 +676,28 @@ attn_mfma_kernel(const AttnBatch batch) {
   mask(k0, s_cur);
   __syncthreads();  // K stage 0 is refilled at the top of the first iteration
 
-  // slot = it mod 3 (offset-table ring), advanced once per tile.
-  auto iteration = [&](int it, int slot, auto has_next, Scores& s_cur, Scores& s_nxt) {
+  // slot = it mod 3 (offset-table ring), advanced once per tile. `parity` is it mod 2 as a
+  // compile-time constant (or -1: taken from `it`); with `swap` the caller alternates the
+  // roles of the two score buffers, so S(it+1) stays where QK^T left it.
+  auto iteration = [&](int it, int slot, auto has_next, auto parity, auto swap, Scores& s_cur,
+                       Scores& s_nxt) {
     constexpr bool NEXT = decltype(has_next)::value;
+    constexpr int PAR = decltype(parity)::value;
+    const int par = PAR >= 0 ? PAR : (it & 1);
+    if (PAR >= 0) {
+      // Loop-carried through an empty asm: the fragment addresses are then not loop
+      // invariants, so the compiler folds the (stage, half) constants into the LDS
+      // instructions' offsets instead of keeping one register per address.
+#pragma unroll
+      for (int k = 0; k < NKS; ++k) asm volatile("" : "+v"(kl[k]));
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) asm volatile("" : "+v"(vl[t]));
+    }
     const int t0 = k0 + it * kTileKeys;
     const int slot1 = slot == 2 ? 0 : slot + 1;  // (it + 1) mod 3
     const int slot2 = slot == 0 ? 2 : slot - 1;  // (it + 2) mod 3
-    if (it + 2 < ntiles) load_k(slot2, it & 1);
-    if (it + 1 < ntiles) load_v(slot1, (it + 1) & 1);
+    if (it + 2 < ntiles) load_k(slot2, par);
+    if (it + 1 < ntiles) load_v(slot1, par ^ 1);
     // Offsets of tile it+3: kTileKeys / kWaves entries from each wave.
     if (it + 3 < ntiles && lane < kTileKeys / kWaves)
       fill_offsets(slot, t0 + 3 * kTileKeys, wave * (kTileKeys / kWaves) + lane);
@@ -683,7 +714,7 @@ attn_mfma_kernel(const AttnBatch batch) {
       constexpr int NPAIR = RG * kHalves * 8;          // P pairs per lane
       static_assert(NPAIR % NQ == 0, "P pairs split evenly over the MFMA steps");
       constexpr int PPS = NPAIR / NQ;                  // pairs per step
-      const int ks = (it + 1) & 1;
+      const int ks = par ^ 1;
       vec8 ring[kRing];
 #pragma unroll
       for (int n = 0; n < kFragAhead; ++n) ring[n] = kfrag(ks, n);
@@ -814,7 +845,7 @@ attn_mfma_kernel(const AttnBatch batch) {
       __builtin_amdgcn_s_setprio(SB_ATTN_PV_PRIO);
 #endif
       constexpr int NV = 2 * kHalves * NDT;  // (half, step, d-tile) triples
-      const int vb = it & 1;
+      const int vb = par;
       vec8 vring[kRing];
 #pragma unroll
       for (int n = 0; n < kFragAhead; ++n) vring[n] = vfrag(vb, n);
@@ -831,7 +862,7 @@ attn_mfma_kernel(const AttnBatch batch) {
       __builtin_amdgcn_s_setprio(0);
 #endif
     }
-    if (NEXT) {
+    if (NEXT && !decltype(swap)::value) {
 #pragma unroll
       for (int g = 0; g < RG; ++g)
 #pragma unroll
@@ -840,12 +871,36 @@ attn_mfma_kernel(const AttnBatch batch) {
     wait_vmem();
     __syncthreads();
   };
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
   int slot = 0;
-  for (int it = 0; it + 1 < ntiles; ++it) {
-    iteration(it, slot, std::true_type{}, s_cur, s_nxt);
-    slot = slot == 2 ? 0 : slot + 1;
+  auto next_slot = [](int sl) { return sl == 2 ? 0 : sl + 1; };
+#if SB_ATTN_UNROLL2
+  // Two tiles per trip: the K/V stages are constants (fragment addresses fold into the LDS
+  // instructions' offsets) and the score buffers swap roles instead of being copied.
+  int it = 0;
+  for (; it + 2 < ntiles; it += 2) {
+    iteration(it, slot, std::true_type{}, P0{}, std::true_type{}, s_cur, s_nxt);
+    slot = next_slot(slot);
+    iteration(it + 1, slot, std::true_type{}, P1{}, std::true_type{}, s_nxt, s_cur);
+    slot = next_slot(slot);
   }
-  iteration(ntiles - 1, slot, std::false_type{}, s_cur, s_nxt);
+  // One or two tiles left (`it` even); the scores of tile `it` are in s_cur.
+  using PR = std::integral_constant<int, -1>;
+  if (it + 1 < ntiles) {
+    iteration(it, slot, std::true_type{}, PR{}, std::false_type{}, s_cur, s_nxt);
+    slot = next_slot(slot);
+    ++it;
+  }
+  iteration(it, slot, std::false_type{}, PR{}, std::false_type{}, s_cur, s_nxt);
+#else
+  using PR = std::integral_constant<int, -1>;
+  for (int it = 0; it + 1 < ntiles; ++it) {
+    iteration(it, slot, std::true_type{}, PR{}, std::false_type{}, s_cur, s_nxt);
+    slot = next_slot(slot);
+  }
+  iteration(ntiles - 1, slot, std::false_type{}, PR{}, std::false_type{}, s_cur, s_nxt);
+#endif
 
   // ---- finish: lane holds d = 32t + 8*(i/4) + 4*lg + (i%4) of each of its rows ----
 #pragma unroll
