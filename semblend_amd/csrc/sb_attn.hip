@@ -332,7 +332,7 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane i's chunk lands at
-// lds_wave + 16 i, where lds_wave is wave-uniform. Written as inline assembly on purpose:
+// LDS byte address lds_wave + 16 i, where lds_wave is wave-uniform. Written as inline assembly on purpose:
 // the compiler treats a direct-to-LDS load it knows about as a pending write to the whole LDS
 // variable and waits for it (vmcnt(0)) before any later read of that variable, which would
 // serialise every prefetch with the tile being computed. Hidden from it, the loads overlap
@@ -341,17 +341,19 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // completions are counted in order, so extra outstanding loads only make them stricter.)
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // m0 is named as clobbered on purpose
-__device__ __forceinline__ void dma_row_chunk(const char* src, const uint16_t* lds_wave) {
-  // The low 32 bits of a generic pointer into LDS are the LDS byte address.
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_wave)));
+__device__ __forceinline__ void dma_row_chunk(const char* src, uint32_t lds_wave) {
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
       "global_load_lds_dwordx4 %1, off"
       :
-      : "s"(m0), "v"(src)
+      : "s"(lds_wave), "v"(src)
       : "memory", "m0");
+}
+// LDS byte address of a pointer into a __shared__ array (wave-uniform arithmetic on it stays
+// in scalar registers).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((SB_LDS const void*)p));
 }
 #pragma clang diagnostic pop
 
@@ -554,7 +556,7 @@ attn_mfma_kernel(const AttnBatch batch) {
     for (int q = 0; q < NLD; ++q) ro[q] = ofs[q * (kThreads / CH) + tid / CH];
 #pragma unroll
     for (int q = 0; q < NLD; ++q)
-      dma_row_chunk(src + ro[q], dst + (q * kThreads + wave * 64) * 8);
+      dma_row_chunk(src + ro[q], lds_addr(dst) + (q * kThreads + wave * 64) * 16);
   };
   auto load_k = [&](int slot, int stage) { load_rows(ksrc, kofs[slot], Ks[stage]); };
   auto load_v = [&](int slot, int stage) {
