@@ -951,6 +951,10 @@ attn_mfma_kernel(const AttnBatch batch) {
 //   M = max_c m_c,  O = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.
 // One workgroup per (32 rows of a row tile, KV head); 8 threads per row, each owning D / 8
 // output elements, so the partial reads of a row are spread over 8 lanes.
+#ifndef SB_MERGE_BATCH_CHUNKS
+#define SB_MERGE_BATCH_CHUNKS 4
+#endif
+constexpr int kMergeBatch = SB_MERGE_BATCH_CHUNKS;  // chunks whose partials a merge lane loads in one batch
 template <int DT, int D>
 __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnBatch batch) {
   __shared__ int red[4];
@@ -995,14 +999,46 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnBatch batch) 
   constexpr int DPT = D / 8;  // values per lane (8 lanes per row)
   const int d_begin = (tid % 8) * DPT;
   const int64_t base = (static_cast<int64_t>(kvh) * a.n_tiles + tile) * a.max_chunks;
-  float mmax = -INFINITY;
-  for (int ch = 0; ch < nchunks; ++ch)
-    mmax = fmaxf(mmax, a.part_ml[((base + ch) * TR + row_in_tile) * 2]);
-  // Each chunk's DPT values are loaded together (one 16-byte load per four), then weighted.
   float acc[DPT];
 #pragma unroll
   for (int e = 0; e < DPT; ++e) acc[e] = 0.f;
   float lsum = 0.f;
+  if (nchunks <= kMergeBatch) {
+    // Every chunk's (m, l) and values requested at once: one round trip to memory.
+    float2 ml[kMergeBatch];
+    float4 v[kMergeBatch][DPT / 4];
+#pragma unroll
+    for (int ch = 0; ch < kMergeBatch; ++ch) {
+      if (ch < nchunks) {
+        const int64_t slot = (base + ch) * TR + row_in_tile;
+        ml[ch] = *reinterpret_cast<const float2*>(a.part_ml + slot * 2);
+#pragma unroll
+        for (int q = 0; q < DPT / 4; ++q)
+          v[ch][q] = *reinterpret_cast<const float4*>(a.part_o + slot * D + d_begin + 4 * q);
+      }
+    }
+    float mmax = -INFINITY;
+#pragma unroll
+    for (int ch = 0; ch < kMergeBatch; ++ch)
+      if (ch < nchunks) mmax = fmaxf(mmax, ml[ch].x);
+#pragma unroll
+    for (int ch = 0; ch < kMergeBatch; ++ch) {
+      if (ch >= nchunks || ml[ch].x == -INFINITY) continue;
+      const float w = __builtin_amdgcn_exp2f(ml[ch].x - mmax);
+      lsum += w * ml[ch].y;
+#pragma unroll
+      for (int q = 0; q < DPT / 4; ++q) {
+        acc[4 * q] += w * v[ch][q].x;
+        acc[4 * q + 1] += w * v[ch][q].y;
+        acc[4 * q + 2] += w * v[ch][q].z;
+        acc[4 * q + 3] += w * v[ch][q].w;
+      }
+    }
+  } else {
+  float mmax = -INFINITY;
+  for (int ch = 0; ch < nchunks; ++ch)
+    mmax = fmaxf(mmax, a.part_ml[((base + ch) * TR + row_in_tile) * 2]);
+  // Each chunk's DPT values are loaded together (one 16-byte load per four), then weighted.
   for (int ch = 0; ch < nchunks; ++ch) {
     const int64_t slot = (base + ch) * TR + row_in_tile;
     const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + slot * 2);
@@ -1020,6 +1056,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnBatch batch) 
       acc[4 * q + 2] += w * v[q].z;
       acc[4 * q + 3] += w * v[q].w;
     }
+  }
   }
   const float inv = 1.f / lsum;
   char* op = a.o + qrow * a.o_s_row + qh * a.o_s_head;
