@@ -113,6 +113,20 @@ def test_paged_gqa_block_sizes(dev, bs):
     assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("seq_len", [384, 383])
+def test_paged_gqa_every_tile_count(dev, dtype, seq_len):
+    """Every position of a short context is a query row, so the row tiles' key ranges grow
+    from one 64-key tile to six (and, at 383, end one key short of a tile): the tile loop
+    runs its two-tile body zero to two times and finishes with one or two tiles, for every
+    combination."""
+    q, kv, bt, _ = _paged_case(28, 4, 128, seq_len, 8, dtype, 70 + seq_len)
+    pos = torch.arange(seq_len, dtype=torch.int32)
+    q = randn((seq_len, 28, 128), dtype, 71 + seq_len)
+    got = tk.partial_prefill_attention_paged(q.to(dev), kv.to(dev), bt.to(dev), pos.to(dev))
+    assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
+
+
 def test_paged_gqa_position_major_layout(dev):
     """A cache stored [blocks, block_size, 2, kv_heads, head_dim] and viewed as
     [blocks, 2, kv_heads, block_size, head_dim]: the position stride (2·H·D) exceeds the
