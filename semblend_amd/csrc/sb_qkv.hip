@@ -49,6 +49,15 @@ constexpr int kQThreads = 256;
 #ifndef SB_QKV_STAGES
 #define SB_QKV_STAGES 2
 #endif
+// Fragments of the next MFMA substep read while the current one's MFMAs issue (0: the
+// compiler's own order).
+#ifndef SB_QKV_FRAG_PIPE
+#define SB_QKV_FRAG_PIPE 1
+#endif
+// Substeps over which a step's refill loads are spread (the first ones of the step).
+#ifndef SB_QKV_DMA_SPREAD
+#define SB_QKV_DMA_SPREAD 2
+#endif
 constexpr int kTK = SB_QKV_TK;        // hidden elements per k-step (2 * kTK-byte tile rows)
 constexpr int kStages = SB_QKV_STAGES;  // LDS ring depth: loads run kStages - 1 steps ahead
 constexpr int kTileChunks = kTK / 8;  // 16-byte chunks per tile row
@@ -124,16 +133,19 @@ __device__ __forceinline__ void qkv_tile(int64_t b, int64_t n_ft, int64_t n_rt, 
 // each stage.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void qkv_dma(const char* src, const uint16_t* lds_wave) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_wave)));
+__device__ __forceinline__ void qkv_dma(const char* src, uint32_t lds_wave) {
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
       "global_load_lds_dwordx4 %1, off"
       :
-      : "s"(m0), "v"(src)
+      : "s"(lds_wave), "v"(src)
       : "memory", "m0");
+}
+// LDS byte address of a pointer into a __shared__ array (wave-uniform arithmetic on it stays
+// in scalar registers).
+__device__ __forceinline__ uint32_t qkv_lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
 }
 #pragma clang diagnostic pop
 
@@ -189,7 +201,8 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
   __shared__ __align__(16) float bias_s[TM];  // the tile's bias (0 without bias / past F)
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, lq = lane & 31, lg = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
+  const int lane = tid & 63, lq = lane & 31, lg = lane >> 5;
   const int wm = wave & 1, wn = wave >> 1;
   const int64_t n_ft = (a.num_features + TM - 1) / TM;
   const int64_t n_rt = (a.num_rows + TN - 1) / TN;
@@ -241,14 +254,18 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
 #pragma unroll
   for (int q = 0; q < LB; ++q)
     bsrc[q] = a.hidden + brow[q * kLoadRows + tid / kTileChunks] + 16 * chunk;
-  auto issue = [&](int stage, int64_t kt) {
+  // Load q of a step (A loads first, then B), each 16 bytes per lane into its stage.
+  auto issue_one = [&](int stage, int64_t kt, int q) {
     const int64_t ko = kt * (kTK * 2);
+    if (q < LA)
+      qkv_dma(asrc[q] + ko, qkv_lds_addr(As(stage)) + (q * kQThreads + wave * 64) * 16);
+    else
+      qkv_dma(bsrc[q - LA] + ko,
+              qkv_lds_addr(Bs(stage)) + ((q - LA) * kQThreads + wave * 64) * 16);
+  };
+  auto issue = [&](int stage, int64_t kt) {
 #pragma unroll
-    for (int q = 0; q < LA; ++q)
-      qkv_dma(asrc[q] + ko, As(stage) + (q * kQThreads + wave * 64) * 8);
-#pragma unroll
-    for (int q = 0; q < LB; ++q)
-      qkv_dma(bsrc[q] + ko, Bs(stage) + (q * kQThreads + wave * 64) * 8);
+    for (int q = 0; q < LA + LB; ++q) issue_one(stage, kt, q);
   };
 
   qf32x16_t acc[BI][BJ];
@@ -265,7 +282,10 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
 #pragma unroll
   for (int s0 = 0; s0 < kStages - 1; ++s0)
     if (s0 < a.k_steps) issue(s0, s0);
-  for (int64_t kt = 0; kt < a.k_steps; ++kt) {
+  // Step kt; REFILL: whether it issues the loads of step kt + kStages - 1 (every step but
+  // the last kStages - 1), a compile-time choice so that the loads need no branch.
+  auto step = [&](int64_t kt, auto refill_c) {
+    constexpr bool REFILL = decltype(refill_c)::value;
     const int st = static_cast<int>(kt % kStages);
     // Steps issued after this one: at most kStages - 2, fewer near the end; they may stay
     // in flight while step kt must have landed.
@@ -274,33 +294,68 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
     else if (kStages >= 3 && ahead >= 1) qkv_wait_vm<LA + LB>();
     else qkv_wait_vm<0>();
     __syncthreads();
-    if (kt + kStages - 1 < a.k_steps)
-      issue(static_cast<int>((kt + kStages - 1) % kStages), kt + kStages - 1);
-    // Per k-substep: the wave's BI A and BJ B fragments, then BI x BJ MFMAs.
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
+    const int rst = static_cast<int>((kt + kStages - 1) % kStages);
+#if !SB_QKV_FRAG_PIPE
+    if (REFILL) issue(rst, kt + kStages - 1);
+#endif
+    // Per k-substep: the wave's BI A and BJ B fragments, then BI x BJ MFMAs. The fragments
+    // are double-buffered: those of substep ks + 1 are read while the MFMAs of substep ks
+    // issue (scheduling barriers keep that order), so the LDS latency sits under BI x BJ
+    // MFMAs instead of stalling the wave, the only one on its SIMD, before each of them.
+    // The loads that refill the ring's free stage go out one after each MFMA.
+    vec8 af[2][BI], bf[2][BJ];
+    auto read_frags = [&](int ks, vec8* a_f, vec8* b_f) {
       const int c = 2 * ks + lg;
-      vec8 af[BI], bf[BJ];
 #pragma unroll
       for (int i = 0; i < BI; ++i) {
         const int r = wm * (32 * BI) + i * 32 + lq;
-        af[i] = *reinterpret_cast<const vec8*>(As(st) + r * kTK + 8 * qswz(r, c));
+        a_f[i] = *reinterpret_cast<const vec8*>(As(st) + r * kTK + 8 * qswz(r, c));
       }
 #pragma unroll
       for (int j = 0; j < BJ; ++j) {
         const int r = wn * (32 * BJ) + j * 32 + lq;
-        bf[j] = *reinterpret_cast<const vec8*>(Bs(st) + r * kTK + 8 * qswz(r, c));
+        b_f[j] = *reinterpret_cast<const vec8*>(Bs(st) + r * kTK + 8 * qswz(r, c));
       }
+    };
+    read_frags(0, af[0], bf[0]);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+#if SB_QKV_FRAG_PIPE
+      if (ks + 1 < NKS) read_frags(ks + 1, af[(ks + 1) & 1], bf[(ks + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#endif
+      const vec8* a_f = af[ks & 1];
+      const vec8* b_f = bf[ks & 1];
 #pragma unroll
       for (int i = 0; i < BI; ++i)
 #pragma unroll
         for (int j = 0; j < BJ; ++j) {
           if (DT == SB_DTYPE_BF16)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_f[i], b_f[j], acc[i][j], 0, 0, 0);
           else
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_f[i], b_f[j], acc[i][j], 0, 0, 0);
+#if SB_QKV_FRAG_PIPE
+          constexpr int kSpread = SB_QKV_DMA_SPREAD < NKS ? SB_QKV_DMA_SPREAD : NKS;
+          constexpr int kPer = (LA + LB + kSpread - 1) / kSpread;  // loads per substep
+          static_assert(kPer <= BI * BJ, "every load follows an MFMA of its substep");
+          const int q = ks * kPer + i * BJ + j;
+          if (REFILL && i * BJ + j < kPer && q < LA + LB) {
+            issue_one(rst, kt + kStages - 1, q);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+#endif
         }
+#if SB_QKV_FRAG_PIPE
+      __builtin_amdgcn_sched_barrier(0);
+#else
+      if (ks + 1 < NKS) read_frags(ks + 1, af[(ks + 1) & 1], bf[(ks + 1) & 1]);
+#endif
     }
+  };
+  {
+    int64_t kt = 0;
+    for (; kt + kStages - 1 < a.k_steps; ++kt) step(kt, std::true_type{});
+    for (; kt < a.k_steps; ++kt) step(kt, std::false_type{});
   }
 
   // Epilogue, phase 1: lane (lq, lg) of block (i, j) holds tile row wn*32*BJ + 32j + lq and,
