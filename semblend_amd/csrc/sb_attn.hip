@@ -79,6 +79,11 @@ static_assert(kRing > kFragAhead && (kRing & (kRing - 1)) == 0, "fragment ring")
 #ifndef SB_ATTN_UNROLL2
 #define SB_ATTN_UNROLL2 1
 #endif
+// Tile loads of the two-tile loop issued one after each early MFMA step of the QK block
+// instead of in a burst at the top of the iteration.
+#ifndef SB_ATTN_LOADS_IN_QK
+#define SB_ATTN_LOADS_IN_QK 1
+#endif
 #ifndef SB_ATTN_ROW_GROUPS
 #define SB_ATTN_ROW_GROUPS 1
 #endif
@@ -558,6 +563,14 @@ attn_mfma_kernel(const AttnBatch batch) {
     for (int q = 0; q < NLD; ++q)
       dma_row_chunk(src + ro[q], lds_addr(dst) + (q * kThreads + wave * 64) * 16);
   };
+  // The same loads in two parts: the row offsets first, then load q of the tile (K or V).
+  auto read_ofs = [&](const uint64_t* ofs, uint64_t* ro) {
+#pragma unroll
+    for (int q = 0; q < NLD; ++q) ro[q] = ofs[q * (kThreads / CH) + tid / CH];
+  };
+  auto dma_one = [&](const char* src, uint64_t ro, uint16_t* dst, int q) {
+    dma_row_chunk(src + ro, lds_addr(dst) + (q * kThreads + wave * 64) * 16);
+  };
   auto load_k = [&](int slot, int stage) { load_rows(ksrc, kofs[slot], Ks[stage]); };
   auto load_v = [&](int slot, int stage) {
     load_rows(vsrc, kPaged ? kofs[slot] : vofs[slot], Vs[stage]);
@@ -682,9 +695,13 @@ attn_mfma_kernel(const AttnBatch batch) {
   // slot = it mod 3 (offset-table ring), advanced once per tile. `parity` is it mod 2 as a
   // compile-time constant (or -1: taken from `it`); with `swap` the caller alternates the
   // roles of the two score buffers, so S(it+1) stays where QK^T left it.
+  // With `ilv` (only where both loads are known to be due: K(it+2) and V(it+1)) the tile
+  // loads go out inside the QK block, one after each of its first 2 NLD MFMA steps.
   auto iteration = [&](int it, int slot, auto has_next, auto parity, auto swap, Scores& s_cur,
-                       Scores& s_nxt) {
+                       Scores& s_nxt, auto ilv) {
     constexpr bool NEXT = decltype(has_next)::value;
+    constexpr bool ILV = decltype(ilv)::value;
+    static_assert(!ILV || NEXT, "interleaved loads ride on the QK block");
     constexpr int PAR = decltype(parity)::value;
     const int par = PAR >= 0 ? PAR : (it & 1);
     if (PAR >= 0) {
@@ -699,8 +716,14 @@ attn_mfma_kernel(const AttnBatch batch) {
     const int t0 = k0 + it * kTileKeys;
     const int slot1 = slot == 2 ? 0 : slot + 1;  // (it + 1) mod 3
     const int slot2 = slot == 0 ? 2 : slot - 1;  // (it + 2) mod 3
-    if (it + 2 < ntiles) load_k(slot2, par);
-    if (it + 1 < ntiles) load_v(slot1, par ^ 1);
+    uint64_t ro_k[NLD], ro_v[NLD];
+    if (ILV) {
+      read_ofs(kofs[slot2], ro_k);
+      read_ofs(kPaged ? kofs[slot1] : vofs[slot1], ro_v);
+    } else {
+      if (it + 2 < ntiles) load_k(slot2, par);
+      if (it + 1 < ntiles) load_v(slot1, par ^ 1);
+    }
     // Offsets of tile it+3: kTileKeys / kWaves entries from each wave.
     if (it + 3 < ntiles && lane < kTileKeys / kWaves)
       fill_offsets(slot, t0 + 3 * kTileKeys, wave * (kTileKeys / kWaves) + lane);
@@ -752,6 +775,11 @@ attn_mfma_kernel(const AttnBatch batch) {
         for (int g = 0; g < RG; ++g)
           s_nxt[g][j] =
               M::mma(ring[n % kRing], qf[g][n / kHalves], n < kHalves ? f32x16_t{} : s_nxt[g][j]);
+        if (ILV) {
+          static_assert(2 * NLD <= NQ, "one load per MFMA step");
+          if (n < NLD) dma_one(ksrc, ro_k[n], Ks[par], n);
+          else if (n < 2 * NLD) dma_one(vsrc, ro_v[n - NLD], Vs[par ^ 1], n - NLD);
+        }
 #if SB_ATTN_VALU_SKEW
         // Three-stage VALU pipeline over the pairs: the fmas of pair n + 1, the exp2 of pair
         // n and the packing and sum of pair n - 1 share step n, so no instruction of a step
@@ -878,31 +906,33 @@ attn_mfma_kernel(const AttnBatch batch) {
   using P1 = std::integral_constant<int, 1>;
   int slot = 0;
   auto next_slot = [](int sl) { return sl == 2 ? 0 : sl + 1; };
+  using ILV = std::integral_constant<bool, SB_ATTN_LOADS_IN_QK != 0>;
+  using NOILV = std::false_type;
 #if SB_ATTN_UNROLL2
   // Two tiles per trip: the K/V stages are constants (fragment addresses fold into the LDS
-  // instructions' offsets) and the score buffers swap roles instead of being copied.
+  // instructions' offsets) and the score buffers swap roles instead of being copied. The
+  // trip runs while both of its tiles have both loads due (tile it + 3 exists).
   int it = 0;
-  for (; it + 2 < ntiles; it += 2) {
-    iteration(it, slot, std::true_type{}, P0{}, std::true_type{}, s_cur, s_nxt);
+  for (; it + 3 < ntiles; it += 2) {
+    iteration(it, slot, std::true_type{}, P0{}, std::true_type{}, s_cur, s_nxt, ILV{});
     slot = next_slot(slot);
-    iteration(it + 1, slot, std::true_type{}, P1{}, std::true_type{}, s_nxt, s_cur);
+    iteration(it + 1, slot, std::true_type{}, P1{}, std::true_type{}, s_nxt, s_cur, ILV{});
     slot = next_slot(slot);
   }
-  // One or two tiles left (`it` even); the scores of tile `it` are in s_cur.
+  // One to three tiles left; the scores of tile `it` are in s_cur.
   using PR = std::integral_constant<int, -1>;
-  if (it + 1 < ntiles) {
-    iteration(it, slot, std::true_type{}, PR{}, std::false_type{}, s_cur, s_nxt);
+  for (; it + 1 < ntiles; ++it) {
+    iteration(it, slot, std::true_type{}, PR{}, std::false_type{}, s_cur, s_nxt, NOILV{});
     slot = next_slot(slot);
-    ++it;
   }
-  iteration(it, slot, std::false_type{}, PR{}, std::false_type{}, s_cur, s_nxt);
+  iteration(it, slot, std::false_type{}, PR{}, std::false_type{}, s_cur, s_nxt, NOILV{});
 #else
   using PR = std::integral_constant<int, -1>;
   for (int it = 0; it + 1 < ntiles; ++it) {
-    iteration(it, slot, std::true_type{}, PR{}, std::false_type{}, s_cur, s_nxt);
+    iteration(it, slot, std::true_type{}, PR{}, std::false_type{}, s_cur, s_nxt, NOILV{});
     slot = next_slot(slot);
   }
-  iteration(ntiles - 1, slot, std::false_type{}, PR{}, std::false_type{}, s_cur, s_nxt);
+  iteration(ntiles - 1, slot, std::false_type{}, PR{}, std::false_type{}, s_cur, s_nxt, NOILV{});
 #endif
 
   // ---- finish: lane holds d = 32t + 8*(i/4) + 4*lg + (i%4) of each of its rows ----
