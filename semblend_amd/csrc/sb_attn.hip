@@ -337,7 +337,8 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane i's chunk lands at
-// LDS byte address lds_wave + 16 i, where lds_wave is wave-uniform. Written as inline assembly on purpose:
+// LDS byte address lds_wave + 16 i, where lds_wave is wave-uniform. Written as inline
+// assembly on purpose:
 // the compiler treats a direct-to-LDS load it knows about as a pending write to the whole LDS
 // variable and waits for it (vmcnt(0)) before any later read of that variable, which would
 // serialise every prefetch with the tile being computed. Hidden from it, the loads overlap
@@ -677,10 +678,10 @@ attn_mfma_kernel(const AttnBatch batch) {
   // Software pipeline over tiles of kTileKeys keys. Iteration `it` computes S(it+1) = QK^T
   // of the next tile while it turns S(it) into P(it) (MFMA and VALU work interleave in one
   // block), then O += V(it)^T P(it). K has two LDS stages and runs two tiles ahead, V two
-  // stages and one tile ahead: at the top of iteration `it` the loads of K(it+2) and V(it+1)
-  // are issued into the stages that QK(it) and PV(it-1) released; each wave waits for its
-  // own loads before the iteration's single barrier. Key offsets come from a three-slot
-  // table ring (slot = tile mod 3) filled three tiles ahead.
+  // stages and one tile ahead: iteration `it` issues the loads of K(it+2) and V(it+1) into
+  // the stages that QK(it) and PV(it-1) released (at its top, or spread over its QK block);
+  // each wave waits for its own loads before the iteration's single barrier. Key offsets
+  // come from a three-slot table ring (slot = tile mod 3) filled three tiles ahead.
   const int ntiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
   Scores s_cur, s_nxt;
   load_k(0, 0);
@@ -984,7 +985,8 @@ attn_mfma_kernel(const AttnBatch batch) {
 #ifndef SB_MERGE_BATCH_CHUNKS
 #define SB_MERGE_BATCH_CHUNKS 4
 #endif
-constexpr int kMergeBatch = SB_MERGE_BATCH_CHUNKS;  // chunks whose partials a merge lane loads in one batch
+// Chunks whose partials a merge lane loads in one batch.
+constexpr int kMergeBatch = SB_MERGE_BATCH_CHUNKS;
 template <int DT, int D>
 __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnBatch batch) {
   __shared__ int red[4];
@@ -1065,28 +1067,28 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnBatch batch) 
       }
     }
   } else {
-  float mmax = -INFINITY;
-  for (int ch = 0; ch < nchunks; ++ch)
-    mmax = fmaxf(mmax, a.part_ml[((base + ch) * TR + row_in_tile) * 2]);
-  // Each chunk's DPT values are loaded together (one 16-byte load per four), then weighted.
-  for (int ch = 0; ch < nchunks; ++ch) {
-    const int64_t slot = (base + ch) * TR + row_in_tile;
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + slot * 2);
-    if (ml.x == -INFINITY) continue;
-    const float w = __builtin_amdgcn_exp2f(ml.x - mmax);
-    lsum += w * ml.y;
-    float4 v[DPT / 4];
+    float mmax = -INFINITY;
+    for (int ch = 0; ch < nchunks; ++ch)
+      mmax = fmaxf(mmax, a.part_ml[((base + ch) * TR + row_in_tile) * 2]);
+    // Each chunk's DPT values are loaded together (one 16-byte load per four), then weighted.
+    for (int ch = 0; ch < nchunks; ++ch) {
+      const int64_t slot = (base + ch) * TR + row_in_tile;
+      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + slot * 2);
+      if (ml.x == -INFINITY) continue;
+      const float w = __builtin_amdgcn_exp2f(ml.x - mmax);
+      lsum += w * ml.y;
+      float4 v[DPT / 4];
 #pragma unroll
-    for (int q = 0; q < DPT / 4; ++q)
-      v[q] = *reinterpret_cast<const float4*>(a.part_o + slot * D + d_begin + 4 * q);
+      for (int q = 0; q < DPT / 4; ++q)
+        v[q] = *reinterpret_cast<const float4*>(a.part_o + slot * D + d_begin + 4 * q);
 #pragma unroll
-    for (int q = 0; q < DPT / 4; ++q) {
-      acc[4 * q] += w * v[q].x;
-      acc[4 * q + 1] += w * v[q].y;
-      acc[4 * q + 2] += w * v[q].z;
-      acc[4 * q + 3] += w * v[q].w;
+      for (int q = 0; q < DPT / 4; ++q) {
+        acc[4 * q] += w * v[q].x;
+        acc[4 * q + 1] += w * v[q].y;
+        acc[4 * q + 2] += w * v[q].z;
+        acc[4 * q + 3] += w * v[q].w;
+      }
     }
-  }
   }
   const float inv = 1.f / lsum;
   char* op = a.o + qrow * a.o_s_row + qh * a.o_s_head;

@@ -145,7 +145,8 @@ __device__ __forceinline__ void qkv_dma(const char* src, uint32_t lds_wave) {
 // LDS byte address of a pointer into a __shared__ array (wave-uniform arithmetic on it stays
 // in scalar registers).
 __device__ __forceinline__ uint32_t qkv_lds_addr(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+  using lds_ptr = __attribute__((address_space(3))) const void*;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr)p));
 }
 #pragma clang diagnostic pop
 
