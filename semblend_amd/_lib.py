@@ -8,6 +8,7 @@ fails to load, every kernel entry point raises ``RuntimeError``.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 from pathlib import Path
@@ -219,8 +220,28 @@ def require_device(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
+# torch's own raw accessors (what its compiler's generated code uses): a plain int for the
+# current stream and device, without building Python stream or device objects per launch.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_current_index = getattr(torch._C, "_cuda_getDevice", None)
+
+
+def _index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
 def stream_handle(device: torch.device) -> int:
+    """The current stream of ``device`` as a raw handle for the C ABI."""
+    if _raw_stream is not None:
+        return _raw_stream(_index(device))
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def on_device(device: torch.device):
+    """Context that makes ``device`` current for a launch; a no-op when it already is."""
+    if _current_index is not None and _current_index() == _index(device):
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 def upload_index(t: torch.Tensor, device: torch.device) -> torch.Tensor:
@@ -236,6 +257,9 @@ def upload_index(t: torch.Tensor, device: torch.device) -> torch.Tensor:
 def as_index(t, device: torch.device) -> torch.Tensor:
     """int32 contiguous device copy of an index tensor or sequence (no copy if already so);
     host data is uploaded without blocking the host."""
+    if (isinstance(t, torch.Tensor) and t.dtype == torch.int32 and t.dim() == 1 and t.is_cuda
+            and t.get_device() == _index(device) and t.is_contiguous()):
+        return t
     if not isinstance(t, torch.Tensor):
         t = torch.as_tensor(list(t), dtype=torch.int32)
     if t.device.type == "cpu":

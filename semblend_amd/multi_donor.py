@@ -168,7 +168,7 @@ def composite_scatter_paged_layers(
     if repeated_donor_rows is None:
         repeated_donor_rows = _lib.rows_repeat(donor_positions, donor_index)
     inv_freq = inv_freq_table(rope_base, head_dim, dev) if rope else None
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_composite_scatter_paged_layers",
             kv_tab.data_ptr(), num_layers, d_tab.data_ptr(), len(donor_kvs),

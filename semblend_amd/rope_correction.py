@@ -108,7 +108,7 @@ def rope_correct_scatter_paged(
     dpos = _lib.as_index(donor_positions, dev)
     tpos = _lib.as_index(target_positions, dev)
     inv_freq = inv_freq_table(rope_base, head_dim, dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_rope_correct_scatter_paged",
             kv_cache.data_ptr(), donor_kv.data_ptr(), bt.data_ptr(), dpos.data_ptr(),
@@ -157,7 +157,7 @@ class PreparedLaunch:
         self.entry, self.args, self.keep, self.device = entry, args, keep, device
 
     def __call__(self) -> None:
-        with torch.cuda.device(self.device):
+        with _lib.on_device(self.device):
             st = _lib.stream_handle(self.device)
             for entry, args in self.launches:
                 _lib.call(entry, *args, st)
@@ -258,7 +258,7 @@ def _rope_k(out: torch.Tensor, k: torch.Tensor, dpos, tpos, head_dim, rope_base)
         raise ValueError("donor_positions and target_positions differ in length")
     inv_freq = inv_freq_table(rope_base, head_dim, dev)
     ws = torch.empty(2 * seq_len, dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_rope_correct_k",
             o4.data_ptr(), k4.data_ptr(), d.data_ptr(), t.data_ptr(), inv_freq.data_ptr(),
@@ -326,7 +326,7 @@ def rope_correct_k_inplace(
         if d.shape[0] == 0:
             return k_tensor
         inv_freq = inv_freq_table(rope_base, head_dim, dev)
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             _lib.call(
                 "sb_rope_correct_k_distinct",
                 k4.data_ptr(), d.data_ptr(), t.data_ptr(), inv_freq.data_ptr(), d.shape[0],
@@ -367,7 +367,7 @@ def permute_paged_kv_with_rope(
     inv_freq = inv_freq_table(rope_base, head_dim, dev)
     ws = torch.empty((len(permutation), 2, num_heads, head_dim), dtype=kv_cache.dtype,
                      device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_permute_paged_kv_with_rope",
             kv_cache.data_ptr(), bt.data_ptr(), src.data_ptr(), tgt.data_ptr(),
@@ -419,7 +419,7 @@ def nope_permute_paged_kv(
     inv_freq = inv_freq_table(rope_base, head_dim, dev)
     ws = torch.empty((len(permutation) + len(vmoves), num_heads, head_dim),
                      dtype=kv_cache.dtype, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_nope_permute_paged_kv",
             kv_cache.data_ptr(), bt.data_ptr(), src.data_ptr(), tgt.data_ptr(),
@@ -494,7 +494,7 @@ def apply_rope_delta_inplace(
     inv_freq = inv_freq_table(rope_base, head_dim, dev)
     reps = list(counts.values())
     repeated = any(c != 1 for c in reps)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         if len(counts) <= _lib.SB_INLINE_POSITIONS_MAX:
             # Short lists travel inside the launch: no index upload.
             _lib.call(

@@ -96,7 +96,7 @@ def scatter_donor_kv(
     tpos = _lib.as_index(target_positions, dev)
     tw, t_tmp = _contig_last(target)
     dw, _ = _contig_last(donor)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_scatter_donor_kv",
             tw.data_ptr(), dw.data_ptr(), dpos.data_ptr(), tpos.data_ptr(), num_pairs,
@@ -135,7 +135,7 @@ def scatter_donor_kv_paged(
     tpos = _lib.as_index(target_positions, dev)
     kw, k_tmp = _contig_last(kv_cache)
     dw, _ = _contig_last(donor_kv)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_scatter_donor_kv_paged",
             kw.data_ptr(), dw.data_ptr(), bt.data_ptr(), dpos.data_ptr(), tpos.data_ptr(),
@@ -188,7 +188,7 @@ def scatter_donor_kv_paged_layers(
     bt = _lib.as_index(block_table, dev)
     dpos = _lib.as_index(donor_positions, dev)
     tpos = _lib.as_index(target_positions, dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_scatter_donor_kv_paged_layers",
             kv_tab.data_ptr(), d_tab.data_ptr(), len(kv_caches), bt.data_ptr(),
@@ -240,7 +240,7 @@ def masked_qkv_projection(
         bias = None if qkv_bias is None else qkv_bias.contiguous()
         ws_bytes = _lib.size_query("sb_masked_qkv_projection_workspace_size", seq_len)
         ws = torch.empty(ws_bytes // 4, dtype=torch.int32, device=dev)
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             _lib.call(
                 "sb_masked_qkv_projection",
                 out.data_ptr(), hidden_states.data_ptr(), qkv_weight.data_ptr(), _lib.ptr(bias),
@@ -334,7 +334,7 @@ def qkv_projection_paged(
         # and writes no K/V for them
         xg = torch.empty((n, hidden), dtype=dt, device=dev)
         dt_code = _lib.dtype_code(hidden_states)
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             _lib.call("sb_qkv_gather_rows", xg.data_ptr(), hidden_states.data_ptr(),
                       pos.data_ptr(), n, seq_len, hidden, hidden_states.stride(0),
                       _lib.ptr(inv), head_dim, ws.data_ptr(), dt_code, _lib.stream_handle(dev))
@@ -347,7 +347,7 @@ def qkv_projection_paged(
                 num_heads * head_dim, _lib.strides(kv_cache), dt_code, _lib.stream_handle(dev),
             )
         return out
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_qkv_projection_paged",
             out.data_ptr(), hidden_states.data_ptr(), qkv_weight.data_ptr(), _lib.ptr(bias),
@@ -403,7 +403,7 @@ def partial_prefill_attention(
     ws_bytes = _lib.size_query("sb_partial_prefill_attention_workspace_size", num_heads,
                                seq_len, head_dim, dt)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_partial_prefill_attention",
             output.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), mask.data_ptr(),
@@ -461,7 +461,7 @@ def partial_prefill_attention_paged(
     ws_bytes = _lib.size_query("sb_partial_attention_paged_workspace_size", num_rows,
                                num_q_heads, num_kv_heads, head_dim, block_size, bt.shape[0], dt)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_partial_attention_paged",
             out.data_ptr(), q.data_ptr(), kv.data_ptr(), bt.data_ptr(), pos.data_ptr(),
@@ -535,7 +535,7 @@ def partial_prefill_attention_paged_varlen(
                                rows_a, blocks_a, num_q_heads, num_kv_heads, head_dim,
                                block_size, dt)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.call(
             "sb_partial_attention_paged_varlen",
             out.data_ptr(), q.data_ptr(), kv.data_ptr(), bt.data_ptr(), bt.stride(0),
