@@ -147,6 +147,7 @@ struct AttnArgs {
   float scale_log2;           // scale * log2(e)
   int ksplit;                 // keys per work item (multiple of kTileKeys)
   int max_chunks;             // ceil(kv_len / ksplit)
+  int device_split;           // 1: ksplit, max_chunks and n_tiles follow the device row count
   int64_t n_tiles;            // row tiles per kv head used for the partial layout
   int tile_rows;              // flattened query rows per workgroup tile
   float* part_o;              // [Hkv][n_tiles][max_chunks][128][D] fp32, or nullptr
@@ -190,8 +191,9 @@ __device__ __forceinline__ int64_t select_request(const AttnBatch& batch, AttnAr
   return b - (merge ? s.merge_begin : s.item_begin);
 }
 
+// Rows of the call: the device-side count of a compacted mask (never more than num_rows).
 __device__ __forceinline__ int64_t attn_num_rows(const AttnArgs& a) {
-  return a.count_ptr ? static_cast<int64_t>(*a.count_ptr) : a.num_rows;
+  return a.count_ptr ? min(static_cast<int64_t>(*a.count_ptr), a.num_rows) : a.num_rows;
 }
 
 __device__ __forceinline__ int clamp_block(const AttnArgs& a, int64_t pb) {
@@ -363,6 +365,46 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 }
 #pragma clang diagnostic pop
 
+// Resident workgroups of the MFMA kernel on 256 CUs (one 4-wave workgroup per CU with two
+// row groups per wave, SB_ATTN_OCCUPANCY with one), and how many work items per slot the
+// split aims for.
+constexpr int kResidentSlots = kRowGroups == 1 ? 256 * SB_ATTN_OCCUPANCY * 4 / kWaves : 256;
+#ifndef SB_ATTN_ITEMS_PER_SLOT
+#define SB_ATTN_ITEMS_PER_SLOT 1
+#endif
+constexpr int kItemsPerSlot = SB_ATTN_ITEMS_PER_SLOT;
+
+// Key-range split of a call: items no longer than the average work per slot (assuming the
+// rows' key ranges average half the context), so that longest-first scheduling balances the
+// CUs. Host plan and device-derived split use this one rule.
+struct KeySplit {
+  int ksplit;
+  int max_chunks;
+};
+__host__ __device__ inline KeySplit key_split(int64_t n_tiles, int64_t num_kv_heads,
+                                              int64_t kv_len, int64_t block_size, bool paged) {
+  const int64_t kv_pad = (kv_len + kTileKeys - 1) / kTileKeys * kTileKeys;
+  int64_t ks = n_tiles * num_kv_heads * (kv_len / 2) / (kResidentSlots * kItemsPerSlot);
+  ks = ks / kTileKeys * kTileKeys;
+  if (ks < 512) ks = 512;
+  if (paged) {
+    const int64_t cap = static_cast<int64_t>(kBtLds) * block_size / kTileKeys * kTileKeys;
+    if (ks > cap) ks = cap;
+  }
+  if (ks > kv_pad) ks = kv_pad;
+  if (ks < kTileKeys) ks = kTileKeys;
+  const int64_t chunks = (kv_len + ks - 1) / ks;
+  return KeySplit{static_cast<int>(ks), static_cast<int>(chunks < 1 ? 1 : chunks)};
+}
+// The device-derived split of a dense call (device_split), from its row-tile count.
+__device__ __forceinline__ void apply_device_split(AttnArgs& a, int64_t n_tiles_live) {
+  if (!a.device_split) return;
+  const KeySplit sp = key_split(n_tiles_live, a.num_kv_heads, a.kv_len, 1, false);
+  a.ksplit = sp.ksplit;
+  a.max_chunks = sp.max_chunks;
+  a.n_tiles = n_tiles_live;
+}
+
 // Work-item decode shared by the attention and merge kernels.
 struct Item {
   int kvh;
@@ -425,6 +467,7 @@ attn_mfma_kernel(const AttnBatch batch) {
   const int64_t rows_kv = n_rows * a.group;
   const int64_t n_tiles_live = (rows_kv + TR - 1) / TR;
   if (n_tiles_live <= 0) return;  // no rows (uniform)
+  apply_device_split(a, n_tiles_live);
   const Item item = decode_item(a, n_tiles_live, item_b);
   if (item.tile < 0 || item.chunk >= a.max_chunks) return;  // uniform, before any barrier
   const int kvh = item.kvh;
@@ -987,17 +1030,15 @@ attn_mfma_kernel(const AttnBatch batch) {
 #endif
 // Chunks whose partials a merge lane loads in one batch.
 constexpr int kMergeBatch = SB_MERGE_BATCH_CHUNKS;
+// One unit: 32 rows of row tile `tile` of KV head `kvh` (mb = (tile * parts + part) * Hkv +
+// kvh). Returns early when the unit has nothing to merge; its one barrier is reached by every
+// thread of the workgroup (the returns before it are uniform).
 template <int DT, int D>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const AttnBatch batch) {
-  __shared__ int red[4];
-  AttnArgs a = batch.a;
-  const int64_t mb = select_request(batch, a, blockIdx.x, true);
+__device__ __forceinline__ void merge_unit(const AttnArgs& a, int64_t mb, int64_t n_tiles_live,
+                                           int64_t rows_kv, int* red) {
   const int tid = threadIdx.x;
   const int TR = a.tile_rows;  // 128 or 256
   const int parts = TR / 32;
-  const int64_t n_rows = attn_num_rows(a);
-  const int64_t rows_kv = n_rows * a.group;
-  const int64_t n_tiles_live = (rows_kv + TR - 1) / TR;
   const int kvh = static_cast<int>(mb % a.num_kv_heads);
   const int64_t rest = mb / a.num_kv_heads;
   const int64_t tile = rest / parts;
@@ -1101,6 +1142,29 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnBatch batch) 
     *reinterpret_cast<uint2*>(op + (d_begin + 4 * q) * 2) = make_uint2(w0, w1);
   }
 }
+
+// STRIDED (calls whose split follows the device row count): a fixed grid strides over the
+// live units; a grid sized for every possible row tile would spend most of its workgroups on
+// the count load alone. Otherwise one unit per workgroup.
+template <int DT, int D, bool STRIDED>
+__global__ __launch_bounds__(256) void attn_merge_kernel(const AttnBatch batch) {
+  __shared__ int red[4];
+  AttnArgs a = batch.a;
+  const int64_t mb = select_request(batch, a, blockIdx.x, true);
+  const int TR = a.tile_rows;
+  const int64_t rows_kv = attn_num_rows(a) * a.group;
+  const int64_t n_tiles_live = (rows_kv + TR - 1) / TR;
+  if (!STRIDED) {
+    merge_unit<DT, D>(a, mb, n_tiles_live, rows_kv, red);
+    return;
+  }
+  apply_device_split(a, n_tiles_live);
+  const int64_t units = n_tiles_live * a.num_kv_heads * (TR / 32);
+  for (int64_t u = mb; u < units; u += gridDim.x) {
+    merge_unit<DT, D>(a, u, n_tiles_live, rows_kv, red);
+    __syncthreads();  // red[] is reused by the next unit
+  }
+}
 template <int DT>
 __device__ __forceinline__ float load_elem(const char* p, int64_t idx) {
   if (DT == SB_DTYPE_F32) return reinterpret_cast<const float*>(p)[idx];
@@ -1197,15 +1261,6 @@ __global__ __launch_bounds__(64) void attn_valu_kernel(AttnArgs a) {
 
 namespace {
 
-// Resident workgroups of the MFMA kernel on 256 CUs (one 4-wave workgroup per CU with two
-// row groups per wave, SB_ATTN_OCCUPANCY with one), and how many work items per slot the
-// split aims for.
-constexpr int kResidentSlots = kRowGroups == 1 ? 256 * SB_ATTN_OCCUPANCY * 4 / kWaves : 256;
-#ifndef SB_ATTN_ITEMS_PER_SLOT
-#define SB_ATTN_ITEMS_PER_SLOT 1
-#endif
-constexpr int kItemsPerSlot = SB_ATTN_ITEMS_PER_SLOT;
-
 // Launches the MFMA attention kernel instantiated for the addressing of `args.a`.
 #define SB_ATT_LAUNCH(DT, D, grid, st, args)                                              \
   do {                                                                                    \
@@ -1243,25 +1298,33 @@ Plan make_plan(int64_t rows_upper, int64_t group, int64_t num_kv_heads, int64_t 
   Plan pl{};
   pl.tile_rows = kWaveRows * kRowGroups * kWaves;
   pl.n_tiles = (rows_upper * group + pl.tile_rows - 1) / pl.tile_rows;
-  const int64_t kv_pad = (kv_len + kTileKeys - 1) / kTileKeys * kTileKeys;
-  // Items no longer than the average work per slot (assuming the rows' key ranges average
-  // half the context), so that longest-first scheduling balances the CUs.
-  int64_t ks = pl.n_tiles * num_kv_heads * (kv_len / 2) / (kResidentSlots * kItemsPerSlot);
-  ks = ks / kTileKeys * kTileKeys;
-  if (ks < 512) ks = 512;
-  if (paged) {
-    const int64_t cap = static_cast<int64_t>(kBtLds) * block_size / kTileKeys * kTileKeys;
-    if (ks > cap) ks = cap;
-  }
-  if (ks > kv_pad) ks = kv_pad;
-  if (ks < kTileKeys) ks = kTileKeys;
-  const int64_t chunks = (kv_len + ks - 1) / ks;
-  pl.ksplit = static_cast<int>(ks);
-  pl.max_chunks = static_cast<int>(chunks < 1 ? 1 : chunks);
+  const KeySplit sp = key_split(pl.n_tiles, num_kv_heads, kv_len, block_size, paged);
+  pl.ksplit = sp.ksplit;
+  pl.max_chunks = sp.max_chunks;
   if (pl.max_chunks > 1)
     pl.part_bytes =
         num_kv_heads * pl.n_tiles * pl.max_chunks * pl.tile_rows * (head_dim + 2) * 4;
   return pl;
+}
+
+// Split of a call whose row count is known only on the device (dense drop-in): the kernels
+// derive it from that count with key_split; the launch covers the largest item count and
+// the workspace the largest partials over every possible count of row tiles.
+constexpr int64_t kMergeStrideGrid = 2048;  // merge workgroups of a device-split call
+struct DeviceSplitBounds {
+  int64_t items;      // workgroups of the attention launch
+  int64_t part_rows;  // flattened rows of split-key partials (O rows, then m/l pairs)
+};
+DeviceSplitBounds device_split_bounds(int64_t n_tiles_upper, int64_t num_kv_heads,
+                                      int64_t kv_len, int tile_rows) {
+  DeviceSplitBounds b{0, 0};
+  for (int64_t t = 1; t <= n_tiles_upper; ++t) {
+    const KeySplit sp = key_split(t, num_kv_heads, kv_len, 1, false);
+    b.items = std::max<int64_t>(b.items, t * num_kv_heads * sp.max_chunks);
+    if (sp.max_chunks > 1)
+      b.part_rows = std::max<int64_t>(b.part_rows, num_kv_heads * t * sp.max_chunks * tile_rows);
+  }
+  return b;
 }
 
 int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upper,
@@ -1277,25 +1340,39 @@ int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upp
     a.max_chunks = pl.max_chunks;
     a.n_tiles = pl.n_tiles;
     a.tile_rows = pl.tile_rows;
-    if (pl.part_bytes > 0) {
-      if (!workspace || workspace_bytes < pl.part_bytes)
+    int64_t part_rows = pl.part_bytes > 0 ? a.num_kv_heads * pl.n_tiles * pl.max_chunks *
+                                                pl.tile_rows
+                                          : 0;
+    int64_t gx = pl.n_tiles * a.num_kv_heads * pl.max_chunks;
+    if (a.device_split) {
+      // The kernels split by the device row count: cover every count that can occur.
+      const DeviceSplitBounds b =
+          device_split_bounds(pl.n_tiles, a.num_kv_heads, a.kv_len, pl.tile_rows);
+      part_rows = b.part_rows;
+      gx = b.items;
+    }
+    if (part_rows > 0) {
+      const int64_t need = part_rows * (a.head_dim + 2) * 4;
+      if (!workspace || workspace_bytes < need)
         return fail(fn, "workspace too small for the split-key partials");
       a.part_o = static_cast<float*>(workspace);
-      a.part_ml = a.part_o + a.num_kv_heads * pl.n_tiles * pl.max_chunks * pl.tile_rows *
-                                 static_cast<int64_t>(a.head_dim);
+      a.part_ml = a.part_o + part_rows * static_cast<int64_t>(a.head_dim);
     }
-    const int64_t gx = pl.n_tiles * a.num_kv_heads * pl.max_chunks;
     if (gx > 0x7fffffff) return fail(fn, "grid too large");
     dim3 grid(static_cast<unsigned>(gx));
-    dim3 mgrid(static_cast<unsigned>(pl.n_tiles * a.num_kv_heads * (pl.tile_rows / 32)));
+    int64_t mx = pl.n_tiles * a.num_kv_heads * (pl.tile_rows / 32);
+    if (a.device_split) mx = std::min<int64_t>(mx, kMergeStrideGrid);  // strided merge
+    dim3 mgrid(static_cast<unsigned>(mx));
     AttnBatch one{};
     one.a = a;
     one.num_reqs = 0;
 #define SB_ATT_CASE(DT, D)                                                              \
   if (dtype == DT && a.head_dim == D) {                                                 \
     SB_ATT_LAUNCH(DT, D, grid, st, one);                                               \
-    if (pl.max_chunks > 1)                                                              \
-      SB_LAUNCH("attn_merge", (attn_merge_kernel<DT, D>), mgrid, dim3(256), st, one);   \
+    if (part_rows > 0 && a.device_split)                                                \
+      SB_LAUNCH("attn_merge", (attn_merge_kernel<DT, D, true>), mgrid, dim3(256), st, one); \
+    else if (part_rows > 0)                                                             \
+      SB_LAUNCH("attn_merge", (attn_merge_kernel<DT, D, false>), mgrid, dim3(256), st, one); \
     return check_launch(fn);                                                            \
   }
     SB_ATT_CASE(SB_DTYPE_BF16, 128)
@@ -1436,7 +1513,7 @@ int launch_attention_varlen(const char* fn, AttnArgs a, int32_t dtype, int64_t n
 #define SB_ATT_VCASE(DT, D)                                                             \
   if (dtype == DT && a.head_dim == D) {                                                 \
     SB_ATT_LAUNCH(DT, D, grid, st, b);                                                 \
-    if (split) SB_LAUNCH("attn_merge", (attn_merge_kernel<DT, D>), mgrid, dim3(256), st, b); \
+    if (split) SB_LAUNCH("attn_merge", (attn_merge_kernel<DT, D, false>), mgrid, dim3(256), st, b); \
     const int rc = check_launch(fn);                                                    \
     if (rc) return rc;                                                                  \
     continue;                                                                           \
@@ -1474,9 +1551,14 @@ extern "C" int64_t sb_partial_prefill_attention_workspace_size(int64_t num_heads
                                                                int64_t seq_len,
                                                                int64_t head_dim,
                                                                int32_t dtype) {
-  // positions (S) + count, rounded to 256 bytes, then the split-key partials.
+  // positions (S) + count, rounded to 256 bytes, then the split-key partials of the largest
+  // split the device row count can select.
   const int64_t idx = ((seq_len + 1) * 4 + 255) / 256 * 256;
-  return idx + part_bytes_for(dtype, seq_len, 1, num_heads, seq_len, head_dim, 1, false);
+  if (!mfma_path(dtype, head_dim) || num_heads <= 0 || seq_len <= 0) return idx;
+  const int tile_rows = kWaveRows * kRowGroups * kWaves;
+  const DeviceSplitBounds b =
+      device_split_bounds((seq_len + tile_rows - 1) / tile_rows, num_heads, seq_len, tile_rows);
+  return idx + b.part_rows * (head_dim + 2) * 4;
 }
 
 extern "C" int sb_partial_prefill_attention(void* out, const void* q, const void* k,
@@ -1548,6 +1630,7 @@ extern "C" int sb_partial_prefill_attention(void* out, const void* q, const void
   a.head_dim = static_cast<int>(head_dim);
   a.scale = scale;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.device_split = 1;  // the row count is known on the device only
   const bool aligned16 =
       vec_bytes({reinterpret_cast<int64_t>(q), reinterpret_cast<int64_t>(k),
                  reinterpret_cast<int64_t>(v), reinterpret_cast<int64_t>(out), qs[0] * es,

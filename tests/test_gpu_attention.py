@@ -64,6 +64,22 @@ def test_dense_mfma(dev, dtype, head_dim, seq_len):
     assert_attn_close(got, want)
 
 
+@pytest.mark.parametrize("n_rows", [1, 40, 700])
+def test_dense_split_from_device_row_count(dev, n_rows):
+    """The dense drop-in knows its row count only on the device, so its kernels derive the
+    key-range split from that count: a few rows of a long context run in many chunks (40
+    rows of 8192 keys: 512-key chunks, merged by the general path past four chunks), more
+    rows in fewer; the launch and the workspace cover every count."""
+    h, s = 4, 8192
+    q, k, v = (randn((h, s, 128), torch.bfloat16, 320 + i) for i in range(3))
+    mask = torch.zeros(s, dtype=torch.bool)
+    mask[torch.randperm(s, generator=gen(323 + n_rows))[:n_rows]] = True
+    mask[s - 1] = True
+    got = tk.partial_prefill_attention(q.to(dev), k.to(dev), v.to(dev), mask.to(dev))
+    assert torch.all(got.cpu()[:, ~mask] == 0)
+    assert_attn_close(got, ref.partial_prefill_attention(q, k, v, mask))
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_dense_other_head_dim(dev, dtype):
     """head_dim 96 takes the general (non-MFMA) kernel."""
