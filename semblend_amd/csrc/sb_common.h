@@ -192,25 +192,51 @@ template <int kUnused = 0>
 __global__ __launch_bounds__(1024) void mask_compact_kernel(const uint8_t* mask, int64_t n,
                                                             int32_t* pos_out,
                                                             int32_t* count_out) {
-  __shared__ int wsum[16];
+  // Each thread takes 16 consecutive mask bytes per round (one 16-byte load when the mask is
+  // 16-byte aligned), so a round covers 16384 positions; a wave scan of the per-thread
+  // counts and the per-wave totals in LDS give every thread its output offset.
+  constexpr int kPer = 16;
+  constexpr int kThreadsC = 1024;
+  __shared__ int wsum[kThreadsC / 64];
   __shared__ int base;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool aligned = (reinterpret_cast<uintptr_t>(mask) & 15) == 0;
   if (tid == 0) base = 0;
   __syncthreads();
-  for (int64_t c0 = 0; c0 < n; c0 += 1024) {
-    const int64_t i = c0 + tid;
-    const bool f = i < n && mask[i] != 0;
-    const uint64_t b = __ballot(f);
-    const int pre = __popcll(b & ((uint64_t{1} << lane) - 1));
-    if (lane == 0) wsum[wave] = __popcll(b);
+  for (int64_t c0 = 0; c0 < n; c0 += static_cast<int64_t>(kThreadsC) * kPer) {
+    const int64_t i0 = c0 + static_cast<int64_t>(tid) * kPer;
+    uint32_t bits = 0;  // bit k: mask[i0 + k] != 0
+    if (aligned && i0 + kPer <= n) {
+      const uint4 v = *reinterpret_cast<const uint4*>(mask + i0);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) bits |= (((w[q] >> (8 * b)) & 0xffu) != 0u) << (4 * q + b);
+    } else {
+      for (int k = 0; k < kPer; ++k)
+        if (i0 + k < n && mask[i0 + k] != 0) bits |= 1u << k;
+    }
+    const int cnt = __popc(bits);
+    int incl = cnt;  // inclusive scan over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
     __syncthreads();
-    int off = base;
+    int off = base + incl - cnt;
     for (int w = 0; w < wave; ++w) off += wsum[w];
-    if (f) pos_out[off + pre] = static_cast<int32_t>(i);
+    while (bits) {
+      const int k = __ffs(bits) - 1;
+      pos_out[off++] = static_cast<int32_t>(i0 + k);
+      bits &= bits - 1;
+    }
     __syncthreads();
     if (tid == 0) {
       int t = 0;
-      for (int w = 0; w < 16; ++w) t += wsum[w];
+      for (int w = 0; w < kThreadsC / 64; ++w) t += wsum[w];
       base += t;
     }
     __syncthreads();
