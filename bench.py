@@ -64,11 +64,11 @@ KERNELS = ("attn_mfma", "attn_merge", "move_rows", "rope_rows", "rope_index", "f
 # this script, scaled by what the same counters read for the 1 GiB copy of copy_ceiling()
 # (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); kernel changes call for a new measurement.
 MEASURED_TRAFFIC_BYTES = {
-    "attn_mfma": (2 * 72792 + 40895) * 1024,
-    "move_rows": (2 * 391166 + 779860) * 1024,
-    "rope_rows": (2 * 114830 + 229384) * 1024,
+    "attn_mfma": (2 * 72949 + 40897) * 1024,
+    "move_rows": (2 * 391166 + 779861) * 1024,
+    "rope_rows": (2 * 114830 + 229388) * 1024,
 }
-MEASURED_TRAFFIC_SOURCE = ("rocprofv3 FETCH_SIZE / WRITE_SIZE passes at commit f4f7826, "
+MEASURED_TRAFFIC_SOURCE = ("rocprofv3 FETCH_SIZE / WRITE_SIZE passes at commit 3d8b7a9, "
                            "profiles/kv_reuse_7b_16k_hbm_traffic.md")
 
 
