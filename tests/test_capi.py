@@ -117,6 +117,24 @@ def test_workspace_size_queries(dtype, expect_split):
     assert dense >= 1001 * 4
 
 
+@pytest.mark.parametrize("heads,seq_len", [(28, 16384), (4, 3000), (32, 8192)])
+def test_dense_workspace_covers_every_row_count(heads, seq_len):
+    """The dense drop-in splits its key range by the row count its kernels find on the device,
+    so its workspace must hold the split-key partials of every count. The requirement of one
+    count is the library's own single-call plan for that many rows, read through the paged
+    query (block size 16: its block-table cap of 16384 keys does not bind at these lengths,
+    so the two plans coincide)."""
+    idx = ((seq_len + 1) * 4 + 255) // 256 * 256
+    dense = _lib.size_query("sb_partial_prefill_attention_workspace_size", heads, seq_len, 128, 2)
+    need = 0
+    for rows in list(range(1, seq_len + 1, 128)) + [seq_len]:
+        need = max(need, _lib.size_query("sb_partial_attention_paged_workspace_size", rows, heads,
+                                         heads, 128, 16, seq_len // 16 if seq_len % 16 == 0
+                                         else seq_len // 16 + 1, 2))
+    assert need > 0
+    assert dense - idx >= need
+
+
 def test_kernel_timing_log_without_launches():
     _lib.kernel_timing(True)
     assert _lib.kernel_time("attn_mfma") == (0.0, 0)
