@@ -397,6 +397,171 @@ def check_projection_and_prefill(impl) -> None:
     assert torch.all(out[~cm] == 0)
 
 
+# ------------------------------------------------------------------------------------------
+# Orchestrator values (partial_prefill, triton_kernels.py:809-923)
+# ------------------------------------------------------------------------------------------
+
+def _prefill_values_case(seed, dtype):
+    """Eight positions: computed {0, 2, 5, 7}; reused {1, 3, 4} from donor positions
+    {0, 2, 1}; position 6 is a reuse position that no pair covers (its K/V stay zero). Three
+    layers of distinct donor rows; hidden size equal to heads x head_dim, so the output
+    projection is square and a transposed one changes values rather than shapes."""
+    seq, h, d, layers = 8, 2, 4, 3
+    hid = h * d
+    hs = (0.5 * _randn((seq, hid), seed)).to(dtype)
+    donor = _randn((layers, 2, h, 5, d), seed + 1, dtype)
+    wo = (0.5 * _randn((hid, h * d), seed + 2)).to(dtype)
+    dp = torch.tensor([0, 2, 1], dtype=torch.int32)
+    tp = torch.tensor([1, 3, 4], dtype=torch.int32)
+    cm = torch.ones(seq, dtype=torch.bool)
+    cm[torch.tensor([1, 3, 4, 6])] = False
+    return hs, donor, wo, dp, tp, cm, h, d
+
+
+def _prefill_float64(hs, donor, wqkv, wo, dp, tp, cm, h, d, bqkv=None, bo=None, scale=None):
+    """The orchestrator's result computed independently in float64 with numpy, from what the
+    reference's stages state (triton_kernels.py:786-799, 831-897): the projection of every
+    computed position is rounded once to the input dtype; each computed row attends
+    causally, per head, over keys whose K/V are the new projection at computed positions,
+    layer 0's donor row at reused positions a pair covers, and zero elsewhere; heads are
+    concatenated and multiplied by the output projection; reuse rows are zero. Returns the
+    output (float64) and the expected new K and V of every computed position."""
+    dtype = hs.dtype
+    seq, hid = hs.shape
+    f = h * d
+    x = hs.double().numpy()
+    w = wqkv.double().numpy()
+    proj = x @ w.T
+    if bqkv is not None:
+        proj = proj + bqkv.double().numpy()[None, :]
+    # rounded as an fp32 GEMM whose result is cast to the input dtype
+    proj = torch.from_numpy(proj).float().to(dtype).double().numpy()
+    comp = cm.numpy().astype(bool)
+    donor64 = donor.double().numpy()
+    src = {int(t): int(s) for s, t in zip(dp.tolist(), tp.tolist())}
+    keys = np.zeros((seq, h, d))
+    vals = np.zeros((seq, h, d))
+    for p in range(seq):
+        if comp[p]:
+            keys[p] = proj[p, f:2 * f].reshape(h, d)
+            vals[p] = proj[p, 2 * f:3 * f].reshape(h, d)
+        elif p in src:
+            keys[p] = donor64[0, 0, :, src[p], :]
+            vals[p] = donor64[0, 1, :, src[p], :]
+    sc = 1.0 / math.sqrt(d) if scale is None else scale
+    wo64 = wo.double().numpy()
+    out = np.zeros((seq, wo64.shape[0]))
+    for i in range(seq):
+        if not comp[i]:
+            continue
+        flat = np.zeros(f)
+        for hh in range(h):
+            qv = proj[i, hh * d:(hh + 1) * d]
+            s = np.array([sc * float(np.dot(qv, keys[k, hh])) for k in range(i + 1)])
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            flat[hh * d:(hh + 1) * d] = sum(p[k] * vals[k, hh] for k in range(i + 1))
+        out[i] = wo64 @ flat
+        if bo is not None:
+            out[i] += bo.double().numpy()
+    return out, keys, vals
+
+
+def check_partial_prefill_selector_closed_form(impl) -> None:
+    """Selector weights make every stage identifiable and exact. Q weights are zero, so every
+    computed row weights its keys 0..i equally; K features copy hidden element c, V features
+    copy -2 x element (c + 1) mod hidden (exact in every dtype). Then:
+      * the row at position 0 attends to itself only: out[0] = W_o . v_new[0] + b;
+      * out[i] = W_o . mean(V over keys 0..i) + b, where V is the new projection at computed
+        positions, layer 0's donor row at covered reuse positions, zero at position 6;
+      * every layer's cache holds the new K (plane 0) and V (plane 1) at computed positions,
+        the layer's own donor rows at covered reuse positions, zeros at position 6;
+      * reuse rows of the output are zero."""
+    for dtype in (torch.float32, torch.bfloat16):
+        hs, donor, wo, dp, tp, cm, h, d = _prefill_values_case(300, dtype)
+        seq, hid = hs.shape
+        f = h * d
+        w = torch.zeros((3 * f, hid))
+        for c in range(f):
+            w[f + c, c] = 1.0
+            w[2 * f + c, (c + 1) % hid] = -2.0
+        w = w.to(dtype)
+        bo = (0.25 * _randn((hid,), 303)).to(dtype)
+        out, kv, computed, reused, ratio = impl.partial_prefill(hs, donor, w, wo, dp, tp, cm,
+                                                                h, d, output_bias=bo)
+        assert (computed, reused) == (4, 4) and abs(ratio - 0.5) < 1e-12
+        x = hs.double()
+        k_new = x[:, :f].reshape(seq, h, d)
+        v_new = -2.0 * torch.roll(x, -1, dims=1)[:, :f].reshape(seq, h, d)
+        merged_v = torch.zeros((seq, h, d), dtype=torch.float64)
+        for p in range(seq):
+            if bool(cm[p]):
+                merged_v[p] = v_new[p]
+        for s, t in zip(dp.tolist(), tp.tolist()):
+            merged_v[t] = donor[0, 1, :, s].double()
+        wo64, bo64 = wo.double(), bo.double()
+        # closed form of row 0, then of every computed row
+        row0 = wo64 @ v_new[0].reshape(-1) + bo64
+        want = torch.zeros((seq, hid), dtype=torch.float64)
+        for i in torch.where(cm)[0].tolist():
+            want[i] = wo64 @ merged_v[:i + 1].mean(dim=0).reshape(-1) + bo64
+        assert torch.allclose(want[0], row0)
+        eps = 2.0 ** -20 if dtype == torch.float32 else 2.0 ** -8
+        bound = (wo64.abs() @ merged_v.abs().amax(dim=0).reshape(-1) + bo64.abs()) * eps
+        err = (out.double() - want).abs()
+        assert bool((err <= bound[None, :]).all()), f"{dtype}: output max error {err.max()}"
+        assert torch.all(out[~cm] == 0)
+        # the cache of every layer
+        for layer in range(donor.shape[0]):
+            for p in range(seq):
+                if bool(cm[p]):
+                    assert torch.equal(kv[layer, 0, :, p].double(), k_new[p])
+                    assert torch.equal(kv[layer, 1, :, p].double(), v_new[p])
+            for s, t in zip(dp.tolist(), tp.tolist()):
+                assert torch.equal(kv[layer, :, :, t], donor[layer, :, :, s])
+            assert not bool(kv[layer, :, :, 6].any())
+
+
+def check_partial_prefill_float64(impl) -> None:
+    """Random weights and biases (Q, K and V all live, non-default scale): the oracle's
+    output within fp32 rounding (fp32) or one ulp plus carried projection rounding (bf16)
+    of the float64 computation above, and the new K/V in every layer equal to the projection
+    rounded once."""
+    for dtype, seed in ((torch.float32, 310), (torch.bfloat16, 320)):
+        hs, donor, wo, dp, tp, cm, h, d = _prefill_values_case(seed, dtype)
+        seq, hid = hs.shape
+        f = h * d
+        wqkv = (0.5 * _randn((3 * f, hid), seed + 5)).to(dtype)
+        bqkv = (0.25 * _randn((3 * f,), seed + 6)).to(dtype)
+        bo = (0.25 * _randn((hid,), seed + 7)).to(dtype)
+        out, kv, *_ = impl.partial_prefill(hs, donor, wqkv, wo, dp, tp, cm, h, d,
+                                           qkv_bias=bqkv, output_bias=bo, scale=0.3)
+        want, keys, vals = _prefill_float64(hs, donor, wqkv, wo, dp, tp, cm, h, d, bqkv, bo,
+                                            scale=0.3)
+        want = torch.from_numpy(want)
+        scale_ref = wo.double().abs() @ torch.from_numpy(np.abs(vals).max(axis=0)).reshape(-1)
+        if dtype == torch.float32:
+            tol = 1e-5 * scale_ref[None, :] + 1e-6
+        else:
+            ulp = 2.0 ** (torch.floor(torch.log2(want.abs().clamp_min(2.0 ** -14))) - 7)
+            tol = ulp + 2.0 ** -10 * scale_ref[None, :]
+        err = (out.double() - want).abs()
+        assert bool((err <= tol).all()), f"{dtype}: output max error {err.max()}"
+        # new K/V: bf16 rows equal the rounded projection (these seeds hold no rounding
+        # ties); fp32 rows within fp32 rounding of sum |x w| + |b|
+        dot = hs.double().abs() @ wqkv.double().abs().T + bqkv.double().abs()
+        for layer in range(donor.shape[0]):
+            for p in torch.where(cm)[0].tolist():
+                for plane, want_rows, lo in ((0, keys, f), (1, vals, 2 * f)):
+                    got = kv[layer, plane, :, p].double()
+                    exp = torch.from_numpy(want_rows[p])
+                    if dtype == torch.float32:
+                        bar = 2.0 ** -21 * dot[p, lo:lo + f].reshape(h, d)
+                        assert bool(((got - exp).abs() <= bar).all())
+                    else:
+                        assert torch.equal(got, exp)
+
+
 
 # ------------------------------------------------------------------------------------------
 # Multi-donor (composite) scatter: concatenation identities
@@ -568,6 +733,8 @@ ALL_CHECKS = [
     check_attention_golden,
     check_gqa_matches_dense,
     check_projection_and_prefill,
+    check_partial_prefill_selector_closed_form,
+    check_partial_prefill_float64,
     check_composite_concatenation,
     check_composite_rope_concatenation,
     check_qkv_projection_mha,

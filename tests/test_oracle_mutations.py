@@ -201,6 +201,50 @@ def _proj_rope_q_skipped(hs, w, pos, kv_cache, bt, h, hkv, d, qkv_bias=None, rop
     return ref.qkv_project_paged(hs, w, pos, kv_cache.clone(), bt, h, hkv, d, qkv_bias, None)
 
 
+def _prefill_mutant(kind):
+    """The orchestrator (triton_kernels.py:809-923) with one planted mistake of ``kind``."""
+
+    def run(hidden_states, donor_kv, qkv_weight, output_projection, donor_positions,
+            target_positions, compute_mask, num_heads, head_dim, qkv_bias=None,
+            output_bias=None, scale=None):
+        seq, layers = hidden_states.shape[0], donor_kv.shape[0]
+        h, d = num_heads, head_dim
+        scale = 1.0 / math.sqrt(d) if scale is None else scale
+        target = torch.zeros((layers, 2, h, seq, d), dtype=hidden_states.dtype)
+        ref.scatter_donor_kv(target, donor_kv, donor_positions, target_positions)
+        qkv = ref.masked_qkv_projection(hidden_states, qkv_weight, compute_mask, qkv_bias).float()
+        if kind == "heads_major_split":
+            qkv = qkv.view(seq, h, 3, d)
+            q_new, k_new, v_new = (qkv[:, :, i].permute(1, 0, 2) for i in range(3))
+        else:
+            qkv = qkv.view(seq, 3, h, d)
+            q_new, k_new, v_new = (qkv[:, i].permute(1, 0, 2) for i in range(3))
+        comp = torch.where(compute_mask)[0]
+        src_layer = layers - 1 if kind == "last_layer_attention" else 0
+        mk = target[src_layer, 0].float().clone()
+        mv = target[src_layer, 1].float().clone()
+        if kind != "new_kv_not_merged":
+            mk[:, comp] = k_new[:, comp]
+            mv[:, comp] = v_new[:, comp]
+        attn = ref.partial_prefill_attention(q_new, mk, mv, compute_mask, scale)
+        flat = attn.permute(1, 0, 2).reshape(seq, h * d)
+        wo = output_projection.float()
+        if kind == "output_projection_transposed":
+            wo = wo.t()
+        out = torch.nn.functional.linear(
+            flat, wo, output_bias.float() if output_bias is not None else None)
+        out = out.to(hidden_states.dtype)
+        out[torch.where(~compute_mask)[0]] = 0.0
+        kw, vw = (v_new, k_new) if kind == "kv_swapped_in_writeback" else (k_new, v_new)
+        for layer in range(layers):
+            target[layer, 0, :, comp] = kw[:, comp].to(target.dtype)
+            target[layer, 1, :, comp] = vw[:, comp].to(target.dtype)
+        computed = int(compute_mask.sum())
+        return out, target, computed, seq - computed, computed / seq if seq else 1.0
+
+    return run
+
+
 FUNCTION_MUTANTS = {
     "rope_delta_reversed": {"rope_correct_k": _rope_k_delta_reversed},
     "attention_causal_off_by_one": {"partial_prefill_attention": _attn_off_by_one},
@@ -216,7 +260,16 @@ FUNCTION_MUTANTS = {
     "projection_kv_interleaved_per_head": {"qkv_project_paged": _proj_kv_interleaved_per_head},
     "projection_rope_on_v": {"qkv_project_paged": _proj_rope_on_v},
     "projection_rope_q_skipped": {"qkv_project_paged": _proj_rope_q_skipped},
+    **{f"prefill_{k}": {"partial_prefill": _prefill_mutant(k)}
+       for k in ("heads_major_split", "new_kv_not_merged", "last_layer_attention",
+                 "output_projection_transposed", "kv_swapped_in_writeback")},
 }
+
+
+def test_prefill_mutant_harness_is_faithful():
+    """The mutant harness with no mistake planted passes every check (so each mutant's
+    failure comes from its planted mistake)."""
+    assert _failures(_ns(partial_prefill=_prefill_mutant("none"))) == []
 
 
 @pytest.mark.parametrize("name", sorted(FUNCTION_MUTANTS))
