@@ -24,6 +24,9 @@ SB_ERR_INVALID_ARGUMENT = 100001
 SB_SCATTER_REPEATED_DONOR_ROWS = 1
 # Most positions the in-place delta RoPE takes by value in its launch (host arrays).
 SB_INLINE_POSITIONS_MAX = 256
+# Constant RoPE deltas must lie strictly within +-2^31 (the C ABI's check; the kernels'
+# sin/cos reduce angles below 2^32 exactly).
+MAX_ROPE_DELTA = 1 << 31
 SB_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 _vp = ctypes.c_void_p
@@ -244,14 +247,30 @@ def on_device(device: torch.device):
     return torch.cuda.device(device)
 
 
+# Pinned staging buffers of host-to-device copies recorded into a HIP graph: every replay
+# copies from the same host address again, so they are kept for the life of the process.
+_CAPTURED_UPLOADS: list[torch.Tensor] = []
+
+
+def pinned_upload(host: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """Device copy of a contiguous host tensor, staged through pinned memory and enqueued on
+    the current stream without blocking the host. Outside graph capture torch's pinned-memory
+    cache keeps the staging block until the copy has run and then reuses it; while the
+    current stream is capturing, the copy becomes a graph node that reads the block at every
+    replay, so the block is kept instead (never returned to the cache)."""
+    pinned = host.pin_memory()
+    out = pinned.to(device, non_blocking=True)
+    if torch.cuda.is_current_stream_capturing():
+        _CAPTURED_UPLOADS.append(pinned)
+    return out
+
+
 def upload_index(t: torch.Tensor, device: torch.device) -> torch.Tensor:
-    """int32 contiguous device copy of a host index tensor, staged through pinned memory so
-    that the copy is enqueued on the current stream without blocking the host (torch's
-    pinned-memory cache keeps the staging block until the copy has run)."""
+    """int32 contiguous device copy of a host index tensor (``pinned_upload``)."""
     host = t.to(torch.int32).contiguous()
     if host.numel() == 0:
         return torch.empty(host.shape, dtype=torch.int32, device=device)
-    return host.pin_memory().to(device, non_blocking=True)
+    return pinned_upload(host, device)
 
 
 def as_index(t, device: torch.device) -> torch.Tensor:

@@ -174,8 +174,9 @@ template <> struct ByteVec<1> { using T = uint8_t; };
 // values a correctly rounded libm returns, which torch's CPU kernels also produce for all but
 // rare arguments. Matching them matters where e*c - o*s cancels: for an output of ~1e-6 from
 // O(1) inputs, a one-ulp difference in cos or sin is several bf16 ulps of the result.
-// x is a RoPE angle (an int32 position or position difference times an inverse frequency
-// <= 1), so |x| < 2^31, the range of sincos_cw.
+// x is a RoPE angle (an int32 position, or an int32 target minus a valid donor position, or a
+// constant delta below 2^31, times an inverse frequency <= 1), so |x| < 2^32, the range of
+// sincos_cw.
 __device__ __forceinline__ void sincos_rn(float x, float* s, float* c) {
   double sd, cd;
   sincos_cw(static_cast<double>(x), &sd, &cd);

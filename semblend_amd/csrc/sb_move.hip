@@ -273,6 +273,9 @@ __device__ __forceinline__ void nope_pairs(float* f, const float* cs, const floa
 // argument block), so a short host list reaches the kernel without a host-to-device copy.
 // Other launches pass the empty InlineArg<false>.
 constexpr int kInlinePositions = SB_INLINE_POSITIONS_MAX;
+// Constant RoPE deltas are int64 on the ABI; the angle delta * inv_freq (inv_freq[0] = 1)
+// must stay within the range sincos_cw reduces exactly.
+constexpr int64_t kMaxRopeDelta = int64_t{1} << 31;
 template <bool INLINE> struct InlineArg {};
 template <> struct InlineArg<true> {
   int32_t pos[kInlinePositions];
@@ -354,7 +357,9 @@ void move_rows_kernel(MoveArgs a, InlineArg<INLINE> ix) {
   if (ROT == ROT_CONST && repeat) reps = repeat[i];
 
   float ang_a = 0.f, ang_b = 0.f;  // angle multipliers (fp32, as torch computes them)
-  if (ROT == ROT_DELTA) ang_a = static_cast<float>(dst_pos[i] - src_pos[i]);
+  // position differences in 64 bits (int32 - int32 may not fit 32): |t - d| < 2^32
+  if (ROT == ROT_DELTA)
+    ang_a = static_cast<float>(static_cast<int64_t>(dst_pos[i]) - src_pos[i]);
   if (ROT == ROT_CONST) ang_a = static_cast<float>(a.const_delta);
   if (ROT == ROT_NOPE) {
     ang_a = static_cast<float>(src_pos[i]);
@@ -547,7 +552,7 @@ void rope_rows_kernel(RopeRowsArgs a) {
 #pragma unroll
             for (int k = 0; k < E; ++k) f[k] = Codec<DT>::round_trip(f[k]);
           }
-          const float delta = static_cast<float>(a.tpos[p] - a.dpos[p]);
+          const float delta = static_cast<float>(static_cast<int64_t>(a.tpos[p]) - a.dpos[p]);
           float cc[NP], ss[NP];
           for (int k = 0; k < NP; ++k)
             sincos_rn(delta * a.inv_freq[j * NP + k], &ss[k], &cc[k]);
@@ -566,7 +571,8 @@ void rope_rows_kernel(RopeRowsArgs a) {
     const int64_t vofs = static_cast<int64_t>(j) * VB;
     float c[NP], sn[NP];
     if (cnt == 1) {
-      const float delta = static_cast<float>(a.tpos[first] - a.dpos[first]);
+      const float delta =
+          static_cast<float>(static_cast<int64_t>(a.tpos[first]) - a.dpos[first]);
 #pragma unroll
       for (int k = 0; k < NP; ++k) sincos_rn(delta * a.inv_freq[j * NP + k], &sn[k], &c[k]);
     }
@@ -1146,6 +1152,8 @@ int rope_delta_setup(const char* fn, void* k_plane, const int32_t* block_table,
   if ((head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
   if (block_size <= 0) return fail(fn, "block_size must be positive");
   if (ks[3] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
+  if (delta <= -kMaxRopeDelta || delta >= kMaxRopeDelta)
+    return fail(fn, "|delta| must be below 2^31 (the range of the kernels' sin/cos)");
   const int64_t es = elem_size(dtype);
   if (!make_geometry(head_dim, es,
                      {reinterpret_cast<int64_t>(k_plane), ks[0] * es, ks[1] * es, ks[2] * es},

@@ -4,13 +4,15 @@
 // to fp32. Evaluated in double precision and rounded once, the fp32 values are the correctly
 // rounded ones except when the exact value lies within about 1e-16 (relative) of a rounding
 // midpoint. A general-purpose double sincos also handles arguments up to 1e308, which takes
-// a wide reduction and many live registers; this one is limited to |x| < 2^31 (positions and
-// position differences are int32) and keeps about a dozen doubles live.
+// a wide reduction and many live registers; this one is limited to |x| < 2^32 (RoPE angles are
+// an int32 position, or a difference of two, times an inverse frequency <= 1; the difference
+// of an int32 target and a valid, non-negative donor position stays below 2^32) and keeps
+// about a dozen doubles live.
 //
 // Method: Cody-Waite argument reduction (W. J. Cody and W. Waite, "Software Manual for the
 // Elementary Functions", 1980): k = rint(x * 2/pi), r = x - k * pi/2 with pi/2 split into three
 // parts of 21 significant bits and a double tail, each subtracted with one fused multiply-add
-// (k * part is exact for |k| < 2^32). Then the Taylor series of sin and cos on
+// (k * part is exact for |k| < 2^32, which |x| < 2^32 keeps: |k| <= |x| 2/pi + 1/2). Then the Taylor series of sin and cos on
 // |r| <= pi/4 (+ rounding slack), through r^17 and r^18, whose first omitted terms are below
 // 5e-18 and 4e-21 there, and the quadrant k mod 4 picks and negates the pair.
 //

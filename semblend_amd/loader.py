@@ -118,8 +118,7 @@ class ChunkedKVLoader:
         from pinned memory on the current stream)."""
         arr, offsets = group_pairs_by_chunk(donor_positions, target_positions,
                                             self.chunk_tokens, num_chunks)
-        host = torch.from_numpy(arr).pin_memory()
-        return host.to(self.dev, non_blocking=True), offsets
+        return _lib.pinned_upload(torch.from_numpy(arr), self.dev), offsets
 
     def load(self, chunks: Sequence[torch.Tensor], donor_positions, target_positions,
              rope: bool = True) -> None:

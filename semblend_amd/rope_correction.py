@@ -475,6 +475,9 @@ def apply_rope_delta_inplace(
     """
     if delta == 0 or not positions:
         return 0
+    if not -_lib.MAX_ROPE_DELTA < int(delta) < _lib.MAX_ROPE_DELTA:
+        raise ValueError(f"apply_rope_delta_inplace: |delta| must be below 2^31, got {delta} "
+                         "(the kernels' sin/cos reduce angles below 2^32 exactly)")
     dev = _lib.require_device(kv_cache)
     shape, st = kv_cache.shape, kv_cache.stride()
     # The K plane starts at the tensor's own address in both layouts (kv index 0); strides
@@ -570,7 +573,7 @@ def _pairs_on_device(permutation, dev: torch.device) -> tuple[torch.Tensor, torc
         pairs = torch.tensor([(int(a), int(b)) for a, b in permutation],
                              dtype=torch.int32).reshape(-1, 2)
     if pairs.device.type == "cpu":
-        pairs = pairs.contiguous().pin_memory().to(dev, non_blocking=True)
+        pairs = _lib.pinned_upload(pairs.contiguous(), dev)
     else:
         pairs = pairs.to(dev)
     pairs = pairs.t().contiguous()

@@ -2,7 +2,8 @@
 // sin and cos, both rounded to float, over the RoPE angles the kernels form:
 //   mode "grid": x = (float)delta * f for every delta in [-D, D] and the 64 inverse
 //                frequencies (fp32) of head_dim 128 at bases 1e4, 5e5 and 1e6;
-//   mode "wide": 2^20 pseudo-random fp32 angles with magnitudes up to 2^31.
+//   mode "wide": 2^20 pseudo-random fp32 angles with magnitudes up to 2^32 (an int32
+//                target position minus a valid donor position, times inv_freq <= 1).
 // A float that differs from the library's is accepted only when the library's double value
 // lies within `tie` (relative) of the midpoint between the two floats; the program prints
 // the counts and exits 1 on any other difference.
@@ -52,7 +53,7 @@ int main(int argc, char** argv) {
     uint64_t st = 0x9E3779B97F4A7C15ull;
     for (int n = 0; n < (1 << 20); ++n) {
       st ^= st << 13; st ^= st >> 7; st ^= st << 17;
-      const double mag = std::ldexp(1.0, static_cast<int>(st % 31)) *
+      const double mag = std::ldexp(1.0, static_cast<int>(st % 32)) *
                          (1.0 + static_cast<double>((st >> 8) & 0xFFFFFF) / 16777216.0);
       const float x = static_cast<float>((st >> 40) & 1 ? -mag : mag);
       check_one(x, 0x1p-38);

@@ -95,6 +95,63 @@ def test_invalid_arguments_are_rejected_without_launch():
                                                fake, fake, None, 4, 1, 16, 8, fake, 4, 1, st,
                                                2, 4, None)
     assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"flags" in lib.sb_last_error_string()
+    # constant RoPE deltas beyond the kernels' sin/cos range, on both in-place entries
+    one = (ctypes.c_int32 * 1)(3)
+    for delta in (1 << 31, -(1 << 31), 1 << 40):
+        rc = lib.sb_apply_rope_delta_inplace(fake, fake, fake, None, 1, delta, fake, 1, 16, 8,
+                                             4, 1, _i64(1, 1, 1, 1), 2, None)
+        assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"2^31" in lib.sb_last_error_string()
+        rc = lib.sb_apply_rope_delta_inplace_host(fake, fake, one, None, 1, delta, fake, 1, 16,
+                                                  8, 4, 1, _i64(1, 1, 1, 1), 2, None)
+        assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"2^31" in lib.sb_last_error_string()
+
+
+def test_rope_delta_range_checked_before_dispatch():
+    """The Python entry rejects |delta| >= 2^31 before touching any tensor (so a CPU tensor
+    gets the range error, not the device error)."""
+    import torch
+
+    from semblend_amd import rope_correction as rc
+
+    kv = torch.zeros((2, 2, 1, 4, 8))
+    bt = torch.tensor([0, 1], dtype=torch.int32)
+    for delta in (1 << 31, -(1 << 31)):
+        with pytest.raises(ValueError, match="2\\^31"):
+            rc.apply_rope_delta_inplace(kv, bt, [0, 1], delta)
+    with pytest.raises(RuntimeError, match="device tensors"):
+        rc.apply_rope_delta_inplace(kv, bt, [0, 1], (1 << 31) - 1)
+
+
+def test_captured_uploads_keep_their_staging_buffer(monkeypatch):
+    """A host-to-device copy recorded into a HIP graph reads its pinned staging buffer at every
+    replay, so while the stream is capturing, pinned_upload keeps that buffer for the process
+    instead of letting torch's pinned-memory cache reuse it. The pinning and the copy are
+    replaced by CPU stand-ins here (no GPU); the bookkeeping is what is checked."""
+    import torch
+
+    staged = []
+
+    def fake_pin(self):
+        staged.append(self.clone())
+        return staged[-1]
+
+    monkeypatch.setattr(torch.Tensor, "pin_memory", fake_pin)
+    cpu = torch.device("cpu")
+    before = len(_lib._CAPTURED_UPLOADS)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    _lib.upload_index(torch.arange(5), cpu)
+    assert len(_lib._CAPTURED_UPLOADS) == before
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    out = _lib.upload_index(torch.arange(7), cpu)
+    assert len(_lib._CAPTURED_UPLOADS) == before + 1
+    assert _lib._CAPTURED_UPLOADS[-1] is staged[-1]
+    assert torch.equal(out, torch.arange(7, dtype=torch.int32))
+    from semblend_amd import rope_correction as rc
+
+    src, tgt = rc._pairs_on_device([(1, 2), (3, 4)], cpu)
+    assert len(_lib._CAPTURED_UPLOADS) == before + 2
+    assert src.tolist() == [1, 3] and tgt.tolist() == [2, 4]
+    del _lib._CAPTURED_UPLOADS[before:]
 
 
 def test_empty_calls_are_no_ops():

@@ -9,6 +9,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+import bench
 from oracle import ref_cpu as ref
 from semblend_amd import rope_correction as rc
 from semblend_amd import triton_kernels as tk
@@ -216,25 +217,31 @@ def test_paged_layers_repeated_donor_rows(dev, rope):
 
 
 def test_paged_layers_full_size_7b(dev):
-    """The timed 28-layer launch of the 7B scatter workload (13926 pairs, caches
-    [2048, 2, 4, 16, 128] bf16, donors [2, 4, 16384, 128]): every layer equals the oracle's
-    scatter of that layer bit for bit. The oracle runs on the first, a middle and the last
-    layer; the other layers are compared with the single-layer entry, whose full-size result
-    is the oracle's (test_paged_full_size_7b_layer)."""
+    """The timed 28-layer launch of the 7B scatter workload (caches [2048, 2, 4, 16, 128]
+    bf16, donors [2, 4, 16384, 128]) with the pairs bench.py builds: 64 donor chunks reused
+    in shuffled order, minus the structured recompute set (the first 256 tokens, two whole
+    chunks, the rest scattered): 13926 pairs. Every layer equals the oracle's scatter of
+    that layer bit for bit, and the single-layer entry lands the same bits."""
     L = 28
-    bt = torch.randperm(2048, generator=gen(60))[:1024].to(torch.int32)
-    dp, tp = _chunk_pairs(16384, 256, 2458, 61)
+    g = gen(60)
+    pos_r = bench.recompute_positions(g)
+    perm = torch.randperm(64, generator=g)
+    t = torch.arange(16384)
+    d = perm[t // 256] * 256 + t % 256
+    keep = torch.ones(16384, dtype=torch.bool)
+    keep[pos_r.long()] = False
+    dp, tp = d[keep].to(torch.int32), t[keep].to(torch.int32)
     assert dp.shape[0] == 13926
+    bt = torch.randperm(2048, generator=g)[:1024].to(torch.int32)
     kvs = [randn((2048, 2, 4, 16, 128), torch.bfloat16, 100 + i).to(dev) for i in range(L)]
     donors = [randn((2, 4, 16384, 128), torch.bfloat16, 200 + i).to(dev) for i in range(L)]
-    single = [k.clone() for k in kvs]
     btd, dpd, tpd = bt.to(dev), dp.to(dev), tp.to(dev)
     tk.scatter_donor_kv_paged_layers(kvs, donors, btd, dpd, tpd)
     for layer in range(L):
-        tk.scatter_donor_kv_paged(single[layer], donors[layer], btd, dpd, tpd)
-        assert torch.equal(kvs[layer].view(torch.int16), single[layer].view(torch.int16))
-    for layer in (0, 13, L - 1):
         kv0 = randn((2048, 2, 4, 16, 128), torch.bfloat16, 100 + layer)
+        single = tk.scatter_donor_kv_paged(kv0.to(dev), donors[layer], btd, dpd, tpd)
+        assert torch.equal(kvs[layer].view(torch.int16), single.view(torch.int16))
+        del single
         want = ref.scatter_donor_kv_paged(kv0, donors[layer].cpu(), bt, dp, tp)
         assert_bit_exact(kvs[layer], want)
 

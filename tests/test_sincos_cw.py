@@ -2,7 +2,7 @@
 rounded to fp32 by ``sincos_rn``) against the C library's double sin and cos, both rounded to
 float, on the CPU: every RoPE angle fp32(delta) * inv_freq for |delta| <= 65536 and the 64
 inverse frequencies of head_dim 128 at bases 1e4, 5e5 and 1e6, plus 2^20 pseudo-random fp32
-angles up to 2^31. The header is compiled for the host by g++ from tests/sincos_check.cpp.
+angles up to 2^32. The header is compiled for the host by g++ from tests/sincos_check.cpp.
 Any float that differs from the library's rounding outside a near-midpoint band fails."""
 
 from __future__ import annotations
