@@ -128,20 +128,25 @@ def delta_groups(deltas: torch.Tensor) -> list[tuple[int, list[int]]]:
             if val[s] != 0]
 
 
-def qwen05b_pipeline(mod_tk, mod_rc, inp: dict, device=None):
+def qwen05b_pipeline(mod_tk, mod_rc, inp: dict, device=None, one_call: bool = False):
     """The pipeline through the drop-in entry points (``mod_tk`` / ``mod_rc`` are the
     triton_kernels / rope_correction modules, or the oracle for both): scatter the donor into
     the paged cache, rotate every token's K in place by its delta (one
-    ``apply_rope_delta_inplace`` call per distinct delta), then causal GQA attention of the
-    recompute rows over that cache. Returns (cache, attention output)."""
+    ``apply_rope_delta_inplace`` call per distinct delta, or with ``one_call`` a single
+    ``apply_rope_deltas_inplace_layers`` call with the per-token deltas), then causal GQA
+    attention of the recompute rows over that cache. Returns (cache, attention output)."""
     c = QWEN05B
     to = (lambda t: t.to(device)) if device is not None else (lambda t: t.clone())
     kv = to(inp["cache"])
     bt = to(inp["block_table"])
     pos = to(inp["positions"])
     mod_tk.scatter_donor_kv_paged(kv, to(inp["donor"]), bt, pos, pos)
-    for dl, where in delta_groups(inp["deltas"]):
-        mod_rc.apply_rope_delta_inplace(kv, bt, where, dl, rope_base=c["theta"])
+    if one_call:
+        mod_rc.apply_rope_deltas_inplace_layers([kv], bt, inp["positions"], inp["deltas"],
+                                                rope_base=c["theta"])
+    else:
+        for dl, where in delta_groups(inp["deltas"]):
+            mod_rc.apply_rope_delta_inplace(kv, bt, where, dl, rope_base=c["theta"])
     if device is not None:
         out = mod_tk.partial_prefill_attention_paged(to(inp["q"]), kv, bt, to(inp["rows"]))
     else:
@@ -368,15 +373,19 @@ def qwen05b_section(dev: torch.device, steps: int, cpu: bool) -> dict:
     rows = inp["rows"].double()
     flops = 4.0 * c["d"] * c["hq"] * float((rows + 1).sum())
     moved = float(c["ctx"]) * 2 * c["hkv"] * c["d"] * 4 * 2
-    qwen05b_pipeline(tk, rc, inp, device=dev)
-    torch.cuda.synchronize()
-    ts = []
-    for _ in range(max(steps, 3)):
-        t0 = time.perf_counter()
-        qwen05b_pipeline(tk, rc, inp, device=dev)
+    def timed(one_call: bool) -> float:
+        qwen05b_pipeline(tk, rc, inp, device=dev, one_call=one_call)
         torch.cuda.synchronize()
-        ts.append(time.perf_counter() - t0)
-    gpu_ms = 1e3 * sorted(ts)[len(ts) // 2]
+        ts = []
+        for _ in range(max(steps, 3)):
+            t0 = time.perf_counter()
+            qwen05b_pipeline(tk, rc, inp, device=dev, one_call=one_call)
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return 1e3 * sorted(ts)[len(ts) // 2]
+
+    gpu_ms = timed(False)
+    one_ms = timed(True)
     res = {
         "workload": "Qwen2.5-0.5B one layer: 14q/2kv x 64, fp32, theta 1e6, 1024 tokens; "
                     "scatter into [128, 2, 2, 16, 64] (permuted block table), per-token "
@@ -385,6 +394,10 @@ def qwen05b_section(dev: torch.device, steps: int, cpu: bool) -> dict:
         "rope_calls": len(delta_groups(inp["deltas"])),
         "attention_flops": flops, "scatter_bytes": moved,
         "gpu": {"ms": round(gpu_ms, 3), "what": "drop-in calls incl. host work, median"},
+        "gpu_one_rope_call": {
+            "ms": round(one_ms, 3),
+            "what": "the same pipeline with the per-token deltas in one "
+                    "apply_rope_deltas_inplace_layers call (same bits), incl. host work"},
     }
     if cpu:
         from oracle import ref_cpu as ref

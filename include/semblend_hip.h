@@ -272,6 +272,39 @@ int sb_apply_rope_delta_inplace_host(void* k_plane, const int32_t* block_table,
                                      int64_t num_blocks_total, int64_t num_blocks_per_seq,
                                      const int64_t* k_strides, int32_t dtype, void* stream);
 
+/* In-place rotation of the K rows of many layers' paged caches, one delta per position, in
+ * one launch: for every layer l and i < num_positions,
+ *   K_l[bt[p / bs], h, p % bs, :] = R(deltas[i]) K_l[...],  p = positions[i].
+ * kv_layer_ptrs: device array of num_layers K-plane base addresses (16-byte aligned), all
+ * caches sharing k_strides[4] = (block, head, pos, dim) and dtype. Positions must be distinct
+ * within one call (rows are rotated concurrently); positions past the block table or in an
+ * invalid physical block are skipped. |deltas[i]| < 2^31.
+ * Replaces the per-(layer, pair) loop of apply_rope_delta_inplace calls in
+ * semblend/integration/trtllm/semblend_provider.py:305-318 and the one-call-per-delta loop
+ * over semblend_core/rope_correction.py:699-783 (apply_rope_delta_inplace). */
+int sb_apply_rope_deltas_inplace_layers(const uint64_t* kv_layer_ptrs, int64_t num_layers,
+                                        const int32_t* block_table, const int32_t* positions,
+                                        const int32_t* deltas, int64_t num_positions,
+                                        const float* inv_freq, int64_t num_heads,
+                                        int64_t block_size, int64_t head_dim,
+                                        int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                                        const int64_t* k_strides, int32_t dtype, void* stream);
+
+/* sb_apply_rope_deltas_inplace_layers with positions and deltas in HOST memory, at most
+ * SB_INLINE_POSITIONS_MAX of them: they travel in the launch's own argument block (no device
+ * buffer, no host-to-device copy; a launch recorded into a HIP graph holds them). Same results;
+ * more positions are rejected with SB_ERR_INVALID_ARGUMENT. The host arrays may be reused as
+ * soon as the call returns. Replaces the same reference loops as the device form. */
+int sb_apply_rope_deltas_inplace_layers_host(const uint64_t* kv_layer_ptrs, int64_t num_layers,
+                                             const int32_t* block_table,
+                                             const int32_t* positions, const int32_t* deltas,
+                                             int64_t num_positions, const float* inv_freq,
+                                             int64_t num_heads, int64_t block_size,
+                                             int64_t head_dim, int64_t num_blocks_total,
+                                             int64_t num_blocks_per_seq,
+                                             const int64_t* k_strides, int32_t dtype,
+                                             void* stream);
+
 /* Permutation inside a paged cache with snapshot semantics: every source row (K and V) is
  * read before any target row is written; V is copied, K rotated by (tgt - src).
  * workspace: device buffer of num_pairs * 2 * H * D elements of dtype.

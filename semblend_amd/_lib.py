@@ -35,6 +35,7 @@ _i32 = ctypes.c_int32
 _f32 = ctypes.c_float
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _i32p = ctypes.POINTER(ctypes.c_int32)
+I32P = _i32p  # host int32 arrays passed by address (numpy: arr.ctypes.data_as(I32P))
 
 # Argument signatures of every exported function (order as in include/semblend_hip.h).
 SIGNATURES: dict[str, list] = {
@@ -60,6 +61,10 @@ SIGNATURES: dict[str, list] = {
                                     _i64, _i64, _i64p, _i32, _vp],
     "sb_apply_rope_delta_inplace_host": [_vp, _vp, _i32p, _i32p, _i64, _i64, _vp, _i64, _i64,
                                          _i64, _i64, _i64, _i64p, _i32, _vp],
+    "sb_apply_rope_deltas_inplace_layers": [_vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i64,
+                                            _i64, _i64, _i64, _i64p, _i32, _vp],
+    "sb_apply_rope_deltas_inplace_layers_host": [_vp, _i64, _vp, _i32p, _i32p, _i64, _vp, _i64,
+                                                 _i64, _i64, _i64, _i64, _i64p, _i32, _vp],
     "sb_permute_paged_kv_with_rope": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                       _i64, _i64, _i64p, _i32, _vp],
     "sb_nope_permute_paged_kv": [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64,
@@ -254,15 +259,22 @@ _CAPTURED_UPLOADS: list[torch.Tensor] = []
 
 def pinned_upload(host: torch.Tensor, device: torch.device) -> torch.Tensor:
     """Device copy of a contiguous host tensor, staged through pinned memory and enqueued on
-    the current stream without blocking the host. Outside graph capture torch's pinned-memory
-    cache keeps the staging block until the copy has run and then reuses it; while the
-    current stream is capturing, the copy becomes a graph node that reads the block at every
-    replay, so the block is kept instead (never returned to the cache)."""
-    pinned = host.pin_memory()
-    out = pinned.to(device, non_blocking=True)
+    the current stream without blocking the host (torch's pinned-memory cache keeps the
+    staging block until the copy has run, then reuses it).
+
+    While the current stream is capturing a HIP graph no pinned memory can be allocated, and a
+    captured copy reads its host buffer again at every replay: a host tensor that is already
+    pinned is copied and kept for the life of the process (so the replays read the values it
+    holds now, as long as the caller does not write to it), anything else raises."""
     if torch.cuda.is_current_stream_capturing():
-        _CAPTURED_UPLOADS.append(pinned)
-    return out
+        if not host.is_pinned():
+            raise RuntimeError(
+                "host index data cannot be uploaded while the stream is capturing a HIP graph: "
+                "pass device tensors (or pinned host tensors), or make the call once before "
+                "capture")
+        _CAPTURED_UPLOADS.append(host)
+        return host.to(device, non_blocking=True)
+    return host.pin_memory().to(device, non_blocking=True)
 
 
 def upload_index(t: torch.Tensor, device: torch.device) -> torch.Tensor:

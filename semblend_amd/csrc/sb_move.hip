@@ -27,7 +27,9 @@
 namespace sb {
 
 enum RowMode : int { ROW_FLAT_POS = 0, ROW_PAGED_POS = 1, ROW_INDEX = 2, ROW_DONOR_POS = 3 };
-enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3 };
+// Rotation of K rows: none; by (destination - source position); NoPE (strip R(source), apply
+// R(destination)); by one delta for every pair; by a per-pair delta (MoveArgs::deltas).
+enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3, ROT_PAIR = 4 };
 
 // Launch shape and access hints, tuned on MI355X for the 7B-shape workloads (28 layers x
 // 4 KV heads x 128, bf16). 256-thread blocks (128/512/1024 were slower). The pair movers keep
@@ -116,6 +118,7 @@ struct MoveArgs {
   const int32_t* src_pos;  // per-pair source positions (FLAT_POS / PAGED_POS sources)
   const int32_t* dst_pos;  // per-pair destination positions
   const int32_t* repeat;   // ROT_CONST: rotations to apply per pair (nullptr = 1)
+  const int32_t* deltas;   // ROT_PAIR: per-pair delta
   const int32_t* block_table;
   int64_t block_size;
   int64_t nb_total;
@@ -279,8 +282,8 @@ constexpr int64_t kMaxRopeDelta = int64_t{1} << 31;
 template <bool INLINE> struct InlineArg {};
 template <> struct InlineArg<true> {
   int32_t pos[kInlinePositions];
-  int32_t rep[kInlinePositions];
-  int has_rep;
+  int32_t aux[kInlinePositions];  // ROT_CONST: repeat counts (when has_aux); ROT_PAIR: deltas
+  int has_aux;
 };
 static_assert(sizeof(MoveArgs) + sizeof(InlineArg<true>) <= 4096, "kernel arguments over 4 KB");
 
@@ -294,7 +297,7 @@ static_assert(sizeof(MoveArgs) + sizeof(InlineArg<true>) <= 4096, "kernel argume
 #endif
 template <int DT, int VB, int ROT, int SRCM, int DSTM, bool INLINE>
 __global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(ROT == ROT_DELTA ? SB_MOVE_ROT_WAVES : 1)))
+__attribute__((amdgpu_waves_per_eu(ROT == ROT_DELTA || ROT == ROT_PAIR ? SB_MOVE_ROT_WAVES : 1)))
 void move_rows_kernel(MoveArgs a, InlineArg<INLINE> ix) {
   constexpr int W = VB / 4;
   constexpr int E = (DT == SB_DTYPE_F32) ? W : 2 * W;
@@ -311,10 +314,12 @@ void move_rows_kernel(MoveArgs a, InlineArg<INLINE> ix) {
   const int32_t* src_pos = a.src_pos;
   const int32_t* dst_pos = a.dst_pos;
   const int32_t* repeat = a.repeat;
+  const int32_t* deltas = a.deltas;
   if constexpr (INLINE) {
     src_pos = ix.pos;
     dst_pos = ix.pos;
-    repeat = ix.has_rep ? ix.rep : nullptr;
+    repeat = (ROT == ROT_CONST && ix.has_aux) ? ix.aux : nullptr;
+    deltas = ix.aux;
   }
 
   int kv, l0, lpg;
@@ -361,6 +366,7 @@ void move_rows_kernel(MoveArgs a, InlineArg<INLINE> ix) {
   if (ROT == ROT_DELTA)
     ang_a = static_cast<float>(static_cast<int64_t>(dst_pos[i]) - src_pos[i]);
   if (ROT == ROT_CONST) ang_a = static_cast<float>(a.const_delta);
+  if (ROT == ROT_PAIR) ang_a = static_cast<float>(deltas[i]);
   if (ROT == ROT_NOPE) {
     ang_a = static_cast<float>(src_pos[i]);
     ang_b = static_cast<float>(dst_pos[i]);
@@ -661,17 +667,19 @@ int launch_move(const char* fn, const MoveArgs& a0, int32_t dtype, const Geometr
   return fail(fn, "unsupported dtype / vector width combination");
 }
 
+template <int ROT>
 int launch_rope_delta_inline(const char* fn, const MoveArgs& a0, const InlineArg<true>& ix,
-                             int32_t dtype, const Geometry& g, hipStream_t stream) {
+                             int32_t dtype, const Geometry& g, int grid_y, hipStream_t stream) {
   MoveArgs a = a0;
   a.vpr = g.vpr;
   a.tpr_log2 = g.tpr_log2;
   const int64_t rows_per_block = kThreads >> g.tpr_log2;
-  dim3 grid(static_cast<unsigned>((a.num_pairs + rows_per_block - 1) / rows_per_block));
+  dim3 grid(static_cast<unsigned>((a.num_pairs + rows_per_block - 1) / rows_per_block),
+            static_cast<unsigned>(grid_y));
 #define SB_INLINE_CASE(DT, VB)                                                            \
   if (dtype == DT && g.vb == VB) {                                                        \
     SB_LAUNCH("move_rows",                                                                \
-              (move_rows_kernel<DT, VB, ROT_CONST, ROW_PAGED_POS, ROW_PAGED_POS, true>), grid, \
+              (move_rows_kernel<DT, VB, ROT, ROW_PAGED_POS, ROW_PAGED_POS, true>), grid,   \
               dim3(kThreads), stream, a, ix);                                             \
     return check_launch(fn);                                                              \
   }
@@ -1231,10 +1239,116 @@ extern "C" int sb_apply_rope_delta_inplace_host(void* k_plane, const int32_t* bl
   std::memset(&ix, 0, sizeof(ix));
   std::memcpy(ix.pos, positions, static_cast<size_t>(num_positions) * sizeof(int32_t));
   if (repeat) {
-    std::memcpy(ix.rep, repeat, static_cast<size_t>(num_positions) * sizeof(int32_t));
-    ix.has_rep = 1;
+    std::memcpy(ix.aux, repeat, static_cast<size_t>(num_positions) * sizeof(int32_t));
+    ix.has_aux = 1;
   }
-  return launch_rope_delta_inline(fn, a, ix, dtype, g, static_cast<hipStream_t>(stream));
+  return launch_rope_delta_inline<ROT_CONST>(fn, a, ix, dtype, g, 1,
+                                             static_cast<hipStream_t>(stream));
+}
+
+namespace sb {
+namespace {
+// Checks and launch arguments of the two multi-layer per-position delta entries (positions
+// and deltas are filled in by the caller); returns the grid.y of the launch in *groups.
+int rope_deltas_layers_setup(const char* fn, const uint64_t* kv_layer_ptrs, int64_t num_layers,
+                             const int32_t* block_table, int64_t num_positions,
+                             const float* inv_freq, int64_t num_heads, int64_t block_size,
+                             int64_t head_dim, int64_t num_blocks_total,
+                             int64_t num_blocks_per_seq, const int64_t* ks, int32_t dtype,
+                             MoveArgs* out, Geometry* g, int* groups) {
+  if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
+  if (!kv_layer_ptrs || !block_table || !inv_freq || !ks) return fail(fn, "null pointer argument");
+  if (num_positions < 0 || num_layers < 0 || num_layers > 65535)
+    return fail(fn, "invalid position or layer count");
+  if ((head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
+  if (block_size <= 0) return fail(fn, "block_size must be positive");
+  if (ks[3] != 1) return fail(fn, "head_dim must be contiguous (stride 1)");
+  const int64_t es = elem_size(dtype);
+  // Per-layer tables are checked for 16-byte alignment by the caller.
+  if (!make_geometry(head_dim, es, {16, ks[0] * es, ks[1] * es, ks[2] * es}, true, g))
+    return fail(fn, "rows are not aligned for vector access");
+  // k_strides = (block, head, pos, dim): a paged side with a single kv plane.
+  const int64_t st5[5] = {ks[0], 0, ks[1], ks[2], ks[3]};
+  MoveArgs a{};
+  a.src = side_paged(nullptr, kv_layer_ptrs, st5, es);
+  a.dst = a.src;
+  a.block_table = block_table;
+  a.block_size = block_size;
+  a.nb_total = num_blocks_total;
+  a.nb_per_seq = num_blocks_per_seq;
+  a.inv_freq = inv_freq;
+  a.num_pairs = num_positions;
+  a.num_heads = static_cast<int>(num_heads);
+  a.num_layers = static_cast<int>(num_layers);
+  a.layers_per_group = layers_per_group_for(num_layers, num_positions, kGroupK);
+  a.kv_first = 0;
+  a.num_kv = 1;
+  *groups = static_cast<int>((num_layers + a.layers_per_group - 1) / a.layers_per_group);
+  *out = a;
+  return SB_OK;
+}
+}  // namespace
+}  // namespace sb
+
+// In-place RoPE of the K plane of many layers' paged caches, one delta per position, in one
+// launch: grid.x over the positions, grid.y over groups of layers (each thread evaluates the
+// cos/sin of its position once per group). Positions must be distinct within a call (their
+// rows are rotated concurrently); a caller that rotates a position several times splits the
+// list into calls with one occurrence each.
+extern "C" int sb_apply_rope_deltas_inplace_layers(
+    const uint64_t* kv_layer_ptrs, int64_t num_layers, const int32_t* block_table,
+    const int32_t* positions, const int32_t* deltas, int64_t num_positions,
+    const float* inv_freq, int64_t num_heads, int64_t block_size, int64_t head_dim,
+    int64_t num_blocks_total, int64_t num_blocks_per_seq, const int64_t* ks, int32_t dtype,
+    void* stream) {
+  const char* fn = "sb_apply_rope_deltas_inplace_layers";
+  clear_error();
+  if (num_positions == 0 || num_layers == 0 || num_heads == 0 || head_dim == 0) return SB_OK;
+  if (!positions || !deltas) return fail(fn, "null pointer argument");
+  MoveArgs a;
+  Geometry g;
+  int groups = 0;
+  const int rc = rope_deltas_layers_setup(fn, kv_layer_ptrs, num_layers, block_table,
+                                          num_positions, inv_freq, num_heads, block_size,
+                                          head_dim, num_blocks_total, num_blocks_per_seq, ks,
+                                          dtype, &a, &g, &groups);
+  if (rc) return rc;
+  a.src_pos = positions;
+  a.dst_pos = positions;
+  a.deltas = deltas;
+  return launch_move<ROT_PAIR, ROW_PAGED_POS, ROW_PAGED_POS>(fn, a, dtype, g, groups,
+                                                             static_cast<hipStream_t>(stream));
+}
+
+// The same with positions and deltas in HOST memory, at most SB_INLINE_POSITIONS_MAX: they
+// travel in the launch's argument block, so no device buffer or copy is involved (and a
+// captured launch holds them).
+extern "C" int sb_apply_rope_deltas_inplace_layers_host(
+    const uint64_t* kv_layer_ptrs, int64_t num_layers, const int32_t* block_table,
+    const int32_t* positions, const int32_t* deltas, int64_t num_positions,
+    const float* inv_freq, int64_t num_heads, int64_t block_size, int64_t head_dim,
+    int64_t num_blocks_total, int64_t num_blocks_per_seq, const int64_t* ks, int32_t dtype,
+    void* stream) {
+  const char* fn = "sb_apply_rope_deltas_inplace_layers_host";
+  clear_error();
+  if (num_positions == 0 || num_layers == 0 || num_heads == 0 || head_dim == 0) return SB_OK;
+  if (!positions || !deltas) return fail(fn, "null pointer argument");
+  if (num_positions < 0 || num_positions > kInlinePositions)
+    return fail(fn, "more positions than SB_INLINE_POSITIONS_MAX");
+  MoveArgs a;
+  Geometry g;
+  int groups = 0;
+  const int rc = rope_deltas_layers_setup(fn, kv_layer_ptrs, num_layers, block_table,
+                                          num_positions, inv_freq, num_heads, block_size,
+                                          head_dim, num_blocks_total, num_blocks_per_seq, ks,
+                                          dtype, &a, &g, &groups);
+  if (rc) return rc;
+  InlineArg<true> ix;
+  std::memset(&ix, 0, sizeof(ix));
+  std::memcpy(ix.pos, positions, static_cast<size_t>(num_positions) * sizeof(int32_t));
+  std::memcpy(ix.aux, deltas, static_cast<size_t>(num_positions) * sizeof(int32_t));
+  return launch_rope_delta_inline<ROT_PAIR>(fn, a, ix, dtype, g, groups,
+                                            static_cast<hipStream_t>(stream));
 }
 
 namespace sb {

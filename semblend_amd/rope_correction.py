@@ -18,6 +18,7 @@ Triton kernels store fp16 regardless of the cache dtype, :183-190, which is not 
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -32,6 +33,7 @@ __all__ = [
     "HAS_TRITON",
     "HAS_HIP",
     "apply_rope_delta_inplace",
+    "apply_rope_deltas_inplace_layers",
     "inv_freq_table",
     "nope_permute_paged_kv",
     "nope_permute_paged_kv_layers",
@@ -497,18 +499,23 @@ def apply_rope_delta_inplace(
     inv_freq = inv_freq_table(rope_base, head_dim, dev)
     reps = list(counts.values())
     repeated = any(c != 1 for c in reps)
+    keys = list(counts.keys())
     with _lib.on_device(dev):
-        if len(counts) <= _lib.SB_INLINE_POSITIONS_MAX:
-            # Short lists travel inside the launch: no index upload.
-            _lib.call(
-                "sb_apply_rope_delta_inplace_host",
-                kv_cache.data_ptr(), bt.data_ptr(), _lib.i32_array(list(counts.keys())),
-                _lib.i32_array(reps) if repeated else None, len(counts), int(delta),
-                inv_freq.data_ptr(), num_heads, block_size, head_dim, nb_total, nbs,
-                _lib.i64_array(kst), _lib.dtype_code(kv_cache), _lib.stream_handle(dev),
-            )
+        inline = _lib.SB_INLINE_POSITIONS_MAX
+        if len(keys) <= inline or torch.cuda.is_current_stream_capturing():
+            # Short lists (and any list under graph capture, in launches of up to 256
+            # positions) travel inside the launch: no index upload.
+            for c0 in range(0, len(keys), inline):
+                _lib.call(
+                    "sb_apply_rope_delta_inplace_host",
+                    kv_cache.data_ptr(), bt.data_ptr(), _lib.i32_array(keys[c0:c0 + inline]),
+                    _lib.i32_array(reps[c0:c0 + inline]) if repeated else None,
+                    len(keys[c0:c0 + inline]), int(delta), inv_freq.data_ptr(), num_heads,
+                    block_size, head_dim, nb_total, nbs, _lib.i64_array(kst),
+                    _lib.dtype_code(kv_cache), _lib.stream_handle(dev),
+                )
             return modified
-        pos_t = _lib.upload_index(torch.tensor(list(counts.keys()), dtype=torch.int32), dev)
+        pos_t = _lib.upload_index(torch.tensor(keys, dtype=torch.int32), dev)
         rep_t = _lib.upload_index(torch.tensor(reps, dtype=torch.int32), dev) if repeated else None
         _lib.call(
             "sb_apply_rope_delta_inplace",
@@ -518,6 +525,126 @@ def apply_rope_delta_inplace(
             _lib.i64_array(kst), _lib.dtype_code(kv_cache), _lib.stream_handle(dev),
         )
     return modified
+
+
+def _delta_rounds(positions, deltas, block_size: int,
+                  num_blocks_per_seq: int) -> tuple[list[tuple[np.ndarray, np.ndarray]], int]:
+    """Host-side resolution of ``apply_rope_deltas_inplace_layers``' (position, delta) list,
+    with the rule of ``apply_rope_delta_inplace`` applied to each entry as a one-position call
+    (semblend_core/rope_correction.py:732-783): delta 0 and positions whose logical block lies
+    past the table are skipped; negative positions index blocks from the end of the table
+    (below -num_blocks_per_seq blocks: IndexError, as there).
+
+    Returns (rounds, entries processed). Round r holds the r-th occurrence of every logical
+    position, in list order, as (int32 positions, int32 deltas): within a round the positions
+    are distinct, and a position's rotations land in list order across the rounds."""
+    pos = np.asarray(positions, dtype=np.int64).reshape(-1)
+    dlt = np.asarray(deltas, dtype=np.int64).reshape(-1)
+    if pos.shape != dlt.shape:
+        raise ValueError(f"positions ({pos.size}) and deltas ({dlt.size}) differ in length")
+    if np.any(np.abs(dlt) >= _lib.MAX_ROPE_DELTA):
+        raise ValueError("apply_rope_deltas_inplace_layers: every |delta| must be below 2^31 "
+                         "(the kernels' sin/cos reduce angles below 2^32 exactly)")
+    blk = pos // block_size                      # floor division, as Python's //
+    keep = (dlt != 0) & (blk < num_blocks_per_seq)
+    if np.any(keep & (blk < -num_blocks_per_seq)):
+        bad = int(pos[keep & (blk < -num_blocks_per_seq)][0])
+        raise IndexError(f"position {bad} indexes block {bad // block_size} of a "
+                         f"{num_blocks_per_seq}-entry table")
+    logical = np.where(blk < 0, blk + num_blocks_per_seq, blk) * block_size + pos % block_size
+    logical, dlt = logical[keep], dlt[keep]
+    n = int(logical.size)
+    if n == 0:
+        return [], 0
+    order = np.argsort(logical, kind="stable")
+    srt = logical[order]
+    start = np.r_[0, np.flatnonzero(np.diff(srt)) + 1]
+    first = np.repeat(start, np.diff(np.r_[start, n]))
+    occurrence = np.empty(n, dtype=np.int64)
+    occurrence[order] = np.arange(n) - first
+    rounds = []
+    for r in range(int(occurrence.max()) + 1):
+        sel = occurrence == r
+        rounds.append((logical[sel].astype(np.int32), dlt[sel].astype(np.int32)))
+    return rounds, n
+
+
+def apply_rope_deltas_inplace_layers(
+    kv_caches: list[torch.Tensor],
+    block_table: torch.Tensor,
+    positions,
+    deltas,
+    rope_base: float = 10000.0,
+    layout: str | None = None,
+) -> int:
+    """Rotate K in place at many positions, each by its own delta, in every layer's cache,
+    with one launch per occurrence round (one launch when no position repeats); V untouched.
+
+    Same result as, and the same count returned by, ::
+
+        sum(apply_rope_delta_inplace(kv, block_table, [p], d, rope_base)
+            for kv in kv_caches for p, d in zip(positions, deltas))
+
+    i.e. the per-(layer, pair) loop of the TRT-LLM post-load hook
+    (semblend/integration/trtllm/semblend_provider.py:305-318) or, for the per-delta caller
+    pattern, one ``apply_rope_delta_inplace`` call per distinct delta over its positions: a
+    position listed several times is rotated that many times, in list order, rounded to the
+    cache dtype after each rotation. Entries with delta 0 or past the block table count as
+    not processed.
+
+    kv_caches: one cache per layer, all with one shape, strides and dtype, in ``layout``
+    ("standard" [NB, 2, H, bs, D], "vllm" [2, NB, bs, H, D], "trt" [NB, 2, tpb, H, D]; None:
+    the reference's detection rule); positions, deltas: integer sequences (or tensors, read on
+    the host) of one length; every |delta| < 2^31. Extension with no single-call reference
+    counterpart (it replaces the loops above).
+    """
+    if not kv_caches:
+        return 0
+    dev = _lib.require_device(*kv_caches)
+    _check_uniform(kv_caches, "kv_caches")
+    nb, heads, bs, hd, st = paged_layout(kv_caches[0], layout)
+    _check_head_dim(hd, hd, "apply_rope_deltas_inplace_layers")
+    if st[4] != 1:
+        raise ValueError("head_dim must be contiguous (stride 1)")
+    if isinstance(positions, torch.Tensor):
+        positions = positions.cpu()
+    if isinstance(deltas, torch.Tensor):
+        deltas = deltas.cpu()
+    nbs = block_table.shape[0]
+    rounds, processed = _delta_rounds(positions, deltas, bs, nbs)
+    if not rounds:
+        return 0
+    bt = _lib.as_index(block_table, dev)
+    inv = inv_freq_table(rope_base, hd, dev)
+    tab = _lib.address_table(kv_caches, dev)
+    kst = _lib.i64_array((st[0], st[2], st[3], st[4]))
+    inline = _lib.SB_INLINE_POSITIONS_MAX
+    capturing = torch.cuda.is_current_stream_capturing()
+    with _lib.on_device(dev):
+        stream = _lib.stream_handle(dev)
+        for pos_r, dlt_r in rounds:
+            n = int(pos_r.size)
+            if n <= inline or capturing:
+                # in the launch's arguments, up to 256 positions per launch
+                for c0 in range(0, n, inline):
+                    p_c, d_c = pos_r[c0:c0 + inline], dlt_r[c0:c0 + inline]
+                    _lib.call(
+                        "sb_apply_rope_deltas_inplace_layers_host",
+                        tab.data_ptr(), len(kv_caches), bt.data_ptr(),
+                        p_c.ctypes.data_as(_lib.I32P), d_c.ctypes.data_as(_lib.I32P),
+                        int(p_c.size), inv.data_ptr(), heads, bs, hd, nb, nbs, kst,
+                        _lib.dtype_code(kv_caches[0]), stream,
+                    )
+                continue
+            # one upload of [positions | deltas] per round
+            both = _lib.upload_index(torch.from_numpy(np.concatenate([pos_r, dlt_r])), dev)
+            _lib.call(
+                "sb_apply_rope_deltas_inplace_layers",
+                tab.data_ptr(), len(kv_caches), bt.data_ptr(), both.data_ptr(),
+                both.data_ptr() + 4 * n, n, inv.data_ptr(), heads, bs, hd, nb, nbs, kst,
+                _lib.dtype_code(kv_caches[0]), stream,
+            )
+    return processed * len(kv_caches)
 
 
 # ------------------------------------------------------------------------------------------

@@ -122,35 +122,33 @@ def test_rope_delta_range_checked_before_dispatch():
         rc.apply_rope_delta_inplace(kv, bt, [0, 1], (1 << 31) - 1)
 
 
-def test_captured_uploads_keep_their_staging_buffer(monkeypatch):
-    """A host-to-device copy recorded into a HIP graph reads its pinned staging buffer at every
-    replay, so while the stream is capturing, pinned_upload keeps that buffer for the process
-    instead of letting torch's pinned-memory cache reuse it. The pinning and the copy are
-    replaced by CPU stand-ins here (no GPU); the bookkeeping is what is checked."""
+def test_uploads_under_capture(monkeypatch):
+    """While the stream is capturing a HIP graph no pinned staging memory can be allocated,
+    and a captured host-to-device copy reads its host buffer again at every replay. So
+    pinned_upload raises for pageable host data under capture, and keeps an already pinned
+    host tensor for the process (the replays read it). Outside capture nothing is kept. The
+    pinning and the copy run as CPU stand-ins here (no GPU); the rule is what is checked."""
     import torch
 
-    staged = []
-
-    def fake_pin(self):
-        staged.append(self.clone())
-        return staged[-1]
-
-    monkeypatch.setattr(torch.Tensor, "pin_memory", fake_pin)
+    monkeypatch.setattr(torch.Tensor, "pin_memory", lambda self: self.clone())
     cpu = torch.device("cpu")
     before = len(_lib._CAPTURED_UPLOADS)
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
-    _lib.upload_index(torch.arange(5), cpu)
+    out = _lib.upload_index(torch.arange(5), cpu)
+    assert torch.equal(out, torch.arange(5, dtype=torch.int32))
     assert len(_lib._CAPTURED_UPLOADS) == before
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
-    out = _lib.upload_index(torch.arange(7), cpu)
-    assert len(_lib._CAPTURED_UPLOADS) == before + 1
-    assert _lib._CAPTURED_UPLOADS[-1] is staged[-1]
-    assert torch.equal(out, torch.arange(7, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="capturing"):
+        _lib.upload_index(torch.arange(7), cpu)
     from semblend_amd import rope_correction as rc
 
-    src, tgt = rc._pairs_on_device([(1, 2), (3, 4)], cpu)
-    assert len(_lib._CAPTURED_UPLOADS) == before + 2
-    assert src.tolist() == [1, 3] and tgt.tolist() == [2, 4]
+    with pytest.raises(RuntimeError, match="capturing"):
+        rc._pairs_on_device([(1, 2), (3, 4)], cpu)
+    pinned = torch.arange(9, dtype=torch.int32)
+    monkeypatch.setattr(torch.Tensor, "is_pinned", lambda self: self is pinned)
+    out = _lib.pinned_upload(pinned, cpu)
+    assert torch.equal(out, pinned) and _lib._CAPTURED_UPLOADS[-1] is pinned
+    assert len(_lib._CAPTURED_UPLOADS) == before + 1
     del _lib._CAPTURED_UPLOADS[before:]
 
 

@@ -250,3 +250,35 @@ def test_graph_projection_paged(dev, backend):
         torch.cuda.synchronize()
         assert torch.equal(out["q"].view(torch.int16), want_q.view(torch.int16))
         assert torch.equal(kv.view(torch.int16), want_kv.view(torch.int16))
+
+
+@pytest.mark.parametrize("n", [300, 2000])
+def test_graph_delta_rope_uploaded_positions(dev, n):
+    """apply_rope_delta_inplace with more distinct positions than travel in the launch (the
+    list is uploaded from pinned memory) and the multi-layer per-position form: captured, the
+    uploads' staging buffers are kept, so every replay rotates the same rows by the same
+    deltas as an eager call on a shadow copy (each replay applies the rotations once more)."""
+    nb, h, bs, d = 160, 4, 16, 128
+    caches = [randn((nb, 2, h, bs, d), torch.bfloat16, 80 + i).to(dev) for i in range(3)]
+    bt = torch.randperm(nb, generator=gen(83))[:128].to(torch.int32).to(dev)
+    pos = torch.randperm(128 * bs, generator=gen(84))[:n].tolist()
+    dl = torch.randint(-500, 501, (n,), generator=gen(85)).tolist()
+
+    def step(cs):
+        rc.apply_rope_delta_inplace(cs[0], bt, pos, 37, rope_base=1e4)
+        rc.apply_rope_deltas_inplace_layers(cs, bt, pos, dl, rope_base=1e4)
+
+    start = [c.clone() for c in caches]
+    shadow = [c.clone() for c in caches]
+    g = _capture(lambda: step(caches))       # its warm-up runs one eager step on caches
+    for c, s in zip(caches, start):
+        c.copy_(s)
+    for _ in range(3):
+        step(shadow)
+        _noise(dev)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for c, s in zip(caches, shadow):
+            assert torch.equal(c.view(torch.int16), s.view(torch.int16))
+    assert not torch.equal(caches[1].view(torch.int16), start[1].view(torch.int16))

@@ -233,3 +233,90 @@ def test_trt_64_token_blocks(dev, dtype):
                                              bt.to(dev), pos.to(dev))
     assert_attn_close(out, ref.partial_attention_paged(q, rc.standard_view(cache, "trt"), bt,
                                                        pos))
+
+
+# ---- in-place RoPE, one delta per position, over many layers ----
+
+def _delta_entries(n_pos, n, seed, max_delta=2048):
+    """(positions, deltas): n random positions with deltas in [-max_delta, max_delta], plus
+    edge entries: a position listed three times with different deltas, one listed twice,
+    negative positions (blocks counted from the end of the table), positions past the table
+    and zero deltas (neither is processed)."""
+    g = gen(seed)
+    pos = torch.randint(0, n_pos, (n,), generator=g).tolist()
+    dl = torch.randint(-max_delta, max_delta + 1, (n,), generator=g).tolist()
+    pos += [pos[0], pos[0], pos[1], -3, -n_pos, n_pos + 5, n_pos, 11, 12]
+    dl += [17, -900, 5, 33, -7, 100, 100, 0, 0]
+    return pos, dl
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rope_deltas_layers_layouts(dev, layout, dtype):
+    """One call over three layers equals the TRT-LLM hook's loop of one-position
+    apply_rope_delta_inplace calls per (layer, pair) (semblend_provider.py:305-318), on the
+    oracle: same count returned, V untouched, K within the RoPE bar for rows rotated several
+    times."""
+    nb, h, bs, d, layers = 40, 4, 16, 128, 3
+    caches = [_cache(layout, nb, h, bs, d, dtype, 30 + i) for i in range(layers)]
+    bt = torch.randperm(nb, generator=gen(33))[:32].to(torch.int32)
+    pos, dl = _delta_entries(32 * bs, 300, 34)
+    got = [c.to(dev) for c in caches]
+    n = rc.apply_rope_deltas_inplace_layers(got, bt.to(dev), pos, dl, rope_base=5e5,
+                                            layout=layout)
+    want_n = 0
+    for c in caches:
+        v = rc.standard_view(c, layout)
+        for p, dd in zip(pos, dl):
+            want_n += ref.apply_rope_delta_inplace(v, bt, [p], dd, rope_base=5e5)
+    assert n == want_n == layers * 305   # 300 random entries + 5 edge entries processed
+    for g_, c in zip(got, caches):
+        gv, wv = rc.standard_view(g_.cpu(), layout), rc.standard_view(c, layout)
+        assert_bit_exact(gv[:, 1], wv[:, 1])
+        assert_rope_close(gv, wv, composed=True)
+
+
+def test_rope_deltas_layers_equals_per_delta_calls(dev):
+    """The Qwen2.5-0.5B caller pattern (fp32, [128, 2, 2, 16, 64], a delta in [-64, 64] per
+    token): one multi-layer call with per-token deltas lands the same bits as one
+    apply_rope_delta_inplace call per distinct delta and layer (same rotation arithmetic)."""
+    import bench
+
+    inp = bench.qwen05b_pipeline_inputs(0)
+    layers = [randn((128, 2, 2, 16, 64), torch.float32, 40 + i).to(dev) for i in range(2)]
+    per_delta = [c.clone() for c in layers]
+    bt = inp["block_table"].to(dev)
+    dl = inp["deltas"]
+    n = rc.apply_rope_deltas_inplace_layers(layers, bt, torch.arange(1024), dl, rope_base=1e6)
+    m = 0
+    for c in per_delta:
+        for delta, ps in bench.delta_groups(dl):
+            m += rc.apply_rope_delta_inplace(c, bt, ps, delta, rope_base=1e6)
+    assert n == m == 2 * int((dl != 0).sum())
+    for a, b in zip(layers, per_delta):
+        assert_bit_exact(a, b)
+
+
+def test_rope_deltas_layers_7b_shape(dev):
+    """28 layers of the Qwen2.5-7B cache ([2048, 2, 4, 16, 128] bf16, vLLM layout), every one
+    of 13926 reused positions rotated by its chunk's delta (constant per 256-token chunk in
+    [-2048, 2048]): one launch; layers 0, 13 and 27 against the oracle's per-delta calls."""
+    g = gen(50)
+    bt = torch.randperm(2048, generator=g)[:1024].to(torch.int32)
+    pos = torch.randperm(16384, generator=g)[:13926].sort().values
+    chunk_delta = torch.randint(-2048, 2049, (64,), generator=g)
+    dl = chunk_delta[pos // 256]
+    caches = [_cache("vllm", 2048, 4, 16, 128, torch.bfloat16, 60 + i) for i in range(28)]
+    got = [c.to(dev) for c in caches]
+    n = rc.apply_rope_deltas_inplace_layers(got, bt.to(dev), pos, dl, rope_base=1e6)
+    assert n == 28 * int((dl != 0).sum())
+    for layer in (0, 13, 27):
+        want = caches[layer].clone()
+        for c in range(64):
+            sel = (pos // 256 == c)
+            ref.apply_rope_delta_inplace(want, bt, pos[sel].tolist(), int(chunk_delta[c]),
+                                         rope_base=1e6)
+        gv = rc.standard_view(got[layer].cpu(), "vllm")
+        wv = rc.standard_view(want, "vllm")
+        assert_bit_exact(gv[:, 1], wv[:, 1])
+        assert_rope_close(gv, wv)

@@ -244,6 +244,45 @@ def test_rotation_counts_agree_with_oracle_count():
     assert n == ref_cpu.apply_rope_delta_inplace(kv, bt, pos, 3)
 
 
+def test_delta_rounds_resolve_like_one_position_calls():
+    """apply_rope_deltas_inplace_layers' host resolution: every (position, delta) entry is
+    treated like a one-position apply_rope_delta_inplace call (the oracle's count per entry
+    decides whether it is processed), each logical position's entries keep their list order
+    across rounds, and no round holds a position twice."""
+    rng = random.Random(7)
+    bs, nbs = 16, 8
+    pos = [rng.randrange(-nbs * bs, nbs * bs + 40) for _ in range(400)] + [5, 5, 5, -11, 117]
+    dl = [rng.choice([0, rng.randrange(-3000, 3000)]) for _ in range(400)] + [1, 2, 3, 4, 5]
+    rounds, n = rc._delta_rounds(pos, dl, bs, nbs)
+    kv = torch.zeros(nbs, 2, 1, bs, 2)
+    bt = torch.arange(nbs, dtype=torch.int32)
+    want = []  # (logical position, delta) of the processed entries, in list order
+    for p, d in zip(pos, dl):
+        if ref_cpu.apply_rope_delta_inplace(kv, bt, [p], d):
+            blk = p // bs
+            want.append(((blk % nbs) * bs + p % bs, d))
+    assert n == len(want)
+    seen: dict[int, list[int]] = {}
+    for rp, rd in rounds:
+        assert rp.dtype == np.int32 and rd.dtype == np.int32
+        assert len(set(rp.tolist())) == rp.size
+        for p, d in zip(rp.tolist(), rd.tolist()):
+            seen.setdefault(p, []).append(d)
+    expect: dict[int, list[int]] = {}
+    for p, d in want:
+        expect.setdefault(p, []).append(d)
+    assert seen == expect
+    # -11 lies in the table's last block (-1), offset 5: logical 117, listed next with 5
+    assert seen[5][-3:] == [1, 2, 3] and seen[117][-2:] == [4, 5]
+    with pytest.raises(IndexError):
+        rc._delta_rounds([-nbs * bs - 1], [3], bs, nbs)
+    with pytest.raises(ValueError, match="2\\^31"):
+        rc._delta_rounds([0], [1 << 31], bs, nbs)
+    with pytest.raises(ValueError, match="length"):
+        rc._delta_rounds([0, 1], [3], bs, nbs)
+    assert rc._delta_rounds([0, 200], [0, 5], bs, nbs) == ([], 0)
+
+
 def test_inv_freq_table_is_the_reference_expression():
     for base, d in ((10000.0, 128), (1e6, 128), (5e5, 64), (500.0, 32)):
         got = rc.inv_freq_table(base, d, torch.device("cpu"))
