@@ -786,10 +786,21 @@ def main() -> int:
         tk.scatter_donor_kv_paged_layers(inp["caches"], inp["donors"], inp["block_table"],
                                          inp["sc_d"], inp["sc_t"])
 
+    # The attention launch is planned once from the host positions (as a serving loop plans a
+    # request once and reuses the plan for every layer): key split and longest-first order.
+    attn_plan = tk.plan_partial_attention_paged(inp["pos_cpu"], HQ, HKV, D, BS,
+                                                inp["block_table"].shape[0], torch.bfloat16,
+                                                dev)
+
     def phase_attn(i):
         tk.partial_prefill_attention_paged(inp["attn_q"], inp["attn_kv"], inp["block_table"],
                                            inp["attn_pos"], out=inp.setdefault(
-                                               "attn_out", torch.empty_like(inp["attn_q"])))
+                                               "attn_out", torch.empty_like(inp["attn_q"])),
+                                           plan=attn_plan)
+
+    def attn_unplanned(i):
+        tk.partial_prefill_attention_paged(inp["attn_q"], inp["attn_kv"], inp["block_table"],
+                                           inp["attn_pos"], out=inp["attn_out"])
 
     phases = [("rope", phase_rope), ("scatter", phase_scatter), ("attention", phase_attn)]
     log(f"warmup {args.warmup}")
@@ -798,19 +809,42 @@ def main() -> int:
             fn(i)
     torch.cuda.synchronize()
 
-    # Per-kernel durations: an eager pass with HIP events attached to each library launch.
-    log(f"kernel timing pass ({args.steps} eager steps)")
-    _lib.kernel_timing(True)
-    for i in range(args.steps):
-        for _, fn in phases:
-            fn(i)
-    torch.cuda.synchronize()
-    _lib.kernel_timing(False)
+    # Per-kernel durations: eager passes with HIP events attached to each library launch, in
+    # three rounds that alternate a pass of whole steps (RoPE, scatter, planned attention)
+    # with a pass of the unplanned attention (after the scatter, as in a step); each kernel's
+    # figure is the median of its three round averages (so that neither form always runs
+    # first after the warm-up).
+    log(f"kernel timing passes (3 rounds of {args.steps} eager steps, two forms each)")
+
+    def timed_pass(fns) -> dict:
+        _lib.kernel_timing(True)
+        for i in range(args.steps):
+            for fn in fns:
+                fn(i)
+        torch.cuda.synchronize()
+        _lib.kernel_timing(False)
+        return {name: _lib.kernel_time(name) for name in KERNELS}
+
+    main_fns = [fn for _, fn in phases]
+    unplanned_fns = [phase_scatter, attn_unplanned]
+    rounds = {"main": [], "unplanned": []}
+    for r in range(3):
+        order = ["main", "unplanned"] if r % 2 == 0 else ["unplanned", "main"]
+        for tag in order:
+            rounds[tag].append(timed_pass(main_fns if tag == "main" else unplanned_fns))
+
+    def median_avg_us(tag: str, name: str) -> tuple[float, int]:
+        avgs = sorted(1e3 * t / n for t, n in (rd[name] for rd in rounds[tag]) if n)
+        n_total = sum(rd[name][1] for rd in rounds[tag])
+        return (avgs[len(avgs) // 2] if avgs else 0.0), n_total
+
     kernels = {}
     for name in KERNELS:
-        total, n = _lib.kernel_time(name)
+        avg_us, n = median_avg_us("main", name)
         if n:
-            kernels[name] = {"launches": n, "avg_us": round(1e3 * total / n, 2)}
+            kernels[name] = {"launches": n, "avg_us": round(avg_us, 2)}
+    unplanned = {name: round(median_avg_us("unplanned", name)[0], 2)
+                 for name in ("attn_mfma", "attn_merge")}
 
     log("capturing one HIP graph per step (RoPE, scatter, attention) and one per phase")
 
@@ -929,7 +963,20 @@ def main() -> int:
             "attention": {"ms": round(avg["attention"], 4),
                           "launch_inclusive_ms": round(launch_ms["attention"], 4),
                           "tflops": round(attn_tflops, 2),
-                          "frac_of_peak": round(attn_tflops / BF16_PEAK_TFLOPS, 4)},
+                          "frac_of_peak": round(attn_tflops / BF16_PEAK_TFLOPS, 4),
+                          "plan": {"ks_first": attn_plan.ks_first,
+                                   "ks_rest": attn_plan.ks_rest,
+                                   "max_chunks": attn_plan.max_chunks,
+                                   "what": "host plan from the recompute positions: key split "
+                                           "and longest-first dispatch order"},
+                          "unplanned": {
+                              "attn_mfma_us": unplanned["attn_mfma"],
+                              "attn_merge_us": unplanned["attn_merge"],
+                              "tflops": round(attn_flops / ((unplanned["attn_mfma"]
+                                                             + unplanned["attn_merge"])
+                                                            * 1e-6) / 1e12, 2),
+                              "what": "the same call without a plan (default split, "
+                                      "workgroup order)"}},
             "scatter": {"ms": round(avg["scatter"], 4),
                         "launch_inclusive_ms": round(launch_ms["scatter"], 4),
                         "gbps": round(scatter_gbps, 1),

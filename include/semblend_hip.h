@@ -399,6 +399,47 @@ int sb_partial_attention_paged(void* out, const void* q, const void* kv_cache,
                                const int64_t* q_strides, const int64_t* o_strides,
                                const int64_t* kv_strides, int32_t dtype, void* stream);
 
+/* Host-planned form of sb_partial_attention_paged. A caller that knows the query positions on
+ * the host (they come from the reuse plan, and one request's positions serve every layer)
+ * plans once: sb_partial_attention_paged_plan reads the HOST positions and writes into `plan`
+ * (capacity int32 entries) the key split {ks_first, ks_rest, max_chunks} followed by the
+ * dispatch order of every work item, longest first (a row tile's first key chunk of ks_first
+ * keys, its later chunks of ks_rest keys, chosen by a longest-first schedule model of the
+ * launch). With plan == NULL it returns the number of entries needed; otherwise the number
+ * written, or a negative SB_ERR_INVALID_ARGUMENT on bad arguments. For a dtype / head_dim
+ * the MFMA kernel does not take, max_chunks is 0 and there are no items.
+ * sb_partial_attention_paged_planned takes the device copy of the item order (plan + 3), its
+ * length (refused unless it is max_chunks * ceil(num_rows * group / 128) * num_kv_heads,
+ * the launch's item count) and the three split values, otherwise the arguments of
+ * sb_partial_attention_paged; its
+ * workspace is sb_partial_attention_paged_planned_workspace_size(...) bytes. The order only
+ * schedules the launch: it names every item whatever the positions hold, so results are
+ * correct for any positions (the same within the attention bar as the unplanned entry; the
+ * split-key partials round differently), and fastest for the positions it was planned from.
+ * No reference counterpart (see sb_partial_attention_paged). */
+int64_t sb_partial_attention_paged_plan(const int32_t* positions, int64_t num_rows,
+                                        int64_t num_q_heads, int64_t num_kv_heads,
+                                        int64_t head_dim, int64_t block_size,
+                                        int64_t num_blocks_per_seq, int32_t dtype,
+                                        int32_t* plan, int64_t capacity);
+int64_t sb_partial_attention_paged_planned_workspace_size(int64_t num_rows,
+                                                          int64_t num_q_heads,
+                                                          int64_t num_kv_heads,
+                                                          int64_t head_dim, int32_t max_chunks,
+                                                          int32_t dtype);
+int sb_partial_attention_paged_planned(void* out, const void* q, const void* kv_cache,
+                                       const int32_t* block_table, const int32_t* positions,
+                                       const int32_t* item_order, int64_t num_items,
+                                       int32_t ks_first, int32_t ks_rest,
+                                       int32_t max_chunks, void* workspace,
+                                       int64_t workspace_bytes, int64_t num_rows,
+                                       int64_t num_q_heads, int64_t num_kv_heads,
+                                       int64_t head_dim, int64_t block_size,
+                                       int64_t num_blocks_total, int64_t num_blocks_per_seq,
+                                       float scale, const int64_t* q_strides,
+                                       const int64_t* o_strides, const int64_t* kv_strides,
+                                       int32_t dtype, void* stream);
+
 /* No-allocation form of sb_partial_attention_paged, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). Same arguments minus the workspace, same kernels, same plan and bit-identical

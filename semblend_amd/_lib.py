@@ -77,6 +77,9 @@ SIGNATURES: dict[str, list] = {
                                      _f32, _i64p, _i64p, _i64p, _i64p, _i32, _vp],
     "sb_partial_attention_paged": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                    _i64, _i64, _i64, _f32, _i64p, _i64p, _i64p, _i32, _vp],
+    "sb_partial_attention_paged_planned": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp,
+                                           _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                           _f32, _i64p, _i64p, _i64p, _i32, _vp],
     "sb_partial_attention_paged_varlen": [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64p, _i64p,
                                           _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                                           _i64p, _i64p, _i64p, _i32, _vp],
@@ -102,6 +105,9 @@ SIZE_QUERIES: dict[str, list] = {
     "sb_partial_attention_paged_varlen_workspace_size": [_i64, _i64p, _i64p, _i64, _i64, _i64,
                                                          _i64, _i32],
     "sb_partial_attention_paged_noalloc_max_scratch": [],
+    "sb_partial_attention_paged_plan": [_i32p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32p,
+                                        _i64],
+    "sb_partial_attention_paged_planned_workspace_size": [_i64, _i64, _i64, _i64, _i32, _i32],
     "sb_masked_qkv_projection_workspace_size": [_i64],
     "sb_qkv_projection_paged_workspace_size": [_i64, _i64, _i32],
 }

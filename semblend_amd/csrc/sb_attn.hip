@@ -38,6 +38,8 @@
 #include "sb_common.h"
 
 #include <algorithm>
+#include <cstring>
+#include <functional>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -103,6 +105,11 @@ constexpr int kWaves = SB_ATTN_WAVES;         // waves per workgroup (each owns 
 constexpr int kThreads = 64 * kWaves;
 constexpr int kHalves = kTileKeys / 32;       // 32-key MFMA blocks per tile
 constexpr int kBtLds = 1024;    // block-table entries staged per chunk
+// Longest key chunk of a paged launch: (kBtLds - 1) blocks, in whole 64-key tiles, so that a
+// chunk starting anywhere inside a block touches at most kBtLds blocks of the table.
+__host__ __device__ constexpr int64_t chunk_cap(int64_t block_size) {
+  return (kBtLds - 1) * block_size / 64 * 64;
+}
 
 // One request of a batched (varlen) launch: its rows, its block-table row, and where its work
 // items, merge workgroups and partial slots start in the launch.
@@ -145,14 +152,31 @@ struct AttnArgs {
   int head_dim;
   float scale;
   float scale_log2;           // scale * log2(e)
-  int ksplit;                 // keys per work item (multiple of kTileKeys)
-  int max_chunks;             // ceil(kv_len / ksplit)
+  int ksplit;                 // keys per work item after a row tile's first chunk
+                              // (multiple of kTileKeys)
+  int ksplit_first;           // keys of a row tile's first chunk (multiple of kTileKeys)
+  int max_chunks;             // chunks of the longest key range (chunk_count(kv_len))
   int device_split;           // 1: ksplit, max_chunks and n_tiles follow the device row count
   int64_t n_tiles;            // row tiles per kv head used for the partial layout
   int tile_rows;              // flattened query rows per workgroup tile
   float* part_o;              // [Hkv][n_tiles][max_chunks][128][D] fp32, or nullptr
   float* part_ml;             // [Hkv][n_tiles][max_chunks][128][2] fp32 (m, l)
+  const int32_t* item_order;  // single-request launches: work item of each workgroup (a
+                              // host-planned order), or nullptr (workgroup b runs item b)
 };
+
+// Key chunks of a row tile: the first covers [0, ksplit_first), each later one ksplit keys.
+__host__ __device__ inline int chunk_begin(const AttnArgs& a, int c) {
+  return c == 0 ? 0 : a.ksplit_first + (c - 1) * a.ksplit;
+}
+__host__ __device__ inline int chunk_len(const AttnArgs& a, int c) {
+  return c == 0 ? a.ksplit_first : a.ksplit;
+}
+__host__ __device__ inline int chunk_count(const AttnArgs& a, int64_t kend) {
+  return kend <= a.ksplit_first
+             ? 1
+             : 1 + static_cast<int>((kend - a.ksplit_first + a.ksplit - 1) / a.ksplit);
+}
 
 // Kernel parameter: the call's arguments and, for a batched launch, the request table (read
 // in place from the kernel-argument segment).
@@ -388,7 +412,7 @@ __host__ __device__ inline KeySplit key_split(int64_t n_tiles, int64_t num_kv_he
   ks = ks / kTileKeys * kTileKeys;
   if (ks < 512) ks = 512;
   if (paged) {
-    const int64_t cap = static_cast<int64_t>(kBtLds) * block_size / kTileKeys * kTileKeys;
+    const int64_t cap = chunk_cap(block_size);
     if (ks > cap) ks = cap;
   }
   if (ks > kv_pad) ks = kv_pad;
@@ -401,6 +425,7 @@ __device__ __forceinline__ void apply_device_split(AttnArgs& a, int64_t n_tiles_
   if (!a.device_split) return;
   const KeySplit sp = key_split(n_tiles_live, a.num_kv_heads, a.kv_len, 1, false);
   a.ksplit = sp.ksplit;
+  a.ksplit_first = sp.ksplit;
   a.max_chunks = sp.max_chunks;
   a.n_tiles = n_tiles_live;
 }
@@ -440,7 +465,12 @@ __global__ __launch_bounds__(kThreads, RG == 1 ? SB_ATTN_OCCUPANCY * 4 / kWaves 
 attn_mfma_kernel(const AttnBatch batch) {
   constexpr bool kPaged = AM != kAddrFlat;
   AttnArgs a = batch.a;
-  const int64_t item_b = select_request(batch, a, blockIdx.x, false);
+  int64_t b0 = blockIdx.x;
+  if (batch.num_reqs <= 0 && a.item_order) {
+    b0 = a.item_order[b0];
+    if (b0 < 0 || b0 >= static_cast<int64_t>(gridDim.x)) return;  // not an item of the launch
+  }
+  const int64_t item_b = select_request(batch, a, b0, false);
   using M = Mma<DT>;
   using vec8 = typename M::vec8;
   constexpr int TR = kWaveRows * RG * kWaves;  // flattened rows per workgroup tile
@@ -502,10 +532,10 @@ attn_mfma_kernel(const AttnBatch batch) {
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) kend_l = max(kend_l, red_max[w]);
   const int kend = __builtin_amdgcn_readfirstlane(kend_l) + 1;
-  const int k0 = item.chunk * a.ksplit;
+  const int k0 = chunk_begin(a, item.chunk);
   if (k0 >= kend) return;  // uniform: kend comes from shared memory
-  const int k1 = min(k0 + a.ksplit, kend);
-  const int nchunks = (kend + a.ksplit - 1) / a.ksplit;
+  const int k1 = min(k0 + chunk_len(a, item.chunk), kend);
+  const int nchunks = chunk_count(a, kend);
   int plim[RG];  // keys beyond the chunk are masked as well
   int pmin_l = 0x7fffffff;
 #pragma unroll
@@ -1058,7 +1088,7 @@ __device__ __forceinline__ void merge_unit(const AttnArgs& a, int64_t mb, int64_
   if ((tid & 63) == 0) red[tid >> 6] = pm;
   __syncthreads();
   const int kend = max(max(red[0], red[1]), max(red[2], red[3])) + 1;
-  const int nchunks = (kend + a.ksplit - 1) / a.ksplit;
+  const int nchunks = chunk_count(a, kend);
   if (nchunks <= 1) return;
   const int row_in_tile = part * 32 + tid / 8;
   const int64_t r = tile * TR + row_in_tile;
@@ -1284,9 +1314,19 @@ bool mfma_path(int32_t dtype, int64_t head_dim) {
          (head_dim == 64 || head_dim == 128);
 }
 
+// A host-planned launch of the single-request paged attention (sb_partial_attention_paged_plan):
+// the key split (first chunk, later chunks) and the dispatch order of the work items.
+struct OrderPlan {
+  int ks_first = 0;
+  int ks_rest = 0;
+  int max_chunks = 0;
+  const int32_t* order = nullptr;  // device: max_chunks * n_tiles * Hkv work items
+};
+
 // Chunking of the key range for one call. rows_upper bounds the query rows.
 struct Plan {
   int ksplit;
+  int ksplit_first;
   int max_chunks;
   int tile_rows;
   int64_t n_tiles;
@@ -1294,13 +1334,21 @@ struct Plan {
 };
 
 Plan make_plan(int64_t rows_upper, int64_t group, int64_t num_kv_heads, int64_t kv_len,
-               int64_t head_dim, int64_t block_size, bool paged) {
+               int64_t head_dim, int64_t block_size, bool paged,
+               const OrderPlan* op = nullptr) {
   Plan pl{};
   pl.tile_rows = kWaveRows * kRowGroups * kWaves;
   pl.n_tiles = (rows_upper * group + pl.tile_rows - 1) / pl.tile_rows;
-  const KeySplit sp = key_split(pl.n_tiles, num_kv_heads, kv_len, block_size, paged);
-  pl.ksplit = sp.ksplit;
-  pl.max_chunks = sp.max_chunks;
+  if (op) {
+    pl.ksplit = op->ks_rest;
+    pl.ksplit_first = op->ks_first;
+    pl.max_chunks = op->max_chunks;
+  } else {
+    const KeySplit sp = key_split(pl.n_tiles, num_kv_heads, kv_len, block_size, paged);
+    pl.ksplit = sp.ksplit;
+    pl.ksplit_first = sp.ksplit;
+    pl.max_chunks = sp.max_chunks;
+  }
   if (pl.max_chunks > 1)
     pl.part_bytes =
         num_kv_heads * pl.n_tiles * pl.max_chunks * pl.tile_rows * (head_dim + 2) * 4;
@@ -1329,14 +1377,16 @@ DeviceSplitBounds device_split_bounds(int64_t n_tiles_upper, int64_t num_kv_head
 
 int launch_attention(const char* fn, AttnArgs a, int32_t dtype, int64_t rows_upper,
                      bool aligned16, void* workspace, int64_t workspace_bytes,
-                     hipStream_t st) {
+                     hipStream_t st, const OrderPlan* op = nullptr) {
   if (rows_upper <= 0) return SB_OK;
   // The MFMA kernel masks keys with -inf scores before the scale is applied, so it takes
   // positive scales; any other scale goes to the VALU kernel, which never forms a masked score.
   if (mfma_path(dtype, a.head_dim) && aligned16 && a.scale_log2 > 0.f) {
     const Plan pl = make_plan(rows_upper, a.group, a.num_kv_heads, a.kv_len, a.head_dim,
-                              a.block_size, a.paged != 0);
+                              a.block_size, a.paged != 0, op);
     a.ksplit = pl.ksplit;
+    a.ksplit_first = pl.ksplit_first;
+    a.item_order = op ? op->order : nullptr;
     a.max_chunks = pl.max_chunks;
     a.n_tiles = pl.n_tiles;
     a.tile_rows = pl.tile_rows;
@@ -1426,7 +1476,7 @@ VarlenPlan make_varlen_plan(int64_t num_reqs, const int64_t* rows, const int64_t
   int64_t ks = work / kResidentSlots;
   ks = ks / kTileKeys * kTileKeys;
   if (ks < 512) ks = 512;
-  const int64_t cap = static_cast<int64_t>(kBtLds) * block_size / kTileKeys * kTileKeys;
+  const int64_t cap = chunk_cap(block_size);
   if (ks > cap) ks = cap;
   const int64_t kv_pad = (kv_max + kTileKeys - 1) / kTileKeys * kTileKeys;
   if (ks > kv_pad) ks = kv_pad;
@@ -1475,6 +1525,7 @@ int launch_attention_varlen(const char* fn, AttnArgs a, int32_t dtype, int64_t n
     return fail(fn, "workspace too small for the split-key partials");
   const int tr = kWaveRows * kRowGroups * kWaves;
   a.ksplit = pl.ksplit;
+  a.ksplit_first = pl.ksplit;
   a.tile_rows = tr;
   a.part_o = pl.part_bytes > 0 ? static_cast<float*>(workspace) : nullptr;
   for (size_t g0 = 0; g0 < pl.order.size(); g0 += kMaxReqs) {
@@ -1540,6 +1591,107 @@ int64_t part_bytes_for(int32_t dtype, int64_t rows_upper, int64_t group, int64_t
   if (!mfma_path(dtype, head_dim)) return 0;
   return make_plan(rows_upper, group, num_kv_heads, kv_len, head_dim, block_size, paged)
       .part_bytes;
+}
+
+// ---- Host planning of the single-request paged attention ----
+// Given the query positions on the host, the planner knows every work item's key range, so it
+// can (a) split the tail of each row tile's key range more finely than the default rule and
+// (b) dispatch the items longest first, which the hardware dispatcher (in workgroup order, to
+// whichever slot frees first) then turns into a longest-processing-time schedule. The default
+// order (chunk ascending, row tile descending) leaves short first chunks of short row tiles
+// ahead of long second chunks, and one long chunk per row tile leaves the last slots
+// idle: on the Qwen2.5-7B 16K workload, 0.88 of the ideal makespan against 0.95 planned (one
+// tile of per-item overhead in the schedule model).
+
+// Per-item set-up (Q loads, block-table staging, pipeline fill) in 64-key-tile units.
+constexpr double kItemOverheadTiles = 1.0;
+
+// Makespan of a longest-first list schedule of `costs` (sorted descending) on `slots` slots.
+double lpt_makespan(const std::vector<double>& costs, int slots) {
+  std::vector<double> load(static_cast<size_t>(slots), 0.0);
+  std::make_heap(load.begin(), load.end(), std::greater<double>());
+  for (double c : costs) {
+    std::pop_heap(load.begin(), load.end(), std::greater<double>());
+    load.back() += c;
+    std::push_heap(load.begin(), load.end(), std::greater<double>());
+  }
+  return *std::max_element(load.begin(), load.end());
+}
+
+struct HostOrderPlan {
+  int ks_first = 0, ks_rest = 0, max_chunks = 0;
+  std::vector<int32_t> order;  // work items, longest first
+};
+
+HostOrderPlan plan_paged_order(const int32_t* pos, int64_t num_rows, int64_t group,
+                               int64_t num_kv_heads, int64_t kv_len, int64_t block_size) {
+  HostOrderPlan hp;
+  const int tr = kWaveRows * kRowGroups * kWaves;
+  const int64_t rows_kv = num_rows * group;
+  const int64_t n_tiles = (rows_kv + tr - 1) / tr;
+  // Key range of each row tile, as the kernel finds it (positions clamped to the table).
+  std::vector<int64_t> kend(static_cast<size_t>(n_tiles), 0);
+  for (int64_t t = 0; t < n_tiles; ++t) {
+    int64_t m = -1;
+    const int64_t r_end = std::min<int64_t>((t + 1) * tr, rows_kv);
+    for (int64_t pi = t * tr / group; pi <= (r_end - 1) / group; ++pi) {
+      int64_t pp = pos[pi];
+      if (pp >= kv_len) pp = kv_len - 1;
+      if (pp >= 0) m = std::max(m, pp);
+    }
+    kend[static_cast<size_t>(t)] = m + 1;
+  }
+  const KeySplit base = key_split(n_tiles, num_kv_heads, kv_len, block_size, true);
+  AttnArgs geo{};
+  auto cost_of = [&](int chunk, int64_t t) -> int64_t {  // 64-key tiles of one item
+    const int64_t k0 = chunk_begin(geo, chunk);
+    const int64_t k1 = std::min<int64_t>(k0 + chunk_len(geo, chunk), kend[static_cast<size_t>(t)]);
+    return k1 > k0 ? (k1 - k0 + kTileKeys - 1) / kTileKeys : 0;
+  };
+  // Candidate splits: the default first chunk, later chunks of 1, 1/2 or 1/4 of it (at least
+  // 512 keys); the shortest modelled makespan wins, ties going to the longer later chunks
+  // (fewer split-key partials to write and merge).
+  double best = 0.0;
+  for (int div : {1, 2, 4}) {
+    int rest = base.ksplit / div / kTileKeys * kTileKeys;
+    if (div > 1 && rest < 512) break;
+    if (rest < kTileKeys) rest = kTileKeys;
+    geo.ksplit_first = base.ksplit;
+    geo.ksplit = rest;
+    std::vector<double> costs;
+    for (int64_t t = 0; t < n_tiles; ++t)
+      for (int c = 0; c < chunk_count(geo, kend[static_cast<size_t>(t)]); ++c) {
+        const int64_t tiles = cost_of(c, t);
+        if (tiles > 0)
+          for (int64_t h = 0; h < num_kv_heads; ++h)
+            costs.push_back(static_cast<double>(tiles) + kItemOverheadTiles);
+      }
+    std::sort(costs.begin(), costs.end(), std::greater<double>());
+    const double ms = costs.empty() ? 0.0 : lpt_makespan(costs, kResidentSlots);
+    if (div == 1 || ms < best * 0.995) {
+      best = ms;
+      hp.ks_first = geo.ksplit_first;
+      hp.ks_rest = geo.ksplit;
+    }
+  }
+  geo.ksplit_first = hp.ks_first;
+  geo.ksplit = hp.ks_rest;
+  hp.max_chunks = chunk_count(geo, kv_len);
+  // Every work item of the launch (the encoding of decode_item), longest first; items past a
+  // row tile's key range run last and exit at once.
+  const int64_t n_items = static_cast<int64_t>(hp.max_chunks) * n_tiles * num_kv_heads;
+  std::vector<std::pair<int64_t, int32_t>> keyed(static_cast<size_t>(n_items));
+  for (int64_t b = 0; b < n_items; ++b) {
+    const int64_t rest = b / num_kv_heads;
+    const int64_t tile = n_tiles - 1 - rest % n_tiles;
+    const int chunk = static_cast<int>(rest / n_tiles);
+    keyed[static_cast<size_t>(b)] = {-cost_of(chunk, tile), static_cast<int32_t>(b)};
+  }
+  std::stable_sort(keyed.begin(), keyed.end(),
+                   [](const auto& x, const auto& y) { return x.first < y.first; });
+  hp.order.resize(static_cast<size_t>(n_items));
+  for (int64_t i = 0; i < n_items; ++i) hp.order[static_cast<size_t>(i)] = keyed[static_cast<size_t>(i)].second;
+  return hp;
 }
 
 }  // namespace
@@ -1731,6 +1883,97 @@ extern "C" int sb_partial_attention_paged(void* out, const void* q, const void* 
   a.kv_len = num_blocks_per_seq * block_size;
   return launch_attention(fn, a, dtype, num_rows, aligned16, workspace, workspace_bytes,
                           static_cast<hipStream_t>(stream));
+}
+
+// Launch plan of sb_partial_attention_paged_planned from HOST positions (see the header).
+extern "C" int64_t sb_partial_attention_paged_plan(const int32_t* positions, int64_t num_rows,
+                                                   int64_t num_q_heads, int64_t num_kv_heads,
+                                                   int64_t head_dim, int64_t block_size,
+                                                   int64_t num_blocks_per_seq, int32_t dtype,
+                                                   int32_t* plan, int64_t capacity) {
+  const char* fn = "sb_partial_attention_paged_plan";
+  clear_error();
+  // errors are returned negated, apart from the entry counts
+  auto err = [&](const char* msg) { return -static_cast<int64_t>(fail(fn, msg)); };
+  if (num_rows < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
+      block_size <= 0 || num_blocks_per_seq <= 0)
+    return err("invalid shape");
+  if (num_rows > 0 && !positions) return err("null positions");
+  const int64_t kv_len = num_blocks_per_seq * block_size;
+  if (kv_len > 0x7ffffffe) return err("sequence too long");
+  HostOrderPlan hp;
+  if (num_rows > 0 && mfma_path(dtype, head_dim))
+    hp = plan_paged_order(positions, num_rows, num_q_heads / num_kv_heads, num_kv_heads, kv_len,
+                          block_size);
+  const int64_t need = 3 + static_cast<int64_t>(hp.order.size());
+  if (!plan) return need;
+  if (capacity < need) return err("plan buffer too small");
+  plan[0] = hp.ks_first;
+  plan[1] = hp.ks_rest;
+  plan[2] = hp.max_chunks;
+  if (!hp.order.empty()) std::memcpy(plan + 3, hp.order.data(), hp.order.size() * sizeof(int32_t));
+  return need;
+}
+
+extern "C" int64_t sb_partial_attention_paged_planned_workspace_size(
+    int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+    int32_t max_chunks, int32_t dtype) {
+  if (num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || max_chunks <= 1 ||
+      !mfma_path(dtype, head_dim))
+    return 0;
+  const int tr = kWaveRows * kRowGroups * kWaves;
+  const int64_t n_tiles = (num_rows * (num_q_heads / num_kv_heads) + tr - 1) / tr;
+  return num_kv_heads * n_tiles * max_chunks * tr * (head_dim + 2) * 4;
+}
+
+extern "C" int sb_partial_attention_paged_planned(
+    void* out, const void* q, const void* kv_cache, const int32_t* block_table,
+    const int32_t* positions, const int32_t* item_order, int64_t num_items, int32_t ks_first,
+    int32_t ks_rest, int32_t max_chunks, void* workspace, int64_t workspace_bytes,
+    int64_t num_rows,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+    int64_t num_blocks_total, int64_t num_blocks_per_seq, float scale, const int64_t* qs,
+    const int64_t* os, const int64_t* kvs, int32_t dtype, void* stream) {
+  const char* fn = "sb_partial_attention_paged_planned";
+  clear_error();
+  if (num_rows == 0 || num_q_heads == 0 || head_dim == 0) return SB_OK;
+  if (num_blocks_per_seq <= 0) return fail(fn, "empty block table or pool");
+  AttnArgs a;
+  bool aligned16 = false;
+  const int rc = paged_args(fn, &a, &aligned16, out, q, kv_cache, block_table, positions,
+                            num_q_heads, num_kv_heads, head_dim, block_size, num_blocks_total,
+                            scale, qs, os, kvs, dtype);
+  if (rc) return rc;
+  a.num_rows = num_rows;
+  a.nb_per_seq = num_blocks_per_seq;
+  a.kv_len = num_blocks_per_seq * block_size;
+  OrderPlan op;
+  const bool use = mfma_path(dtype, head_dim) && max_chunks > 0;
+  if (use) {
+    // The split must cover the key range in at most max_chunks chunks that each fit the
+    // kernel's staged block-table slice.
+    const int64_t cap = chunk_cap(block_size);
+    if (!item_order) return fail(fn, "null item order");
+    const int64_t n_tiles = (num_rows * (num_q_heads / num_kv_heads) +
+                             kWaveRows * kRowGroups * kWaves - 1) /
+                            (kWaveRows * kRowGroups * kWaves);
+    if (num_items != static_cast<int64_t>(max_chunks) * n_tiles * num_kv_heads)
+      return fail(fn, "num_items is not max_chunks * row tiles * num_kv_heads");
+    if (ks_first <= 0 || ks_rest <= 0 || ks_first % kTileKeys || ks_rest % kTileKeys ||
+        ks_first > cap || ks_rest > cap)
+      return fail(fn, "invalid key split");
+    AttnArgs geo{};
+    geo.ksplit_first = ks_first;
+    geo.ksplit = ks_rest;
+    if (chunk_count(geo, a.kv_len) != max_chunks)
+      return fail(fn, "max_chunks does not match the key split and the block table");
+    op.ks_first = ks_first;
+    op.ks_rest = ks_rest;
+    op.max_chunks = max_chunks;
+    op.order = item_order;
+  }
+  return launch_attention(fn, a, dtype, num_rows, aligned16, workspace, workspace_bytes,
+                          static_cast<hipStream_t>(stream), use ? &op : nullptr);
 }
 
 extern "C" int64_t sb_partial_attention_paged_varlen_workspace_size(

@@ -21,6 +21,7 @@ built from those pieces. CPU tensors are rejected: the kernels exist only for HI
 
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 
@@ -41,6 +42,8 @@ __all__ = [
     "partial_prefill",
     "partial_prefill_attention",
     "partial_prefill_attention_paged",
+    "plan_partial_attention_paged",
+    "PagedAttentionPlan",
     "partial_prefill_layer_paged",
     "PagedLayerResult",
     "qkv_projection_paged",
@@ -414,6 +417,63 @@ def partial_prefill_attention(
     return output
 
 
+class PagedAttentionPlan:
+    """Launch plan of :func:`partial_prefill_attention_paged` for one set of query positions
+    (built by :func:`plan_partial_attention_paged`): the key split and the longest-first
+    dispatch order of the work items, on the device. One request's plan serves every layer."""
+
+    def __init__(self, num_rows, num_q_heads, num_kv_heads, head_dim, block_size,
+                 num_blocks_per_seq, dtype, ks_first, ks_rest, max_chunks, order):
+        self.num_rows, self.num_q_heads, self.num_kv_heads = num_rows, num_q_heads, num_kv_heads
+        self.head_dim, self.block_size = head_dim, block_size
+        self.num_blocks_per_seq, self.dtype = num_blocks_per_seq, dtype
+        self.ks_first, self.ks_rest, self.max_chunks = ks_first, ks_rest, max_chunks
+        self.order = order  # int32 device tensor (empty when the MFMA kernel does not apply)
+
+    def matches(self, num_rows, num_q_heads, num_kv_heads, head_dim, block_size,
+                num_blocks_per_seq, dtype) -> bool:
+        return (self.num_rows, self.num_q_heads, self.num_kv_heads, self.head_dim,
+                self.block_size, self.num_blocks_per_seq, self.dtype) == (
+                    num_rows, num_q_heads, num_kv_heads, head_dim, block_size,
+                    num_blocks_per_seq, dtype)
+
+
+def plan_partial_attention_paged(
+    compute_positions,
+    num_q_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    block_size: int,
+    num_blocks_per_seq: int,
+    dtype: torch.dtype,
+    device,
+) -> PagedAttentionPlan:
+    """Plan :func:`partial_prefill_attention_paged` for the given query positions (host data;
+    a device tensor is read back once): the longest-first order in which its work items are
+    dispatched, and a key split whose later chunks may be shorter than the first, chosen so
+    that the last workgroups finish together. Results are correct for any positions; the plan
+    makes the launch fastest for these. Extension with no reference counterpart."""
+    dev = torch.device(device)
+    pos = torch.as_tensor(compute_positions).reshape(-1).to("cpu", torch.int32).contiguous()
+    dt = _lib.dtype_code(torch.empty(0, dtype=dtype))
+    args = (ctypes.cast(pos.data_ptr(), _lib.I32P), pos.numel(),
+            num_q_heads, num_kv_heads, head_dim, block_size, num_blocks_per_seq, dt)
+    need = _lib.size_query("sb_partial_attention_paged_plan", *args, None, 0)
+    if need < 3:
+        raise RuntimeError("sb_partial_attention_paged_plan failed: "
+                           + _lib.lib().sb_last_error_string().decode())
+    buf = torch.empty(need, dtype=torch.int32)
+    got = _lib.size_query("sb_partial_attention_paged_plan", *args,
+                          ctypes.cast(buf.data_ptr(), _lib.I32P), need)
+    if got != need:
+        raise RuntimeError("sb_partial_attention_paged_plan failed: "
+                           + _lib.lib().sb_last_error_string().decode())
+    ks_first, ks_rest, max_chunks = (int(v) for v in buf[:3])
+    order = buf[3:].to(dev) if need > 3 else torch.empty(0, dtype=torch.int32, device=dev)
+    return PagedAttentionPlan(pos.numel(), num_q_heads, num_kv_heads, head_dim, block_size,
+                              num_blocks_per_seq, dtype, ks_first, ks_rest, max_chunks, order)
+
+
 def partial_prefill_attention_paged(
     query: torch.Tensor,
     kv_cache: torch.Tensor,
@@ -421,6 +481,7 @@ def partial_prefill_attention_paged(
     compute_positions: torch.Tensor,
     scale: float | None = None,
     out: torch.Tensor | None = None,
+    plan: PagedAttentionPlan | None = None,
 ) -> torch.Tensor:
     """GQA causal attention over a paged cache for a compact set of query rows.
 
@@ -433,6 +494,9 @@ def partial_prefill_attention_paged(
     ``[0, len(block_table) * block_size)``: one at or past the end attends the whole table,
     and a row with a negative position is left unwritten (no memory outside the inputs is
     touched either way).
+    ``plan``: from :func:`plan_partial_attention_paged` for these positions (same row count,
+    heads, head_dim, block size, table length and dtype), to launch with its split and
+    longest-first order.
     Extension with no reference counterpart: the reference attention is MHA over contiguous
     K/V (semblend_core/triton_kernels.py:655-734), gathered from the cache by its callers.
     """
@@ -458,6 +522,26 @@ def partial_prefill_attention_paged(
         raise ValueError("compute_positions must have one entry per query row")
     bt = _lib.as_index(block_table, dev)
     dt = _lib.dtype_code(q)
+    if plan is not None:
+        if not plan.matches(num_rows, num_q_heads, num_kv_heads, head_dim, block_size,
+                            bt.shape[0], q.dtype):
+            raise ValueError("plan was made for another shape (rows, heads, head_dim, block "
+                             "size, block-table length or dtype)")
+        ws_bytes = _lib.size_query("sb_partial_attention_paged_planned_workspace_size",
+                                   num_rows, num_q_heads, num_kv_heads, head_dim,
+                                   plan.max_chunks, dt)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+        with _lib.on_device(dev):
+            _lib.call(
+                "sb_partial_attention_paged_planned",
+                out.data_ptr(), q.data_ptr(), kv.data_ptr(), bt.data_ptr(), pos.data_ptr(),
+                plan.order.data_ptr() if plan.order.numel() else None, plan.order.numel(),
+                plan.ks_first, plan.ks_rest, plan.max_chunks, _lib.ptr(ws), ws_bytes, num_rows, num_q_heads,
+                num_kv_heads, head_dim, block_size, nb_total, bt.shape[0], float(scale),
+                _lib.strides(q), _lib.strides(out), _lib.strides(kv), dt,
+                _lib.stream_handle(dev),
+            )
+        return out
     ws_bytes = _lib.size_query("sb_partial_attention_paged_workspace_size", num_rows,
                                num_q_heads, num_kv_heads, head_dim, block_size, bt.shape[0], dt)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None

@@ -62,9 +62,10 @@ def assert_rope_close(got: torch.Tensor, ref: torch.Tensor, composed: bool = Fal
     """RoPE parity bar (see the constants above). ``composed``: rows rotated several times
     with a rounding to the dtype in between; a rounding that falls differently in an
     intermediate step then carries through, so the bound is one ulp of the pair norm.
-    Returns element counts per clause for 16-bit dtypes: ``exact``, ``within_1ulp`` (1 ulp
-    apart, not equal) and ``norm_only`` (more than 1 ulp apart, within 2^-21 of the pair
-    norm), plus ``total``."""
+    Returns element counts per clause, plus ``total``: for 16-bit dtypes ``exact``,
+    ``within_1ulp`` (1 ulp apart, not equal) and ``norm_only`` (more than 1 ulp apart, within
+    2^-21 of the pair norm); for fp32 ``exact``, ``within_rel`` (not equal, within 1e-5 of
+    |want|) and ``floor_only`` (outside 1e-5 |want|, within the 1e-5 * 0.1 |pair| floor)."""
     got = got.cpu()
     ref = ref.cpu()
     assert got.shape == ref.shape and got.dtype == ref.dtype
@@ -73,7 +74,10 @@ def assert_rope_close(got: torch.Tensor, ref: torch.Tensor, composed: bool = Fal
     if got.dtype == torch.float32:
         allowed = ROPE_F32_RTOL * torch.maximum(ref.abs(), 0.1 * norm)
         bad = diff > allowed
-        stats = {"total": bad.numel()}
+        by_rel = diff <= ROPE_F32_RTOL * ref.abs()
+        stats = {"total": bad.numel(), "exact": int((diff == 0).sum()),
+                 "within_rel": int(((diff > 0) & by_rel).sum()),
+                 "floor_only": int((~by_rel & ~bad).sum())}
     else:
         ulps = ulp_distance(got, ref)
         by_norm = diff <= ROPE_16_NORM_TOL * norm

@@ -177,15 +177,14 @@ def test_dense_workspace_covers_every_row_count(heads, seq_len):
     """The dense drop-in splits its key range by the row count its kernels find on the device,
     so its workspace must hold the split-key partials of every count. The requirement of one
     count is the library's own single-call plan for that many rows, read through the paged
-    query (block size 16: its block-table cap of 16384 keys does not bind at these lengths,
-    so the two plans coincide)."""
+    query (block size 32: its chunk cap of 1023 blocks, 32736 keys, does not bind at these
+    lengths, so the two plans coincide)."""
     idx = ((seq_len + 1) * 4 + 255) // 256 * 256
     dense = _lib.size_query("sb_partial_prefill_attention_workspace_size", heads, seq_len, 128, 2)
     need = 0
     for rows in list(range(1, seq_len + 1, 128)) + [seq_len]:
         need = max(need, _lib.size_query("sb_partial_attention_paged_workspace_size", rows, heads,
-                                         heads, 128, 16, seq_len // 16 if seq_len % 16 == 0
-                                         else seq_len // 16 + 1, 2))
+                                         heads, 128, 32, -(-seq_len // 32), 2))
     assert need > 0
     assert dense - idx >= need
 
@@ -196,3 +195,88 @@ def test_kernel_timing_log_without_launches():
     _lib.kernel_timing(False)
     rc = _lib.lib().sb_kernel_timing_read(None, None, None)
     assert rc == _lib.SB_ERR_INVALID_ARGUMENT
+
+
+def _plan(pos, hq=28, hkv=4, d=128, bs=16, nbps=1024, dtype=2):
+    import torch
+
+    p = torch.as_tensor(pos, dtype=torch.int32).contiguous()
+    ptr = ctypes.cast(p.data_ptr(), _lib.I32P)
+    need = _lib.size_query("sb_partial_attention_paged_plan", ptr, p.numel(), hq, hkv, d, bs,
+                           nbps, dtype, None, 0)
+    buf = torch.zeros(max(need, 1), dtype=torch.int32)
+    got = _lib.size_query("sb_partial_attention_paged_plan", ptr, p.numel(), hq, hkv, d, bs,
+                          nbps, dtype, ctypes.cast(buf.data_ptr(), _lib.I32P), need)
+    assert got == need
+    return buf[:need].tolist()
+
+
+@pytest.mark.parametrize("seed,rows,sort", [(0, 2458, True), (1, 700, True), (2, 2458, False),
+                                            (3, 40, True)])
+def test_attention_plan_orders_every_item_longest_first(seed, rows, sort):
+    """The host plan of the paged attention (7B shape: 28/4 heads, 16384-token table): its
+    split covers the key range in max_chunks chunks that fit the kernel's block-table slice;
+    its order is a permutation of every work item of the launch, and the items' key counts
+    (recomputed here from the positions, with the kernel's item encoding and chunk rule) never
+    increase along it."""
+    import torch
+
+    g = torch.Generator("cpu").manual_seed(seed)
+    pos = torch.randperm(16384, generator=g)[:rows]
+    if sort:
+        pos = pos.sort().values
+    plan = _plan(pos)
+    ks1, ks2, mc = plan[:3]
+    order = plan[3:]
+    assert ks1 > 0 and ks2 > 0 and ks1 % 64 == 0 and ks2 % 64 == 0 and ks1 <= 1024 * 16
+    chunks = 1 if 16384 <= ks1 else 1 + -(-(16384 - ks1) // ks2)
+    assert mc == chunks
+    tr, group, hkv = 128, 7, 4
+    n_tiles = -(-rows * group // tr)
+    assert sorted(order) == list(range(mc * n_tiles * hkv))
+    kend = [max(int(pos[r // group]) for r in range(t * tr, min((t + 1) * tr, rows * group)))
+            + 1 for t in range(n_tiles)]
+
+    def keys(b):
+        rest = b // hkv
+        tile = n_tiles - 1 - rest % n_tiles
+        c = rest // n_tiles
+        k0 = 0 if c == 0 else ks1 + (c - 1) * ks2
+        k1 = min(k0 + (ks1 if c == 0 else ks2), kend[tile])
+        return max(0, -(-(k1 - k0) // 64))
+
+    costs = [keys(b) for b in order]
+    assert all(a >= b for a, b in zip(costs, costs[1:]))
+
+
+def test_attention_plan_edge_cases():
+    lib = _lib.lib()
+    # fp32 (the VALU kernel): no split, no items
+    assert _plan([5, 9, 100], dtype=0) == [0, 0, 0]
+    # a capacity below the need, and bad shapes, are refused
+    import torch
+
+    p = torch.tensor([1, 2, 3], dtype=torch.int32)
+    ptr = ctypes.cast(p.data_ptr(), _lib.I32P)
+    small = torch.zeros(4, dtype=torch.int32)
+    rc = _lib.size_query("sb_partial_attention_paged_plan", ptr, 3, 28, 4, 128, 16, 64, 2,
+                         ctypes.cast(small.data_ptr(), _lib.I32P), 4)
+    assert rc == -_lib.SB_ERR_INVALID_ARGUMENT
+    assert b"too small" in lib.sb_last_error_string()
+    assert _lib.size_query("sb_partial_attention_paged_plan", ptr, 3, 28, 5, 128, 16, 64, 2,
+                           None, 0) < 0
+    # the planned launch rejects a split that does not match max_chunks, before any launch
+    fake = 4096
+    rc = lib.sb_partial_attention_paged_planned(
+        fake, fake, fake, fake, fake, fake, 12, 8640, 4288, 2, None, 0, 10, 28, 4, 128, 16, 2048,
+        1024, 0.1, _i64(1, 1, 1), _i64(1, 1, 1), _i64(1, 1, 1, 1, 1), 2, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"max_chunks" in lib.sb_last_error_string()
+    rc = lib.sb_partial_attention_paged_planned(
+        fake, fake, fake, fake, fake, fake, 12, 8001, 4288, 3, None, 0, 10, 28, 4, 128, 16, 2048,
+        1024, 0.1, _i64(1, 1, 1), _i64(1, 1, 1), _i64(1, 1, 1, 1, 1), 2, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"split" in lib.sb_last_error_string()
+    # 10 rows x 7 q-heads per KV head = 1 row tile: 3 chunks x 1 x 4 heads = 12 items
+    rc = lib.sb_partial_attention_paged_planned(
+        fake, fake, fake, fake, fake, fake, 11, 8640, 4288, 3, None, 0, 10, 28, 4, 128, 16,
+        2048, 1024, 0.1, _i64(1, 1, 1), _i64(1, 1, 1), _i64(1, 1, 1, 1, 1), 2, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"num_items" in lib.sb_last_error_string()

@@ -234,3 +234,58 @@ def test_paged_gqa_rising_scores_rescale(dev, dtype):
     # the softmax is peaked: most rows put nearly all weight on a few late keys
     assert float(want.abs().amax()) > 1.0
     assert_attn_close(got, want)
+
+
+# ---- host-planned launches (split + longest-first order) ----
+
+def test_paged_gqa_planned_bench_workload(dev):
+    """The planned launch on the bench's 7B inputs: every row against the oracle, and a
+    plan of other positions (same shape) is still correct, only slower."""
+    inp = bench.build_inputs(dev)
+    q, kv, pos, bt = inp["attn_q"], inp["attn_kv"], inp["attn_pos"], inp["block_table"]
+    plan = tk.plan_partial_attention_paged(inp["pos_cpu"], 28, 4, 128, 16, bt.shape[0],
+                                           torch.bfloat16, dev)
+    assert plan.max_chunks >= 2 and plan.ks_rest < plan.ks_first
+    got = tk.partial_prefill_attention_paged(q, kv, bt, pos, plan=plan)
+    want = ref.partial_attention_paged(q.cpu(), kv.cpu(), bt.cpu(), pos.cpu())
+    assert_attn_close(got.cpu(), want)
+    other = recompute_set(16384, pos.shape[0], 5)
+    plan2 = tk.plan_partial_attention_paged(other, 28, 4, 128, 16, bt.shape[0], torch.bfloat16,
+                                            dev)
+    got2 = tk.partial_prefill_attention_paged(q, kv, bt, pos, plan=plan2)
+    assert_attn_close(got2.cpu(), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv,d,seq,rows,bs", [(28, 4, 128, 4096, 600, 16),
+                                                   (32, 8, 128, 8192, 800, 16),
+                                                   (14, 2, 64, 3000, 450, 32),
+                                                   (8, 8, 128, 2048, 300, 24)])
+def test_paged_gqa_planned_shapes(dev, dtype, hq, hkv, d, seq, rows, bs):
+    q, kv, bt, pos = _paged_case(hq, hkv, d, seq, rows, dtype, 130 + hq + bs, bs=bs)
+    plan = tk.plan_partial_attention_paged(pos, hq, hkv, d, bs, bt.shape[0], dtype, dev)
+    got = tk.partial_prefill_attention_paged(q.to(dev), kv.to(dev), bt.to(dev), pos.to(dev),
+                                             plan=plan)
+    assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
+
+
+def test_paged_gqa_planned_unsorted_and_fp32(dev):
+    """Positions in any order (the plan reads them as given); fp32 takes the VALU kernel,
+    for which the plan is empty."""
+    q, kv, bt, pos = _paged_case(28, 4, 128, 2048, 400, torch.bfloat16, 140)
+    perm = torch.randperm(pos.shape[0], generator=gen(141))
+    q, pos = q[perm].contiguous(), pos[perm].contiguous()
+    plan = tk.plan_partial_attention_paged(pos, 28, 4, 128, 16, bt.shape[0], torch.bfloat16, dev)
+    got = tk.partial_prefill_attention_paged(q.to(dev), kv.to(dev), bt.to(dev), pos.to(dev),
+                                             plan=plan)
+    assert_attn_close(got, ref.partial_attention_paged(q, kv, bt, pos))
+    q32, kv32 = q.float(), kv.float()
+    plan32 = tk.plan_partial_attention_paged(pos, 28, 4, 128, 16, bt.shape[0], torch.float32,
+                                             dev)
+    assert plan32.max_chunks == 0 and plan32.order.numel() == 0
+    got32 = tk.partial_prefill_attention_paged(q32.to(dev), kv32.to(dev), bt.to(dev),
+                                               pos.to(dev), plan=plan32)
+    assert_attn_close(got32, ref.partial_attention_paged(q32, kv32, bt, pos))
+    with pytest.raises(ValueError, match="another shape"):
+        tk.partial_prefill_attention_paged(q.to(dev)[:10], kv.to(dev), bt.to(dev),
+                                           pos.to(dev)[:10], plan=plan)

@@ -282,3 +282,27 @@ def test_graph_delta_rope_uploaded_positions(dev, n):
         for c, s in zip(caches, shadow):
             assert torch.equal(c.view(torch.int16), s.view(torch.int16))
     assert not torch.equal(caches[1].view(torch.int16), start[1].view(torch.int16))
+
+
+def test_graph_attention_paged_planned(dev):
+    hq, hkv, d, bs, seq, rows = 28, 4, 128, 16, 8192, 900
+    nb = seq // bs + 8
+    kv = randn((nb, 2, hkv, bs, d), torch.bfloat16, 90).to(dev)
+    bt = torch.randperm(nb, generator=gen(91))[: seq // bs].to(torch.int32).to(dev)
+    pos_h = torch.randperm(seq, generator=gen(92))[:rows].sort().values.to(torch.int32)
+    pos = pos_h.to(dev)
+    q = randn((rows, hq, d), torch.bfloat16, 93).to(dev)
+    plan = tk.plan_partial_attention_paged(pos_h, hq, hkv, d, bs, seq // bs, torch.bfloat16,
+                                           dev)
+    out = torch.empty_like(q)
+    tk.partial_prefill_attention_paged(q, kv, bt, pos, out=out, plan=plan)
+    torch.cuda.synchronize()
+    want = out.clone()
+    g = _capture(lambda: tk.partial_prefill_attention_paged(q, kv, bt, pos, out=out, plan=plan))
+    for _ in range(3):
+        out.zero_()
+        _noise(dev)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))

@@ -225,6 +225,17 @@ def test_rope_bar_clause_statistics(dev, capsys):
         print(f"\n[rope bar] 7B layer, bf16 K: {stats}")
     assert stats["exact"] + stats["within_1ulp"] + stats["norm_only"] == stats["total"]
     assert stats["norm_only"] <= 1e-4 * stats["total"]
+    # the same layer in fp32: how many elements pass only by the 0.1 |pair| floor
+    kv32 = torch.zeros((2048, 2, 4, 16, 128), dtype=torch.float32)
+    donor32 = randn((2, 4, 16384, 128), torch.float32, 70)
+    got = rc.rope_correct_scatter_paged(kv32.to(dev), donor32.to(dev), bt.to(dev), dp.to(dev),
+                                        tp.to(dev), rope_base=1e6).cpu()
+    want = ref.rope_correct_scatter_paged(kv32.clone(), donor32, bt, dp, tp, rope_base=1e6)
+    stats = assert_rope_close(got[slots, 0], want[slots, 0])
+    with capsys.disabled():
+        print(f"[rope bar] 7B layer, fp32 K: {stats}")
+    assert stats["exact"] + stats["within_rel"] + stats["floor_only"] == stats["total"]
+    assert stats["floor_only"] <= 1e-4 * stats["total"]
 
 
 # ---- apply_rope_delta_inplace (rope_correction.py:699-783) ----
