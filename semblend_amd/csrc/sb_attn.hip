@@ -502,39 +502,109 @@ attn_mfma_kernel(const AttnBatch batch) {
   if (item.tile < 0 || item.chunk >= a.max_chunks) return;  // uniform, before any barrier
   const int kvh = item.kvh;
 
+  // The chunk's first key and its end within the table are known from the item alone, so
+  // everything that needs only them (the block-table slice, the key offsets of the first
+  // three tiles, the Q fragments of paged calls) is requested together with the positions,
+  // and one barrier publishes it all: one global round trip before the first tile loads.
+  const int k0 = chunk_begin(a, item.chunk);
+  if (k0 >= a.kv_len) return;  // uniform, before any barrier
+  const int kc = static_cast<int>(min(static_cast<int64_t>(k0 + chunk_len(a, item.chunk)),
+                                      a.kv_len));
+  int lb0 = 0;
+  if (kPaged) {
+    lb0 = static_cast<int>(k0 / a.block_size);
+    const int nb = static_cast<int>((kc - 1) / a.block_size) - lb0 + 1;  // <= kBtLds
+    for (int i = tid; i < nb; i += kThreads) bt_s[i] = clamp_block(a, a.block_table[lb0 + i]);
+  }
+  const char* kbase = a.k + kvh * a.k_s_head;
+  const char* vbase = a.v + kvh * a.v_s_head;
+  // Byte offset of key `key` relative to kbase / vbase, the key's block given (paged K and V
+  // rows share one offset, kept in kofs only).
+  auto key_offset = [&](int key, int pb) -> uint64_t {
+    if (AM == kAddrPagedNarrow) {
+      const uint32_t in_block =
+          static_cast<uint32_t>(key) & (static_cast<uint32_t>(a.block_size) - 1u);
+      return static_cast<uint64_t>(static_cast<uint32_t>(pb)) *
+                 static_cast<uint32_t>(a.s_block) +
+             __umul24(in_block, static_cast<uint32_t>(a.s_pos));
+    }
+    const int lb = a.bs_log2 >= 0 ? key >> a.bs_log2 : key / static_cast<int>(a.block_size);
+    return static_cast<uint64_t>(pb) * a.s_block +
+           static_cast<uint64_t>(key - lb * a.block_size) * a.s_pos;
+  };
+  auto key_block = [&](int key) -> int {
+    if (AM == kAddrPagedNarrow) return key >> a.bs_log2;  // power-of-two blocks
+    return a.bs_log2 >= 0 ? key >> a.bs_log2 : key / static_cast<int>(a.block_size);
+  };
+  // Offsets of the keys of tile `slot` (keys past kc_lim are clamped to it: masked later),
+  // the blocks read from the staged slice.
+  int kc_lim = kc - 1;
+  auto fill_offsets = [&](int slot, int t0, int i) {
+    const int key = min(t0 + i, kc_lim);
+    if (kPaged) {
+      kofs[slot][i] = key_offset(key, bt_s[key_block(key) - lb0]);
+    } else {
+      kofs[slot][i] = static_cast<uint64_t>(key) * a.k_s_seq;
+      vofs[slot][i] = static_cast<uint64_t>(key) * a.v_s_seq;
+    }
+  };
+  // The first three tiles' offsets, with the blocks read from the global table (the same
+  // lines the slice loads fetch) so that they do not wait for the slice.
+  if (tid < 3 * kTileKeys) {
+    const int key = min(k0 + tid, kc_lim);
+    const int slot = tid / kTileKeys, i = tid % kTileKeys;
+    if (kPaged) {
+      kofs[slot][i] = key_offset(key, clamp_block(a, a.block_table[key_block(key)]));
+    } else {
+      kofs[slot][i] = static_cast<uint64_t>(key) * a.k_s_seq;
+      vofs[slot][i] = static_cast<uint64_t>(key) * a.v_s_seq;
+    }
+  }
+
   // This lane's query rows: one per row group.
   int p[RG], qh[RG];
   int64_t qrow[RG];
   int pmax_l = -1;
+  vec8 qf[RG][NKS];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
     const int64_t r = item.tile * TR + (wave * RG + g) * kWaveRows + lq;
     p[g] = -1;
     qrow[g] = 0;
     qh[g] = 0;
-    if (r < rows_kv) {
+    const bool valid = r < rows_kv;
+    if (valid) {
       const int64_t pi = r / a.group;
       qh[g] = kvh * a.group + static_cast<int>(r - pi * a.group);
       int pp = a.positions[pi];
       if (pp >= a.kv_len) pp = static_cast<int>(a.kv_len - 1);
-      qrow[g] = a.q_by_position ? pp : pi;
+      qrow[g] = a.q_by_position ? max(pp, 0) : pi;
       p[g] = pp < 0 ? -1 : pp;
     }
     pmax_l = max(pmax_l, p[g]);
+    // Q fragments (B operand), the query rows as given; a paged call's row address does
+    // not depend on its position, so these loads go out with the position's.
+    const char* qp = a.q + qrow[g] * a.q_s_row + qh[g] * a.q_s_head;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      vec8 v = {};
+      if (valid) v = *reinterpret_cast<const vec8*>(qp + (16 * s + 8 * lg) * 2);
+      qf[g][s] = v;
+    }
   }
   // Wave-uniform values are moved to scalar registers (readfirstlane) so that the compiler
   // sees them as uniform: branches on them stay scalar branches instead of being turned into
   // per-lane selects (the mask below would otherwise run on every tile).
   const int pmax_w = __builtin_amdgcn_readfirstlane(wave_max_i(pmax_l));
   if (lane == 0) red_max[wave] = pmax_w;
-  __syncthreads();
+  __syncthreads();  // red_max, the block-table slice and the first offset tables
   int kend_l = red_max[0];
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) kend_l = max(kend_l, red_max[w]);
   const int kend = __builtin_amdgcn_readfirstlane(kend_l) + 1;
-  const int k0 = chunk_begin(a, item.chunk);
   if (k0 >= kend) return;  // uniform: kend comes from shared memory
-  const int k1 = min(k0 + chunk_len(a, item.chunk), kend);
+  const int k1 = min(kc, kend);
+  kc_lim = k1 - 1;
   const int nchunks = chunk_count(a, kend);
   int plim[RG];  // keys beyond the chunk are masked as well
   int pmin_l = 0x7fffffff;
@@ -542,61 +612,14 @@ attn_mfma_kernel(const AttnBatch batch) {
   for (int g = 0; g < RG; ++g) {
     plim[g] = min(p[g], k1 - 1);
     if (p[g] >= 0) pmin_l = min(pmin_l, plim[g]);
+    if (p[g] < 0) {  // a row with no position (negative) reads nothing: zero query
+#pragma unroll
+      for (int s = 0; s < NKS; ++s) qf[g][s] = vec8{};
+    }
   }
   const int pmin_w = __builtin_amdgcn_readfirstlane(wave_min_i(pmin_l));
   const int pmax_c = min(pmax_w, k1 - 1);
-
-  // Q fragments (B operand), the query rows as given.
-  vec8 qf[RG][NKS];
-#pragma unroll
-  for (int g = 0; g < RG; ++g) {
-    const char* qp = a.q + qrow[g] * a.q_s_row + qh[g] * a.q_s_head;
-#pragma unroll
-    for (int s = 0; s < NKS; ++s) {
-      vec8 v = {};
-      if (p[g] >= 0) v = *reinterpret_cast<const vec8*>(qp + (16 * s + 8 * lg) * 2);
-      qf[g][s] = v;
-    }
-  }
   const float c_log2 = a.scale_log2;  // scale * log2(e): score units -> log2 domain
-
-  // Stage the chunk's block-table slice, then the key-offset tables of the first three tiles.
-  int lb0 = 0;
-  if (kPaged) {
-    lb0 = static_cast<int>(k0 / a.block_size);
-    const int nb = static_cast<int>((k1 - 1) / a.block_size) - lb0 + 1;
-    for (int i = tid; i < nb; i += kThreads) bt_s[i] = clamp_block(a, a.block_table[lb0 + i]);
-    __syncthreads();
-  }
-  const char* kbase = a.k + kvh * a.k_s_head;
-  const char* vbase = a.v + kvh * a.v_s_head;
-  // Byte offsets of key `key` (clamped into [k0, k1)) relative to kbase / vbase. Paged K
-  // and V rows share one offset, kept in kofs only.
-  auto fill_offsets = [&](int slot, int t0, int i) {
-    const int key = min(t0 + i, k1 - 1);
-    if (kPaged) {
-      uint64_t off;
-      if (AM == kAddrPagedNarrow) {
-        const int lb = key >> a.bs_log2;
-        const uint32_t in_block =
-            static_cast<uint32_t>(key) & (static_cast<uint32_t>(a.block_size) - 1u);
-        off = static_cast<uint64_t>(static_cast<uint32_t>(bt_s[lb - lb0])) *
-                  static_cast<uint32_t>(a.s_block) +
-              __umul24(in_block, static_cast<uint32_t>(a.s_pos));
-      } else {
-        const int lb = a.bs_log2 >= 0 ? key >> a.bs_log2 : key / static_cast<int>(a.block_size);
-        off = static_cast<uint64_t>(bt_s[lb - lb0]) * a.s_block +
-              static_cast<uint64_t>(key - lb * a.block_size) * a.s_pos;
-      }
-      kofs[slot][i] = off;
-    } else {
-      kofs[slot][i] = static_cast<uint64_t>(key) * a.k_s_seq;
-      vofs[slot][i] = static_cast<uint64_t>(key) * a.v_s_seq;
-    }
-  };
-  if (tid < 3 * kTileKeys) fill_offsets(tid / kTileKeys, k0 + (tid / kTileKeys) * kTileKeys,
-                                        tid % kTileKeys);
-  __syncthreads();
 
   // Softmax state per row: O and l are relative to a reference max m_ref (log2 domain,
   // of scale * log2(e) * s); negm = -m_ref enters every exp2 through one fma. A row is
