@@ -524,10 +524,12 @@ def rope_scatter_section(dev: torch.device, inp, steps: int) -> dict:
     """Fused RoPE scatter of the 28-layer scatter workload (same 13926 pairs and bytes), from
     one donor (``rope_correct_scatter_paged_layers``) and as a composite from four donors
     (each 256-token target chunk owned by a random one of four 16384-token donors,
-    ``composite_scatter_paged_layers``), K rotated by a per-chunk delta. Graph replays timed
-    with HIP events."""
+    ``prepare_composite_scatter_paged_layers``, pairs grouped by donor; and, as
+    ``four_donors_indexed``, the per-call form with a per-pair donor index), K rotated by a
+    per-chunk delta. Graph replays timed with HIP events."""
     from semblend_amd import rope_correction as rc
-    from semblend_amd.multi_donor import composite_scatter_paged_layers
+    from semblend_amd.multi_donor import (composite_scatter_paged_layers,
+                                          prepare_composite_scatter_paged_layers)
 
     g = torch.Generator("cpu").manual_seed(3)
     gd = torch.Generator(dev).manual_seed(3)
@@ -544,12 +546,18 @@ def rope_scatter_section(dev: torch.device, inp, steps: int) -> dict:
         rc.rope_correct_scatter_paged_layers(inp["caches"], inp["donors"], inp["block_table"],
                                              inp["sc_d"], inp["sc_t"], rope_base=ROPE_BASE)
 
-    def four_donors():
+    def four_donors_indexed():
         composite_scatter_paged_layers(inp["caches"], donors, inp["block_table"], didx,
                                        inp["sc_d"], inp["sc_t"], rope=True, rope_base=ROPE_BASE)
 
+    # bound once per request, pairs grouped by donor (each workgroup's pairs share a donor)
+    four_donors = prepare_composite_scatter_paged_layers(
+        inp["caches"], donors, inp["block_table"], didx.cpu(), inp["sc_d"].cpu(),
+        inp["sc_t"].cpu(), rope=True, rope_base=ROPE_BASE)
+
     out = {"pairs": int(n_pairs), "bytes": nbytes}
-    for name, fn in (("one_donor", one_donor), ("four_donors", four_donors)):
+    for name, fn in (("one_donor", one_donor), ("four_donors", four_donors),
+                     ("four_donors_indexed", four_donors_indexed)):
         gr = capture(fn)
         gr.replay()
         torch.cuda.synchronize()

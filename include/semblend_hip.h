@@ -220,6 +220,29 @@ int sb_composite_scatter_paged_layers(const uint64_t* kv_layer_ptrs, int64_t num
                                       int64_t num_blocks_per_seq, const int64_t* kv_strides,
                                       int32_t dtype, int32_t flags, void* stream);
 
+/* sb_composite_scatter_paged_layers with the pairs grouped by donor instead of a per-pair
+ * donor index: donor k's pairs occupy [segment_ends[k-1], segment_ends[k]) of donor_pos /
+ * target_pos (segment_ends: host [num_donors], each end but the last a multiple of 256, the
+ * last equal to num_pairs; a segment is padded with pairs whose positions are -1, which are
+ * skipped). Every workgroup's pairs then share one donor, so its strides and layer table are
+ * read once per workgroup instead of once per pair. At most 16 donors. Same results as the
+ * indexed form. No reference counterpart (see sb_composite_scatter_paged_layers). */
+int sb_composite_scatter_paged_layers_grouped(const uint64_t* kv_layer_ptrs,
+                                              int64_t num_layers,
+                                              const uint64_t* donor_layer_ptrs,
+                                              int64_t num_donors,
+                                              const int64_t* donor_strides,
+                                              const int64_t* segment_ends,
+                                              const int32_t* donor_pos,
+                                              const int32_t* target_pos,
+                                              const float* inv_freq, int64_t num_pairs,
+                                              int64_t num_heads, int64_t block_size,
+                                              int64_t head_dim, const int32_t* block_table,
+                                              int64_t num_blocks_total,
+                                              int64_t num_blocks_per_seq,
+                                              const int64_t* kv_strides, int32_t dtype,
+                                              int32_t flags, void* stream);
+
 /* Flat RoPE correction over k [L, H, S, D] (k_strides[4]; pass L = 1 for [H, S, D]):
  * for each pair i in order, the row at donor position d_i is rotated by (t_i - d_i) and
  * rounded to dtype; rows hit by several pairs are rotated once per pair, in pair order.

@@ -24,6 +24,8 @@ SB_ERR_INVALID_ARGUMENT = 100001
 SB_SCATTER_REPEATED_DONOR_ROWS = 1
 # Most positions the in-place delta RoPE takes by value in its launch (host arrays).
 SB_INLINE_POSITIONS_MAX = 256
+# Segment alignment (pairs) of the donor-grouped composite scatter.
+SB_GROUPED_PAIR_ALIGN = 256
 # Constant RoPE deltas must lie strictly within +-2^31 (the C ABI's check; the kernels'
 # sin/cos reduce angles below 2^32 exactly).
 MAX_ROPE_DELTA = 1 << 31
@@ -53,6 +55,9 @@ SIGNATURES: dict[str, list] = {
     "sb_composite_scatter_paged_layers": [_vp, _i64, _vp, _i64, _i64p, _vp, _vp, _vp, _vp,
                                           _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64p, _i32,
                                           _i32, _vp],
+    "sb_composite_scatter_paged_layers_grouped": [_vp, _i64, _vp, _i64, _i64p, _i64p, _vp, _vp,
+                                                  _vp, _i64, _i64, _i64, _i64, _vp, _i64, _i64,
+                                                  _i64p, _i32, _i32, _vp],
     "sb_rope_correct_k": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p,
                           _i64p, _i32, _vp],
     "sb_rope_correct_k_distinct": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64p,

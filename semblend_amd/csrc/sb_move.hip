@@ -110,7 +110,15 @@ struct DonorSet {
   int64_t s_seq[kMaxDonors];
   int64_t bound[kMaxDonors];   // rows held by each donor tensor
   int64_t first_pos[kMaxDonors];  // sequence position of each donor tensor's row 0
+  // Grouped launches (grouped != 0): the pairs are grouped by donor, donor k's pairs (padded
+  // with skipped pairs) ending at pair seg_end[k], every boundary a multiple of
+  // kGroupedPairAlign, so that each workgroup's pairs share one donor; index is unused.
+  int grouped;
+  int64_t seg_end[kMaxDonors];
 };
+// Boundary alignment of grouped launches: a multiple of every workgroup's pair count
+// (kThreads / threads-per-row, a power of two up to kThreads).
+constexpr int64_t kGroupedPairAlign = 256;
 
 struct MoveArgs {
   RowSide src, dst;
@@ -339,8 +347,18 @@ void move_rows_kernel(MoveArgs a, InlineArg<INLINE> ix) {
   RowSide src = a.src;
   int64_t src_off, dst_off;
   if (SRCM == ROW_DONOR_POS) {
-    const int dn = a.donors.index[i] - a.donors.first;
-    if (dn < 0 || dn >= a.donors.count) return;  // another launch's donor, or invalid
+    int dn;
+    if (a.donors.grouped) {
+      // The workgroup's donor, from its first pair: uniform, so the donor's strides and layer
+      // table come through scalar loads.
+      const int64_t first_pair = static_cast<int64_t>(blockIdx.x) * (kThreads >> a.tpr_log2);
+      int k = 0;
+      while (k + 1 < a.donors.count && first_pair >= a.donors.seg_end[k]) ++k;
+      dn = __builtin_amdgcn_readfirstlane(k);
+    } else {
+      dn = a.donors.index[i] - a.donors.first;
+      if (dn < 0 || dn >= a.donors.count) return;  // another launch's donor, or invalid
+    }
     src.layers = a.donors.layers + static_cast<int64_t>(a.donors.first + dn) * a.num_layers;
     src.s_kv = a.donors.s_kv[dn];
     src.s_head = a.donors.s_head[dn];
@@ -934,21 +952,32 @@ extern "C" int sb_rope_correct_scatter_paged_layers(
 // Composite (multi-donor) scatter over many layers: pair i moves donor
 // donor_index[i]'s rows at donor_pos[i] to target_pos[i] of every layer's paged cache,
 // rotating K by (target - donor) when inv_freq is given.
-extern "C" int sb_composite_scatter_paged_layers(
-    const uint64_t* kv_layer_ptrs, int64_t num_layers, const uint64_t* donor_layer_ptrs,
-    int64_t num_donors, const int64_t* donor_strides, const int32_t* donor_index,
-    const int32_t* donor_pos, const int32_t* target_pos, const float* inv_freq,
-    int64_t num_pairs, int64_t num_heads, int64_t block_size, int64_t head_dim,
-    const int32_t* block_table, int64_t num_blocks_total, int64_t num_blocks_per_seq,
-    const int64_t* kv_strides, int32_t dtype, int32_t flags, void* stream) {
-  const char* fn = "sb_composite_scatter_paged_layers";
+static int composite_impl(
+    const char* fn, const uint64_t* kv_layer_ptrs, int64_t num_layers,
+    const uint64_t* donor_layer_ptrs, int64_t num_donors, const int64_t* donor_strides,
+    const int32_t* donor_index, const int64_t* segment_ends, const int32_t* donor_pos,
+    const int32_t* target_pos, const float* inv_freq, int64_t num_pairs, int64_t num_heads,
+    int64_t block_size, int64_t head_dim, const int32_t* block_table, int64_t num_blocks_total,
+    int64_t num_blocks_per_seq, const int64_t* kv_strides, int32_t dtype, int32_t flags,
+    void* stream) {
   clear_error();
   if (num_pairs == 0 || num_layers == 0 || num_heads == 0 || head_dim == 0 || num_donors == 0)
     return SB_OK;
   if (!valid_dtype(dtype)) return fail(fn, "invalid dtype");
-  if (!kv_layer_ptrs || !donor_layer_ptrs || !donor_strides || !donor_index || !donor_pos ||
-      !target_pos || !block_table || !kv_strides)
+  if (!kv_layer_ptrs || !donor_layer_ptrs || !donor_strides || (!donor_index && !segment_ends) ||
+      !donor_pos || !target_pos || !block_table || !kv_strides)
     return fail(fn, "null pointer argument");
+  if (segment_ends) {
+    if (num_donors > kMaxDonors) return fail(fn, "a grouped launch takes at most 16 donors");
+    int64_t prev = 0;
+    for (int64_t k = 0; k < num_donors; ++k) {
+      const int64_t e = segment_ends[k];
+      const bool last = k + 1 == num_donors;
+      if (e < prev || (last ? e != num_pairs : e % kGroupedPairAlign != 0))
+        return fail(fn, "segment ends must rise, sit on multiples of 256 and end at num_pairs");
+      prev = e;
+    }
+  }
   const bool rope = inv_freq != nullptr;
   if (rope && (head_dim % 2) != 0) return fail(fn, "head_dim must be even for RoPE");
   if (block_size <= 0) return fail(fn, "block_size must be positive");
@@ -976,6 +1005,9 @@ extern "C" int sb_composite_scatter_paged_layers(
   a.dst = side_paged(nullptr, kv_layer_ptrs, kv_strides, es);
   a.donors.layers = donor_layer_ptrs;
   a.donors.index = donor_index;
+  a.donors.grouped = segment_ends ? 1 : 0;
+  if (segment_ends)
+    for (int64_t k = 0; k < num_donors; ++k) a.donors.seg_end[k] = segment_ends[k];
   a.src_pos = donor_pos;
   a.dst_pos = target_pos;
   a.block_table = block_table;
@@ -1009,6 +1041,44 @@ extern "C" int sb_composite_scatter_paged_layers(
     if (rc) return rc;
   }
   return SB_OK;
+}
+
+extern "C" int sb_composite_scatter_paged_layers(
+    const uint64_t* kv_layer_ptrs, int64_t num_layers, const uint64_t* donor_layer_ptrs,
+    int64_t num_donors, const int64_t* donor_strides, const int32_t* donor_index,
+    const int32_t* donor_pos, const int32_t* target_pos, const float* inv_freq,
+    int64_t num_pairs, int64_t num_heads, int64_t block_size, int64_t head_dim,
+    const int32_t* block_table, int64_t num_blocks_total, int64_t num_blocks_per_seq,
+    const int64_t* kv_strides, int32_t dtype, int32_t flags, void* stream) {
+  if (!donor_index && num_pairs != 0) {
+    clear_error();
+    return fail("sb_composite_scatter_paged_layers", "null pointer argument");
+  }
+  return composite_impl("sb_composite_scatter_paged_layers", kv_layer_ptrs, num_layers,
+                        donor_layer_ptrs, num_donors, donor_strides, donor_index, nullptr,
+                        donor_pos, target_pos, inv_freq, num_pairs, num_heads, block_size,
+                        head_dim, block_table, num_blocks_total, num_blocks_per_seq, kv_strides,
+                        dtype, flags, stream);
+}
+
+// The composite scatter with its pairs grouped by donor (host segment ends): each workgroup's
+// pairs share one donor, whose strides and layer table the workgroup reads once.
+extern "C" int sb_composite_scatter_paged_layers_grouped(
+    const uint64_t* kv_layer_ptrs, int64_t num_layers, const uint64_t* donor_layer_ptrs,
+    int64_t num_donors, const int64_t* donor_strides, const int64_t* segment_ends,
+    const int32_t* donor_pos, const int32_t* target_pos, const float* inv_freq,
+    int64_t num_pairs, int64_t num_heads, int64_t block_size, int64_t head_dim,
+    const int32_t* block_table, int64_t num_blocks_total, int64_t num_blocks_per_seq,
+    const int64_t* kv_strides, int32_t dtype, int32_t flags, void* stream) {
+  if (!segment_ends && num_pairs != 0) {
+    clear_error();
+    return fail("sb_composite_scatter_paged_layers_grouped", "null segment ends");
+  }
+  return composite_impl("sb_composite_scatter_paged_layers_grouped", kv_layer_ptrs,
+                        num_layers, donor_layer_ptrs, num_donors, donor_strides, nullptr,
+                        segment_ends, donor_pos, target_pos, inv_freq, num_pairs, num_heads,
+                        block_size, head_dim, block_table, num_blocks_total,
+                        num_blocks_per_seq, kv_strides, dtype, flags, stream);
 }
 
 namespace sb {

@@ -21,7 +21,7 @@ import torch
 
 from . import _lib
 from .partial_attention import PartialAttentionPlan, compute_donor_kv_indices
-from .rope_correction import inv_freq_table
+from .rope_correction import PreparedLaunch, inv_freq_table
 
 __all__ = [
     "MultiDonorPositionMapping",
@@ -29,6 +29,8 @@ __all__ = [
     "composite_pairs_from_plan",
     "composite_scatter_paged",
     "composite_scatter_paged_layers",
+    "group_pairs_by_donor",
+    "prepare_composite_scatter_paged_layers",
 ]
 
 
@@ -137,24 +139,7 @@ def composite_scatter_paged_layers(
     nb_total, _, num_heads, block_size, head_dim = ref.shape
     dev = _lib.require_device(*kv_caches, *(t for per in donor_kvs for t in per))
     _check_same(kv_caches, "kv_caches")
-    if donor_first_positions is None:
-        donor_first_positions = [0] * len(donor_kvs)
-    if len(donor_first_positions) != len(donor_kvs):
-        raise ValueError("one first position per donor")
-    strides = []
-    for k, per_layer in enumerate(donor_kvs):
-        if len(per_layer) != num_layers:
-            raise ValueError(f"donor {k} has {len(per_layer)} layers, the cache {num_layers}")
-        _check_same(per_layer, f"donor {k} layers")
-        d0 = per_layer[0]
-        if d0.dim() != 4 or d0.shape[0] != 2 or d0.shape[1] != num_heads or d0.shape[3] != head_dim:
-            raise ValueError(f"donor {k} must be [2, {num_heads}, S, {head_dim}]")
-        if d0.dtype != ref.dtype:
-            raise TypeError("donors and caches must share a dtype")
-        if d0.stride(3) != 1:
-            raise ValueError("donor head_dim must be contiguous (stride 1)")
-        strides += [d0.stride(0), d0.stride(1), d0.stride(2), d0.shape[2],
-                    int(donor_first_positions[k])]
+    strides = _donor_strides(donor_kvs, ref, num_layers, donor_first_positions)
     if rope and head_dim % 2:
         raise ValueError("head_dim must be even for RoPE")
     kv_tab = _lib.address_table(kv_caches, dev)
@@ -207,6 +192,128 @@ def composite_scatter_paged(
     composite_scatter_paged_layers([kv_cache], [[t] for t in tensors], block_table, didx, dpos,
                                    tpos, rope=rope, rope_base=rope_base)
     return kv_cache
+
+
+def _donor_strides(donor_kvs, ref: torch.Tensor, num_layers: int,
+                   donor_first_positions) -> list[int]:
+    """Per donor: kv, head and sequence strides (elements), rows held and first position, after
+    checking every donor's layers against the caches (``num_layers`` layers like ``ref``)."""
+    _, _, num_heads, _, head_dim = ref.shape
+    if donor_first_positions is None:
+        donor_first_positions = [0] * len(donor_kvs)
+    if len(donor_first_positions) != len(donor_kvs):
+        raise ValueError("one first position per donor")
+    strides = []
+    for k, per_layer in enumerate(donor_kvs):
+        if len(per_layer) != num_layers:
+            raise ValueError(f"donor {k} has {len(per_layer)} layers, the cache {num_layers}")
+        _check_same(per_layer, f"donor {k} layers")
+        d0 = per_layer[0]
+        if d0.dim() != 4 or d0.shape[0] != 2 or d0.shape[1] != num_heads or d0.shape[3] != head_dim:
+            raise ValueError(f"donor {k} must be [2, {num_heads}, S, {head_dim}]")
+        if d0.dtype != ref.dtype:
+            raise TypeError("donors and caches must share a dtype")
+        if d0.stride(3) != 1:
+            raise ValueError("donor head_dim must be contiguous (stride 1)")
+        strides += [d0.stride(0), d0.stride(1), d0.stride(2), d0.shape[2],
+                    int(donor_first_positions[k])]
+    return strides
+
+
+def group_pairs_by_donor(donor_index, donor_positions, target_positions, num_donors: int,
+                         align: int = _lib.SB_GROUPED_PAIR_ALIGN, donors_per_launch: int = 16):
+    """Host grouping of composite pairs for the grouped launch: pairs of an unknown donor
+    are dropped (the indexed launch skips them), the rest are ordered by donor (stable), and
+    every donor's run is padded with (-1, -1) pairs to a multiple of ``align``, except the last
+    of each launch. Donors go in launches of ``donors_per_launch``.
+
+    Returns one (first donor, donor count, int32 donor positions, int32 target positions,
+    int64 segment ends) per launch that has pairs."""
+    didx = np.asarray(donor_index, dtype=np.int64).reshape(-1)
+    dpos = np.asarray(donor_positions, dtype=np.int64).reshape(-1)
+    tpos = np.asarray(target_positions, dtype=np.int64).reshape(-1)
+    if not (didx.size == dpos.size == tpos.size):
+        raise ValueError("donor_index, donor_positions and target_positions differ in length")
+    keep = (didx >= 0) & (didx < num_donors)
+    didx, dpos, tpos = didx[keep], dpos[keep], tpos[keep]
+    order = np.argsort(didx, kind="stable")
+    didx, dpos, tpos = didx[order], dpos[order], tpos[order]
+    bounds = np.searchsorted(didx, np.arange(num_donors + 1))
+    launches = []
+    for first in range(0, num_donors, donors_per_launch):
+        count = min(donors_per_launch, num_donors - first)
+        parts_d, parts_t, ends, n = [], [], [], 0
+        for k in range(first, first + count):
+            seg_d = dpos[bounds[k]:bounds[k + 1]]
+            seg_t = tpos[bounds[k]:bounds[k + 1]]
+            last = k == first + count - 1
+            pad = 0 if last else (-len(seg_d)) % align
+            parts_d += [seg_d, np.full(pad, -1)]
+            parts_t += [seg_t, np.full(pad, -1)]
+            n += len(seg_d) + pad
+            ends.append(n)
+        if bounds[first + count] > bounds[first]:
+            launches.append((first, count, np.concatenate(parts_d).astype(np.int32),
+                             np.concatenate(parts_t).astype(np.int32),
+                             np.asarray(ends, dtype=np.int64)))
+    return launches
+
+
+def prepare_composite_scatter_paged_layers(
+    kv_caches: list[torch.Tensor],
+    donor_kvs: Sequence[Sequence[torch.Tensor]],
+    block_table: torch.Tensor,
+    donor_index,
+    donor_positions,
+    target_positions,
+    rope: bool = True,
+    rope_base: float = 10000.0,
+    donor_first_positions: Sequence[int] | None = None,
+    repeated_donor_rows: bool | None = None,
+) -> PreparedLaunch | None:
+    """Bind :func:`composite_scatter_paged_layers` once, with the pairs grouped by donor on the
+    host (device tensors are read back once), so that each workgroup's pairs share one donor
+    (``sb_composite_scatter_paged_layers_grouped``: the donor's strides and layer table are
+    read once per workgroup, not per pair). Calling the returned object enqueues the launches
+    (one per 16 donors) on the current stream; it holds the uploaded pairs and tables, so the
+    tensors must keep their storage. Same results as the per-call form. Returns None when no
+    pair names a known donor."""
+    if not kv_caches or not donor_kvs:
+        return None
+    num_layers = len(kv_caches)
+    ref = kv_caches[0]
+    nb_total, _, num_heads, block_size, head_dim = ref.shape
+    dev = _lib.require_device(*kv_caches, *(t for per in donor_kvs for t in per))
+    _check_same(kv_caches, "kv_caches")
+    strides = _donor_strides(donor_kvs, ref, num_layers, donor_first_positions)
+    if rope and head_dim % 2:
+        raise ValueError("head_dim must be even for RoPE")
+    host = [x.cpu() if isinstance(x, torch.Tensor) else x
+            for x in (donor_index, donor_positions, target_positions)]
+    if repeated_donor_rows is None:
+        repeated_donor_rows = _lib.rows_repeat(_as_tensor(host[1]), _as_tensor(host[0]))
+    launches = group_pairs_by_donor(*host, num_donors=len(donor_kvs))
+    if not launches:
+        return None
+    kv_tab = _lib.address_table(kv_caches, dev)
+    bt = _lib.as_index(block_table, dev)
+    inv_freq = inv_freq_table(rope_base, head_dim, dev) if rope else None
+    keep = [kv_tab, bt, inv_freq]
+    calls = []
+    for first, count, dp, tp, ends in launches:
+        d_tab = _lib.address_table([t for per in donor_kvs[first:first + count] for t in per],
+                                   dev)
+        both = _lib.upload_index(torch.from_numpy(np.concatenate([dp, tp])), dev)
+        n = int(dp.size)
+        st = _lib.i64_array(strides[5 * first:5 * (first + count)])
+        en = _lib.i64_array(ends.tolist())
+        keep += [d_tab, both, st, en]
+        calls.append(("sb_composite_scatter_paged_layers_grouped", (
+            kv_tab.data_ptr(), num_layers, d_tab.data_ptr(), count, st, en, both.data_ptr(),
+            both.data_ptr() + 4 * n, inv_freq.data_ptr() if inv_freq is not None else None, n,
+            num_heads, block_size, head_dim, bt.data_ptr(), nb_total, bt.shape[0],
+            _lib.strides(ref), _lib.dtype_code(ref), _lib.scatter_flags(repeated_donor_rows))))
+    return PreparedLaunch(calls[0][0], calls[0][1], tuple(keep), dev, more=tuple(calls[1:]))
 
 
 def _as_tensor(x) -> torch.Tensor:

@@ -106,6 +106,22 @@ def test_invalid_arguments_are_rejected_without_launch():
         assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"2^31" in lib.sb_last_error_string()
 
 
+def test_grouped_composite_rejects_bad_segments():
+    lib = _lib.lib()
+    fake = 4096
+    st = _i64(1, 1, 1, 4, 0, 1, 1, 1, 4, 0)
+    kvs = _i64(1, 1, 1, 1, 1)
+    for ends, n in (((100, 300), 300), ((256, 300), 299), ((512, 256), 256)):
+        rc = lib.sb_composite_scatter_paged_layers_grouped(
+            fake, 2, fake, 2, st, _i64(*ends), fake, fake, None, n, 1, 16, 8, fake, 4, 1, kvs,
+            2, 0, None)
+        assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"segment" in lib.sb_last_error_string()
+    rc = lib.sb_composite_scatter_paged_layers_grouped(
+        fake, 2, fake, 17, _i64(*([1] * 85)), _i64(*([0] * 17)), fake, fake, None, 10, 1, 16,
+        8, fake, 4, 1, kvs, 2, 0, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"16 donors" in lib.sb_last_error_string()
+
+
 def test_rope_delta_range_checked_before_dispatch():
     """The Python entry rejects |delta| >= 2^31 before touching any tensor (so a CPU tensor
     gets the range error, not the device error)."""

@@ -18,6 +18,7 @@ from semblend_amd.multi_donor import (
     MultiDonorPositionMapping,
     composite_scatter_paged,
     composite_scatter_paged_layers,
+    prepare_composite_scatter_paged_layers,
 )
 from tests.helpers import assert_rope_close, gen, randn
 
@@ -254,3 +255,37 @@ def test_composite_empty_inputs(dev):
     composite_scatter_paged(caches[0], [donors[0][0]], bt, MultiDonorPositionMapping())
     for a, b in zip(caches, base):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("rope", [True, False], ids=["rope", "copy"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n_donors", [3, 19])
+def test_grouped_composite_matches_indexed(dev, dtype, rope, n_donors):
+    """The donor-grouped launch (pairs grouped and padded by donor on the host, one launch per
+    16 donors) lands the indexed launch's bits, skipped pairs included; 19 donors take two
+    launches. Donors of different lengths, one a strided view, one a staged window whose row 0
+    is a later sequence position."""
+    layers, h, bs = 3, 4, 16
+    d = 64 if dtype == torch.float32 else 128
+    lens = [300 + 37 * k for k in range(n_donors)]
+    firsts = [0] * n_donors
+    firsts[-1] = 64
+    donors = [[_donor(n, h, d, dtype, 100 * k + l, pad=40 if k == 1 else 0)
+               for l in range(layers)] for k, n in enumerate(lens)]
+    nb, nb_seq = 160, 128
+    bt = torch.randperm(nb, generator=gen(15))[:nb_seq].to(torch.int32)
+    didx, dpos, tpos = _plan(lens, nb_seq, bs, 64, 16 + n_donors, skip_frac=0.1)
+    dpos = torch.where(didx == n_donors - 1, dpos + 64, dpos)  # the window's true positions
+    base = _caches(layers, nb, h, bs, d, dtype, 17)
+    dd = [[t.to(dev) for t in per] for per in donors]
+    want = [c.to(dev) for c in base]
+    composite_scatter_paged_layers(want, dd, bt.to(dev), didx, dpos, tpos, rope=rope,
+                                   rope_base=5e5, donor_first_positions=firsts)
+    got = [c.to(dev) for c in base]
+    call = prepare_composite_scatter_paged_layers(got, dd, bt.to(dev), didx.to(dev), dpos, tpos,
+                                                  rope=rope, rope_base=5e5,
+                                                  donor_first_positions=firsts)
+    assert len(call.launches) == (2 if n_donors > 16 else 1)
+    call()
+    for g_, w in zip(got, want):
+        assert torch.equal(g_.view(torch.uint8), w.view(torch.uint8))

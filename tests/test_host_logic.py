@@ -383,3 +383,34 @@ def test_layout_detection_and_empty():
     with pytest.raises(ValueError):
         rc.paged_layout(std, "nhd")
     assert rc.prepare_permute_paged_kv_layers([std], torch.zeros(2), []) is None
+
+
+def test_group_pairs_by_donor():
+    """Grouping for the donor-grouped composite launch: unknown donors dropped, pairs in donor
+    order (stable within a donor), each donor's run padded with (-1, -1) to a multiple of the
+    alignment except the last of its launch, launches of at most 16 donors."""
+    from semblend_amd.multi_donor import group_pairs_by_donor
+
+    rng = np.random.default_rng(3)
+    n, nd = 900, 20
+    didx = rng.integers(-2, nd + 2, n)
+    dpos = rng.integers(0, 5000, n)
+    tpos = rng.permutation(20000)[:n]
+    launches = group_pairs_by_donor(didx, dpos, tpos, nd, align=256)
+    assert [(f, c) for f, c, *_ in launches] == [(0, 16), (16, 4)]
+    seen = []
+    for first, count, dp, tp, ends in launches:
+        assert dp.dtype == np.int32 and tp.dtype == np.int32 and ends.dtype == np.int64
+        assert ends[-1] == dp.size == tp.size
+        assert all(e % 256 == 0 for e in ends[:-1]) and all(np.diff(ends) >= 0)
+        start = 0
+        for k, e in zip(range(first, first + count), ends):
+            seg_d, seg_t = dp[start:e], tp[start:e]
+            real = seg_t >= 0
+            want = [(int(a), int(b)) for a, b, c in zip(dpos, tpos, didx) if c == k]
+            assert list(zip(seg_d[real].tolist(), seg_t[real].tolist())) == want
+            assert np.all(seg_d[~real] == -1) and not np.any(real[real.argmin():]) or real.all()
+            seen += want
+            start = e
+    assert len(seen) == int(((didx >= 0) & (didx < nd)).sum())
+    assert group_pairs_by_donor([5], [1], [2], 3) == []
