@@ -89,6 +89,29 @@ static_assert(kRing > kFragAhead && (kRing & (kRing - 1)) == 0, "fragment ring")
 #ifndef SB_ATTN_ROW_GROUPS
 #define SB_ATTN_ROW_GROUPS 1
 #endif
+// Instruction trims of the two-tile loop, together 1.4% on the 7B workload (272.1 -> 268.1 us,
+// alternating runs on one box; each alone within the run-to-run spread), results unchanged:
+//  * FILL_ONE_WAVE: the key offsets of tile it + 3 are written by one wave per tile (wave
+//    it mod kWaves, one entry per lane) instead of a share of them by every wave;
+//  * M0_AHEAD: M0 (the direct-to-LDS destination) is written one MFMA step before its load,
+//    not right before it with a wait state;
+//  * SADDR: paged loads with every key row of the cache within 4 GiB of the K / V base take
+//    the base in scalar registers and a 32-bit per-lane offset (no 64-bit address arithmetic);
+//    needs M0_AHEAD;
+//  * DOT2_ZERO: the first v_dot2 of each 8-element P pack takes an inline zero accumulator
+//    (VOP3) instead of a zeroed register.
+#ifndef SB_ATTN_FILL_ONE_WAVE
+#define SB_ATTN_FILL_ONE_WAVE 1
+#endif
+#ifndef SB_ATTN_M0_AHEAD
+#define SB_ATTN_M0_AHEAD 1
+#endif
+#ifndef SB_ATTN_SADDR
+#define SB_ATTN_SADDR 1
+#endif
+#ifndef SB_ATTN_DOT2_ZERO
+#define SB_ATTN_DOT2_ZERO 1
+#endif
 // Row groups per wave: each K/V fragment read from LDS feeds this many MFMAs.
 constexpr int kRowGroups = SB_ATTN_ROW_GROUPS;
 #ifndef SB_ATTN_TILE_KEYS
@@ -97,8 +120,13 @@ constexpr int kRowGroups = SB_ATTN_ROW_GROUPS;
 #ifndef SB_ATTN_OCCUPANCY
 #define SB_ATTN_OCCUPANCY 2
 #endif
+// Waves per workgroup (32 flattened rows each); one 8-wave workgroup per CU shares each K/V
+// tile load among 256 rows, half the direct-to-LDS traffic of two 4-wave workgroups: 7B
+// workload 268.1 -> 265.3 us with the trims above (273.0 with neither; alternating runs on
+// one box). Register-staged V tiles (global load, ds_write_b128) instead of direct-to-LDS
+// loads were slower (270.7 us).
 #ifndef SB_ATTN_WAVES
-#define SB_ATTN_WAVES 4
+#define SB_ATTN_WAVES 8
 #endif
 constexpr int kTileKeys = SB_ATTN_TILE_KEYS;  // keys per LDS tile (32 or 64)
 constexpr int kWaves = SB_ATTN_WAVES;         // waves per workgroup (each owns 32 rows)
@@ -289,6 +317,13 @@ template <> struct Mma<SB_DTYPE_BF16> {
     const x2 one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
     return __builtin_amdgcn_fdot2_f32_bf16(v, one, acc, false);
   }
+  // 0 + the sum of v, the zero as an inline constant of the VOP3 form (no zeroed register).
+  __device__ __forceinline__ static float sum2z(x2 v, uint32_t one) {
+    float r;
+    asm volatile("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(v), "v"(one));
+    return r;
+  }
+  static constexpr uint32_t kOnePair = 0x3f803f80u;
   // acc + sum of the 8 (rounded) elements of v, two per v_dot2.
   __device__ __forceinline__ static float sum8(vec8 v, float acc) {
     typedef __bf16 x2 __attribute__((ext_vector_type(2)));
@@ -326,6 +361,12 @@ template <> struct Mma<SB_DTYPE_F16> {
     const x2 one = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
     return __builtin_amdgcn_fdot2(v, one, acc, false);
   }
+  __device__ __forceinline__ static float sum2z(x2 v, uint32_t one) {
+    float r;
+    asm volatile("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(v), "v"(one));
+    return r;
+  }
+  static constexpr uint32_t kOnePair = 0x3c003c00u;
   __device__ __forceinline__ static float sum8(vec8 v, float acc) {
     typedef _Float16 x2 __attribute__((ext_vector_type(2)));
     const x2 one = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
@@ -381,6 +422,19 @@ __device__ __forceinline__ void dma_row_chunk(const char* src, uint32_t lds_wave
       :
       : "s"(lds_wave), "v"(src)
       : "memory", "m0");
+}
+// The same load in two parts, for callers that keep the M0 write and the load apart: the LDS
+// destination goes to M0 first, and the load (which reads M0) must follow at least one other
+// instruction later (the M0 write-to-use wait state). Nothing between them may write M0.
+__device__ __forceinline__ void dma_set_m0(uint32_t lds_wave) {
+  asm volatile("s_mov_b32 m0, %0" : : "s"(lds_wave) : "m0");
+}
+__device__ __forceinline__ void dma_at_m0(const char* src) {
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src) : "memory");
+}
+// The same with the wave's base address in scalar registers and a 32-bit byte offset per lane.
+__device__ __forceinline__ void dma_at_m0_s(const char* base, uint32_t voff) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base) : "memory");
 }
 // LDS byte address of a pointer into a __shared__ array (wave-uniform arithmetic on it stays
 // in scalar registers).
@@ -620,6 +674,10 @@ attn_mfma_kernel(const AttnBatch batch) {
   const int pmin_w = __builtin_amdgcn_readfirstlane(wave_min_i(pmin_l));
   const int pmax_c = min(pmax_w, k1 - 1);
   const float c_log2 = a.scale_log2;  // scale * log2(e): score units -> log2 domain
+#if SB_ATTN_DOT2_ZERO
+  uint32_t one_pair = M::kOnePair;  // (1, 1) in the input type, for the P pack sums
+  asm volatile("" : "+v"(one_pair));  // one register for the whole loop
+#endif
 
   // Softmax state per row: O and l are relative to a reference max m_ref (log2 domain,
   // of scale * log2(e) * s); negm = -m_ref enters every exp2 through one fma. A row is
@@ -665,8 +723,19 @@ attn_mfma_kernel(const AttnBatch batch) {
 #pragma unroll
     for (int q = 0; q < NLD; ++q) ro[q] = ofs[q * (kThreads / CH) + tid / CH];
   };
+  constexpr bool kSaddr = SB_ATTN_SADDR && SB_ATTN_M0_AHEAD && AM == kAddrPagedNarrow;
+  const uint32_t k_lane = 16 * kswz<CH>(tid / CH, tid % CH);  // chunk part of the offsets
+  const uint32_t v_lane = 16 * vswz<CH>(tid / CH, tid % CH);
+  auto read_ofs32 = [&](const uint64_t* ofs, uint32_t lanep, uint32_t* ro) {
+#pragma unroll
+    for (int q = 0; q < NLD; ++q)
+      ro[q] = static_cast<uint32_t>(ofs[q * (kThreads / CH) + tid / CH]) + lanep;
+  };
   auto dma_one = [&](const char* src, uint64_t ro, uint16_t* dst, int q) {
     dma_row_chunk(src + ro, lds_addr(dst) + (q * kThreads + wave * 64) * 16);
+  };
+  auto dma_dst = [&](uint16_t* dst, int q) -> uint32_t {
+    return lds_addr(dst) + (q * kThreads + wave * 64) * 16;
   };
   auto load_k = [&](int slot, int stage) { load_rows(ksrc, kofs[slot], Ks[stage]); };
   auto load_v = [&](int slot, int stage) {
@@ -814,7 +883,11 @@ attn_mfma_kernel(const AttnBatch batch) {
     const int slot1 = slot == 2 ? 0 : slot + 1;  // (it + 1) mod 3
     const int slot2 = slot == 0 ? 2 : slot - 1;  // (it + 2) mod 3
     uint64_t ro_k[NLD], ro_v[NLD];
-    if (ILV) {
+    uint32_t ro_k32[NLD], ro_v32[NLD];
+    if (ILV && kSaddr) {
+      read_ofs32(kofs[slot2], k_lane, ro_k32);
+      read_ofs32(kofs[slot1], v_lane, ro_v32);
+    } else if (ILV) {
       read_ofs(kofs[slot2], ro_k);
       read_ofs(kPaged ? kofs[slot1] : vofs[slot1], ro_v);
     } else {
@@ -822,8 +895,13 @@ attn_mfma_kernel(const AttnBatch batch) {
       if (it + 1 < ntiles) load_v(slot1, par ^ 1);
     }
     // Offsets of tile it+3: kTileKeys / kWaves entries from each wave.
+#if SB_ATTN_FILL_ONE_WAVE
+    static_assert(kTileKeys == 64, "one entry per lane");
+    if (it + 3 < ntiles && wave == (it & (kWaves - 1))) fill_offsets(slot, t0 + 3 * kTileKeys, lane);
+#else
     if (it + 3 < ntiles && lane < kTileKeys / kWaves)
       fill_offsets(slot, t0 + 3 * kTileKeys, wave * (kTileKeys / kWaves) + lane);
+#endif
     const bool live = t0 <= pmax_c;
     // ---- S(it+1) on the matrix cores while P(it) is formed on the vector ALUs ----
     // The block is laid out by hand: step n reads the K fragment of step n + kFragAhead,
@@ -854,7 +932,11 @@ attn_mfma_kernel(const AttnBatch batch) {
         const int hj = r / 8, h = (r / 4) % 2, w = r % 4;
         const auto pr = M::cvt2(e0, e1);
         pw[g][hj][h][w] = __builtin_bit_cast(uint32_t, pr);
+#if SB_ATTN_DOT2_ZERO
+        acc[g][hj][h] = w == 0 ? M::sum2z(pr, one_pair) : M::sum2(pr, acc[g][hj][h]);
+#else
         acc[g][hj][h] = M::sum2(pr, w == 0 ? 0.f : acc[g][hj][h]);
+#endif
       };
       float fa0[NPAIR], fa1[NPAIR], ea0[NPAIR], ea1[NPAIR];
 #pragma unroll
@@ -862,6 +944,13 @@ attn_mfma_kernel(const AttnBatch batch) {
         fa0[q] = __builtin_fmaf(c_log2, s_at(q, 0), negm[q / (kHalves * 8)]);
         fa1[q] = __builtin_fmaf(c_log2, s_at(q, 1), negm[q / (kHalves * 8)]);
       }
+#endif
+#if SB_ATTN_M0_AHEAD
+      // load n of the step loop: K(it+2) part n, then V(it+1) part n - NLD
+      auto load_dst = [&](int n) -> uint32_t {
+        return n < NLD ? dma_dst(Ks[par], n) : dma_dst(Vs[par ^ 1], n - NLD);
+      };
+      if (ILV) dma_set_m0(load_dst(0));
 #endif
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -874,8 +963,20 @@ attn_mfma_kernel(const AttnBatch batch) {
               M::mma(ring[n % kRing], qf[g][n / kHalves], n < kHalves ? f32x16_t{} : s_nxt[g][j]);
         if (ILV) {
           static_assert(2 * NLD <= NQ, "one load per MFMA step");
+#if SB_ATTN_M0_AHEAD
+          // M0 was written in the previous step (or before the loop), an MFMA ago.
+          if (kSaddr) {
+            if (n < NLD) dma_at_m0_s(kbase, ro_k32[n]);
+            else if (n < 2 * NLD) dma_at_m0_s(vbase, ro_v32[n - NLD]);
+          } else {
+            if (n < NLD) dma_at_m0(ksrc + ro_k[n]);
+            else if (n < 2 * NLD) dma_at_m0(vsrc + ro_v[n - NLD]);
+          }
+          if (n + 1 < 2 * NLD) dma_set_m0(load_dst(n + 1));
+#else
           if (n < NLD) dma_one(ksrc, ro_k[n], Ks[par], n);
           else if (n < 2 * NLD) dma_one(vsrc, ro_v[n - NLD], Vs[par ^ 1], n - NLD);
+#endif
         }
 #if SB_ATTN_VALU_SKEW
         // Three-stage VALU pipeline over the pairs: the fmas of pair n + 1, the exp2 of pair
@@ -1866,8 +1967,13 @@ int paged_args(const char* fn, AttnArgs* pa, bool* aligned16, void* out, const v
   a.nb_total = num_blocks_total;
   a.s_block = kvs[0] * es;
   a.s_pos = kvs[3] * es;
+  // Narrow addressing: 32-bit block strides and in-block offsets, and (for 32-bit load
+  // offsets) every row of the cache within 4 GiB of the K and V bases.
+  const int64_t extent = (num_blocks_total - 1) * a.s_block + (block_size - 1) * a.s_pos +
+                         (num_kv_heads - 1) * std::max(a.k_s_head, a.v_s_head) + head_dim * es;
   a.narrow_ofs = a.bs_log2 >= 0 && a.s_block >= 0 && a.s_block <= 0xFFFFFFFFll &&
-                 a.s_pos >= 0 && a.s_pos < (1ll << 24) && block_size < (1ll << 24);
+                 a.s_pos >= 0 && a.s_pos < (1ll << 24) && block_size < (1ll << 24) &&
+                 extent < (1ll << 32);
   a.num_kv_heads = static_cast<int>(num_kv_heads);
   a.group = static_cast<int>(num_q_heads / num_kv_heads);
   a.head_dim = static_cast<int>(head_dim);

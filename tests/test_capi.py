@@ -247,7 +247,13 @@ def test_attention_plan_orders_every_item_longest_first(seed, rows, sort):
     assert ks1 > 0 and ks2 > 0 and ks1 % 64 == 0 and ks2 % 64 == 0 and ks1 <= 1024 * 16
     chunks = 1 if 16384 <= ks1 else 1 + -(-(16384 - ks1) // ks2)
     assert mc == chunks
-    tr, group, hkv = 128, 7, 4
+    group, hkv = 7, 4
+    # flattened query rows per workgroup tile, from the workspace the library reports for a
+    # one-row call (hkv x 1 tile x mc chunks x tr rows x (head_dim + 2) fp32 values)
+    ws1 = _lib.size_query("sb_partial_attention_paged_planned_workspace_size", 1, 28, hkv, 128,
+                          max(mc, 2), 2)
+    tr = ws1 // (hkv * max(mc, 2) * 130 * 4)
+    assert tr in (128, 256) and ws1 == hkv * max(mc, 2) * tr * 130 * 4
     n_tiles = -(-rows * group // tr)
     assert sorted(order) == list(range(mc * n_tiles * hkv))
     kend = [max(int(pos[r // group]) for r in range(t * tr, min((t + 1) * tr, rows * group)))
