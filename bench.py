@@ -26,7 +26,8 @@ events around every replay, which adds one graph launch (about 8 us on this GPU)
 The RoPE and scatter phases stream 2 GB through the 256 MB Infinity Cache before every
 attention launch, so no timed kernel finds its inputs cached from the previous step.
 ``roofline`` prices the MFMA attention kernel's average launch against the bf16 peak.
-``phases.copy_ceiling`` is a plain 1 GiB device copy, the achievable HBM rate.
+``phases.copy_ceiling`` is a plain 1 GiB device copy through the library's flat copy kernel,
+the achievable HBM rate; every HBM phase also reports ``frac_of_copy`` against it.
 ``rope_scatter`` times the scatter workload again with K rotated on the way (one donor, and
 a composite from four donors); ``chunk_load`` streams the same donor from pinned host memory
 in 256-token chunks with the RoPE scatter overlapped. The CPU
@@ -238,21 +239,27 @@ def build_inputs(dev: torch.device):
     return inp
 
 
-def copy_ceiling(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> float:
-    """Achievable HBM bandwidth of a plain device copy (read + write), GB/s."""
+def copy_ceiling(dev: torch.device, nbytes: int = 1 << 30, reps: int = 10) -> dict:
+    """Achievable HBM bandwidth of a plain 1 GiB device copy (read + write), GB/s: the
+    library's flat copy (one 16-byte vector per thread, nontemporal; the ceiling the movers'
+    ``frac_of_copy`` refers to) and torch's ``copy_`` beside it."""
+    from semblend_amd import _lib
+
     a = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     b = torch.empty_like(a)
-    b.copy_(a)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        b.copy_(a)
-    e1.record()
-    torch.cuda.synchronize()
-    gbps = 2.0 * nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    out = {}
+    for name, fn in (("library", lambda: _lib.device_copy(b, a)), ("torch", lambda: b.copy_(a))):
+        fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = 2.0 * nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
     del a, b
-    return gbps
+    return out
 
 
 def gemm_ceiling(dev: torch.device, n: int = 8192, reps: int = 10) -> float:
@@ -526,7 +533,8 @@ def rope_scatter_section(dev: torch.device, inp, steps: int) -> dict:
     (each 256-token target chunk owned by a random one of four 16384-token donors,
     ``prepare_composite_scatter_paged_layers``, pairs grouped by donor; and, as
     ``four_donors_indexed``, the per-call form with a per-pair donor index), K rotated by a
-    per-chunk delta. Graph replays timed with HIP events."""
+    per-chunk delta. Graph replays timed with HIP events, each after a RoPE pass (as in a step)
+    and back to back."""
     from semblend_amd import rope_correction as rc
     from semblend_amd.multi_donor import (composite_scatter_paged_layers,
                                           prepare_composite_scatter_paged_layers)
@@ -555,27 +563,46 @@ def rope_scatter_section(dev: torch.device, inp, steps: int) -> dict:
         inp["caches"], donors, inp["block_table"], didx.cpu(), inp["sc_d"].cpu(),
         inp["sc_t"].cpu(), rope=True, rope_base=ROPE_BASE)
 
+    # Each replay is timed after a RoPE pass over K[28,4,8192,128] (470 MB through the
+    # Infinity Cache, as in a step: the donor rows come from HBM) and, as ``back_to_back``,
+    # right after the previous replay (part of the donor rows then still sit in the Infinity
+    # Cache, as when a donor chunk was uploaded or computed just before).
+    rope_gr = capture(lambda: rc.rope_correct_k_inplace(
+        inp["rope_k"][0], inp["rope_d"], inp["rope_t"], head_dim=D, rope_base=ROPE_BASE,
+        distinct_donors=True))
     out = {"pairs": int(n_pairs), "bytes": nbytes}
     for name, fn in (("one_donor", one_donor), ("four_donors", four_donors),
                      ("four_donors_indexed", four_donors_indexed)):
         gr = capture(fn)
         gr.replay()
         torch.cuda.synchronize()
-        evs = []
-        for _ in range(steps):
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record()
-            gr.replay()
-            e1.record()
-            evs.append((e0, e1))
-        torch.cuda.synchronize()
-        t = [a.elapsed_time(b) for a, b in evs]
+        times = {}
+        for ctx in ("after_rope", "back_to_back"):
+            evs = []
+            for _ in range(steps):
+                if ctx == "after_rope":
+                    rope_gr.replay()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                gr.replay()
+                e1.record()
+                evs.append((e0, e1))
+            torch.cuda.synchronize()
+            times[ctx] = [a.elapsed_time(b) for a, b in evs]
+        t = times["after_rope"]
         avg = sum(t) / len(t)
+        t2 = times["back_to_back"]
+        avg2 = sum(t2) / len(t2)
         out[name] = {"ms": round(avg, 4), "ms_median": round(sorted(t)[len(t) // 2], 4),
                      "gbps": round(nbytes / (avg * 1e-3) / 1e9, 1),
-                     "frac_of_peak": round(nbytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                     "frac_of_peak": round(nbytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "back_to_back": {
+                         "ms": round(avg2, 4),
+                         "gbps": round(nbytes / (avg2 * 1e-3) / 1e9, 1),
+                         "frac_of_peak": round(nbytes / (avg2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
         del gr
+    del rope_gr
     return out
 
 
@@ -913,10 +940,11 @@ def main() -> int:
     torch.cuda.synchronize()
     rope_idx_ms = sum(a.elapsed_time(b) for a, b in idx_ev) / len(idx_ev)
     del idx_graphs, step_graphs
-    copy_gbps = copy_ceiling(dev)
+    copy_rates = copy_ceiling(dev)
+    copy_gbps = copy_rates["library"]
     gemm_tflops = gemm_ceiling(dev)
     log("kernels (avg us): " + ", ".join(f"{k} {v['avg_us']}" for k, v in kernels.items())
-        + f"; copy ceiling {copy_gbps:.0f} GB/s")
+        + f"; copy ceiling {copy_gbps:.0f} GB/s (torch copy_ {copy_rates['torch']:.0f})")
     # Phase durations on the GPU: the phase's kernels, each bracketed by HIP events that the
     # runtime stamps with the kernel's start and end, in the interleaved eager pass above.
     avg = {"rope": kernels["rope_rows"]["avg_us"] * 1e-3,
@@ -990,13 +1018,15 @@ def main() -> int:
                         "gbps": round(scatter_gbps, 1),
                         "kernel_gbps": round(scatter_bytes / (kernels["move_rows"]["avg_us"] * 1e-6) / 1e9, 1),
                         "traffic_bytes": MEASURED_TRAFFIC_BYTES["move_rows"],
-                        "frac_of_peak": round(scatter_gbps / HBM_PEAK_GBS, 4)},
+                        "frac_of_peak": round(scatter_gbps / HBM_PEAK_GBS, 4),
+                        "frac_of_copy": round(scatter_gbps / copy_gbps, 4)},
             "rope": {"ms": round(avg["rope"], 4),
                      "launch_inclusive_ms": round(launch_ms["rope"], 4),
                      "gbps": round(rope_gbps, 1),
                      "kernel_gbps": round(rope_bytes / (kernels["rope_rows"]["avg_us"] * 1e-6) / 1e9, 1),
                      "traffic_bytes": MEASURED_TRAFFIC_BYTES["rope_rows"],
                      "frac_of_peak": round(rope_gbps / HBM_PEAK_GBS, 4),
+                     "frac_of_copy": round(rope_gbps / copy_gbps, 4),
                      "what": "one launch per step (donor positions distinct: d = 0..8191)",
                      "indexed": {"ms": round(rope_idx_ms, 4),
                                  "gbps": round(rope_bytes / (rope_idx_ms * 1e-3) / 1e9, 1),
@@ -1007,13 +1037,19 @@ def main() -> int:
                              "what": "8192^3 bf16 torch matmul (hipBLASLt), 10 repeats"},
             "copy_ceiling": {"gbps": round(copy_gbps, 1),
                              "frac_of_peak": round(copy_gbps / HBM_PEAK_GBS, 4),
-                             "what": "1 GiB device-to-device copy (torch copy_), 10 repeats"},
+                             "torch_copy_gbps": round(copy_rates["torch"], 1),
+                             "what": "1 GiB device-to-device copy through the library's flat "
+                                     "copy kernel (one 16-byte vector per thread, "
+                                     "nontemporal), 10 repeats; torch copy_ beside it"},
         },
         "kernels": kernels,
     }
     log("fused RoPE scatter: one donor and four-donor composite")
     result["rope_scatter"] = rope_scatter_section(dev, inp, args.steps)
     rs = result["rope_scatter"]
+    for k in ("one_donor", "four_donors", "four_donors_indexed"):
+        rs[k]["frac_of_copy"] = round(rs[k]["gbps"] / copy_gbps, 4)
+        rs[k]["back_to_back"]["frac_of_copy"] = round(rs[k]["back_to_back"]["gbps"] / copy_gbps, 4)
     log(f"rope scatter: one donor {rs['one_donor']['ms']:.3f} ms ({rs['one_donor']['gbps']:.0f} GB/s), "
         f"four donors {rs['four_donors']['ms']:.3f} ms ({rs['four_donors']['gbps']:.0f} GB/s)")
     log("compacted QKV projection with the K/V write")
@@ -1045,6 +1081,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         result["llama3_8b_batch"] = llama_batch_section(dev, 3, not args.no_cpu_baseline)
         lb = result["llama3_8b_batch"]
+        lb["scatter_rope"]["frac_of_copy"] = round(lb["scatter_rope"]["gbps"] / copy_gbps, 4)
         log(f"llama batch: scatter+rope {lb['scatter_rope']['ms']:.2f} ms "
             f"({lb['scatter_rope']['gbps']:.0f} GB/s), attention {lb['attention']['ms']:.2f} ms "
             f"({lb['attention']['tflops']:.1f} TFLOP/s)")

@@ -515,6 +515,16 @@ int sb_partial_attention_paged_varlen(void* out, const void* q, const void* kv_c
                                       const int64_t* kv_strides, int32_t dtype, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * Flat device copy (measurement reference; no reference counterpart)
+ * ---------------------------------------------------------------------------------------- */
+
+/* dst[0:num_bytes) = src[0:num_bytes): one 16-byte vector per thread with nontemporal loads
+ * and stores, the achievable HBM rate the row movers are compared with. Both buffers must be
+ * 16-byte aligned and num_bytes a multiple of 16; the buffers must not overlap. Logged by the
+ * kernel timing below under "copy". */
+int sb_device_copy(void* dst, const void* src, int64_t num_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * Kernel timing (instrumentation for benchmarks; no reference counterpart)
  * ---------------------------------------------------------------------------------------- */
 
@@ -523,7 +533,7 @@ int sb_partial_attention_paged_varlen(void* out, const void* q, const void* kv_c
  * kernel's own start and end, so no extra work enters the stream); enable == 0 stops logging
  * (the log stays readable). At most 65536 launches are logged. Kernel names:
  * "move_rows", "rope_rows", "rope_index", "fill_i32", "attn_mfma", "attn_valu", "attn_merge",
- * "mask_compact", "zero_rows". */
+ * "mask_compact", "zero_rows", "copy". */
 int sb_kernel_timing_enable(int32_t enable);
 
 /* Sum of the logged durations (ms) and number of logged launches of one kernel. Waits for the

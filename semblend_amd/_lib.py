@@ -99,6 +99,7 @@ SIGNATURES: dict[str, list] = {
     "sb_qkv_gather_rows": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i32, _vp],
     "sb_qkv_epilogue_paged": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp,
                               _vp, _i64, _i64, _i64, _i64, _i64, _i64p, _i32, _vp],
+    "sb_device_copy": [_vp, _vp, _i64, _vp],
     "sb_kernel_timing_enable": [_i32],
     "sb_kernel_timing_read": [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), _i64p],
 }
@@ -384,6 +385,20 @@ def address_table(tensors, device: torch.device) -> torch.Tensor:
     else:
         tab.record_stream(torch.cuda.current_stream(device))
     return tab
+
+
+def device_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """``dst <- src`` (same byte count, contiguous, 16-byte aligned) through the library's
+    flat copy kernel on the current stream: the achievable-bandwidth reference that the row
+    movers are measured against."""
+    if not (dst.is_contiguous() and src.is_contiguous()):
+        raise ValueError("device_copy takes contiguous tensors")
+    nbytes = dst.numel() * dst.element_size()
+    if nbytes != src.numel() * src.element_size():
+        raise ValueError("device_copy: byte counts differ")
+    dev = require_device(dst, src)
+    with on_device(dev):
+        call("sb_device_copy", dst.data_ptr(), src.data_ptr(), nbytes, stream_handle(dev))
 
 
 def kernel_timing(enable: bool) -> None:

@@ -26,7 +26,16 @@
 
 namespace sb {
 
-enum RowMode : int { ROW_FLAT_POS = 0, ROW_PAGED_POS = 1, ROW_INDEX = 2, ROW_DONOR_POS = 3 };
+// ROW_DONOR_GROUPED: ROW_DONOR_POS with the pairs grouped by donor so that every workgroup's
+// pairs share one donor (the donor index is then wave-uniform and its strides and layer table
+// are read by scalar loads).
+enum RowMode : int {
+  ROW_FLAT_POS = 0,
+  ROW_PAGED_POS = 1,
+  ROW_INDEX = 2,
+  ROW_DONOR_POS = 3,
+  ROW_DONOR_GROUPED = 4
+};
 // Rotation of K rows: none; by (destination - source position); NoPE (strip R(source), apply
 // R(destination)); by one delta for every pair; by a per-pair delta (MoveArgs::deltas).
 enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3, ROT_PAIR = 4 };
@@ -34,11 +43,14 @@ enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3, R
 // Launch shape and access hints, tuned on MI355X for the 7B-shape workloads (28 layers x
 // 4 KV heads x 128, bf16). 256-thread blocks (128/512/1024 were slower). The pair movers keep
 // 4 rows in flight per thread and walk 2 layers x all heads of one plane (1.6 GB scatter:
-// 288 us; 4 layers 292, 7 layers 300, 8 rows in flight 298); the row-centric RoPE keeps 8
-// rows in flight (83.1 us for K[28,4,8192,128], 84.6 with 4). Nontemporal loads and stores:
-// the rows are touched once (316 -> 291 us for the scatter). About 4096 RoPE blocks: fewer
-// leave the per-thread set-up exposed, more repeat it (84.6 us at 4096, 86 at 2048, 90 at
-// 6144).
+// 288 us; 4 layers 292, 7 layers 300, 8 rows in flight 298; 1 or 2 rows in flight 302-306).
+// Nontemporal loads and stores: the rows are touched once (316 -> 291 us for the scatter).
+// The row-centric RoPE runs short threads: about 16384 blocks (4 of the 112 rows of
+// K[28,4,8192,128] per thread, cos/sin evaluated once for them) with 2 rows in flight: 76.8 us
+// against 84.3 us for 4096 blocks of 14 rows, 8 in flight; 2 rows per thread 103 us (the
+// cos/sin dominate), 7 rows 79.3 us; 4 rows in flight 79.7 us, 1 row 88.3 us (interleaved
+// runs in one process, one box). A plain 16-byte copy behaves the same way: one vector per
+// thread moves 6.5 TB/s, four 6.2-6.3, eight 4.3.
 #ifndef SB_MOVE_THREADS
 #define SB_MOVE_THREADS 256
 #endif
@@ -46,10 +58,10 @@ enum RotMode : int { ROT_NONE = 0, ROT_DELTA = 1, ROT_NOPE = 2, ROT_CONST = 3, R
 #define SB_MOVE_BATCH 4
 #endif
 #ifndef SB_ROPE_BATCH
-#define SB_ROPE_BATCH 8
+#define SB_ROPE_BATCH 2
 #endif
 #ifndef SB_ROPE_TARGET_BLOCKS
-#define SB_ROPE_TARGET_BLOCKS 4096
+#define SB_ROPE_TARGET_BLOCKS 16384
 #endif
 // (layer, head) rows per thread of the row-centric RoPE; 0 derives it from the block target.
 #ifndef SB_ROPE_ROWS_PER_GROUP
@@ -110,10 +122,9 @@ struct DonorSet {
   int64_t s_seq[kMaxDonors];
   int64_t bound[kMaxDonors];   // rows held by each donor tensor
   int64_t first_pos[kMaxDonors];  // sequence position of each donor tensor's row 0
-  // Grouped launches (grouped != 0): the pairs are grouped by donor, donor k's pairs (padded
-  // with skipped pairs) ending at pair seg_end[k], every boundary a multiple of
+  // Grouped launches (ROW_DONOR_GROUPED sources): the pairs are grouped by donor, donor k's
+  // pairs (padded with skipped pairs) ending at pair seg_end[k], every boundary a multiple of
   // kGroupedPairAlign, so that each workgroup's pairs share one donor; index is unused.
-  int grouped;
   int64_t seg_end[kMaxDonors];
 };
 // Boundary alignment of grouped launches: a multiple of every workgroup's pair count
@@ -178,8 +189,28 @@ __device__ __forceinline__ bool resolve_row(const MoveArgs& a, const RowSide& s,
   }
 }
 
+// Base address of layer l of a row side. SCALAR: the table entry is read through the constant
+// address space with a wave-uniform index, i.e. by a scalar load (the table is written by the
+// host before the launch and only read here). Otherwise it is a vector load from the same
+// address in every lane, which the compiler emits for a table it cannot prove unaliased by the
+// kernel's stores.
+//
+// Measured on the 7B workload (28 layers, 13926 pairs), each launch timed after a RoPE pass as
+// in a KV-reuse step: scalar reads help only the donor-grouped composite source, whose table
+// pointer was per-lane before (four-donor composite 305 -> 299 us); for the plain and the
+// one-donor scatters they cost 1-3% (289 -> 293 us, 285 -> 293 us): with the table load out of
+// each row's dependence chain the waves keep more row loads in flight, which helps when the
+// rows come from the Infinity Cache (back-to-back launches: 274 -> 266 us) and hurts when they
+// come from HBM.
+typedef __attribute__((address_space(4))) const uint64_t sb_const_u64;
+template <bool SCALAR>
 __device__ __forceinline__ char* layer_base(const RowSide& s, int l) {
-  return s.layers ? reinterpret_cast<char*>(s.layers[l]) : s.base + l * s.s_layer;
+  if (!s.layers) return s.base + l * s.s_layer;
+  if (SCALAR) {
+    const sb_const_u64* t = (const sb_const_u64*)(s.layers);
+    return reinterpret_cast<char*>(t[__builtin_amdgcn_readfirstlane(l)]);
+  }
+  return reinterpret_cast<char*>(s.layers[l]);
 }
 
 // Unpacks VB bytes held as W 32-bit words into E fp32 values (and back).
@@ -346,9 +377,9 @@ void move_rows_kernel(MoveArgs a, InlineArg<INLINE> ix) {
 
   RowSide src = a.src;
   int64_t src_off, dst_off;
-  if (SRCM == ROW_DONOR_POS) {
+  if (SRCM == ROW_DONOR_POS || SRCM == ROW_DONOR_GROUPED) {
     int dn;
-    if (a.donors.grouped) {
+    if (SRCM == ROW_DONOR_GROUPED) {
       // The workgroup's donor, from its first pair: uniform, so the donor's strides and layer
       // table come through scalar loads.
       const int64_t first_pair = static_cast<int64_t>(blockIdx.x) * (kThreads >> a.tpr_log2);
@@ -394,7 +425,10 @@ void move_rows_kernel(MoveArgs a, InlineArg<INLINE> ix) {
   auto row_of = [&](const RowSide& side, int r) {
     const int l = l0 + r / a.num_heads;
     const int h = r - (r / a.num_heads) * a.num_heads;
-    return layer_base(side, l) + kv * side.s_kv + h * side.s_head;
+    // (a grouped composite source, src.layers, is uniform per workgroup)
+    const char* base = (SRCM == ROW_DONOR_GROUPED && &side == &src) ? layer_base<true>(side, l)
+                                                                      : layer_base<false>(side, l);
+    return const_cast<char*>(base) + kv * side.s_kv + h * side.s_head;
   };
   for (int j = lane; j < a.vpr; j += tpr) {
     float c0[NPA], s0[NPA], c1[NPA], s1[NPA];
@@ -505,9 +539,9 @@ struct RopeRowsArgs {
 
 // The pair-centric form (donor positions distinct) has no multi-pair path. Its knobs: waves
 // per SIMD (1: the compiler's choice, 67 VGPRs and 7 waves with sincos_cw) and rows per batch.
-// On the 7B workload (28 x 4 x 8192 rows) the defaults take 85-86 us; 8 waves 86 us (61
-// VGPRs), 4-row batches at 8 waves 91 us. (With the general-purpose double sincos it held
-// 90 VGPRs, and 8 waves spilled 46 registers: 107 us.)
+// On the 7B workload (28 x 4 x 8192 rows, 4 rows per thread) the defaults take 76.8 us, 8
+// waves 77.3 us. (With the general-purpose double sincos it held 90 VGPRs, and 8 waves
+// spilled 46 registers: 107 us at 14 rows per thread.)
 #ifndef SB_ROPE_DISTINCT_WAVES
 #define SB_ROPE_DISTINCT_WAVES 1
 #endif
@@ -1005,7 +1039,6 @@ static int composite_impl(
   a.dst = side_paged(nullptr, kv_layer_ptrs, kv_strides, es);
   a.donors.layers = donor_layer_ptrs;
   a.donors.index = donor_index;
-  a.donors.grouped = segment_ends ? 1 : 0;
   if (segment_ends)
     for (int64_t k = 0; k < num_donors; ++k) a.donors.seg_end[k] = segment_ends[k];
   a.src_pos = donor_pos;
@@ -1035,9 +1068,17 @@ static int composite_impl(
       a.donors.bound[k] = d[3];
       a.donors.first_pos[k] = d[4];
     }
-    const int rc =
-        rope ? launch_move<ROT_DELTA, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, slices, st)
-             : launch_move<ROT_NONE, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, slices, st);
+    int rc;
+    if (segment_ends)
+      rc = rope ? launch_move<ROT_DELTA, ROW_DONOR_GROUPED, ROW_PAGED_POS>(fn, a, dtype, g,
+                                                                          slices, st)
+                : launch_move<ROT_NONE, ROW_DONOR_GROUPED, ROW_PAGED_POS>(fn, a, dtype, g,
+                                                                         slices, st);
+    else
+      rc = rope ? launch_move<ROT_DELTA, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, slices,
+                                                                      st)
+                : launch_move<ROT_NONE, ROW_DONOR_POS, ROW_PAGED_POS>(fn, a, dtype, g, slices,
+                                                                     st);
     if (rc) return rc;
   }
   return SB_OK;
@@ -1653,4 +1694,38 @@ extern "C" int sb_nope_permute_paged_kv_layers(
                    block_table, src_pos, tgt_pos, num_pairs, v_src_pos, v_tgt_pos, num_v_pairs,
                    inv_freq, workspace, num_heads, block_size, head_dim, num_blocks_total,
                    num_blocks_per_seq, kv_strides, dtype, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------------------
+// Flat device copy: the achievable-bandwidth reference the movers are measured against. One
+// 16-byte vector per thread, nontemporal load and store, 256-thread blocks. On MI355X this
+// moves 6.5 TB/s (1 GiB and 235-470 MB copies); four vectors per thread 6.2-6.3 TB/s, eight
+// 4.3 TB/s, the runtime's device-to-device copy 5.1-5.4 TB/s.
+// ---------------------------------------------------------------------------------------
+namespace sb {
+__global__ __launch_bounds__(256) void copy_vec16_kernel(const char* src, char* dst,
+                                                         int64_t num_vec) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= num_vec) return;
+  uint32_t w[4];
+  load_vec<16, true>(src + i * 16, w);
+  store_vec<16, true>(dst + i * 16, w);
+}
+}  // namespace sb
+
+extern "C" int sb_device_copy(void* dst, const void* src, int64_t num_bytes, void* stream) {
+  const char* fn = "sb_device_copy";
+  clear_error();
+  if (num_bytes == 0) return SB_OK;
+  if (!dst || !src) return fail(fn, "null pointer argument");
+  if (num_bytes < 0 || num_bytes % 16 != 0) return fail(fn, "num_bytes must be a multiple of 16");
+  if (reinterpret_cast<uintptr_t>(dst) % 16 != 0 || reinterpret_cast<uintptr_t>(src) % 16 != 0)
+    return fail(fn, "buffers must be 16-byte aligned");
+  const int64_t num_vec = num_bytes / 16;
+  const int64_t blocks = (num_vec + 255) / 256;
+  if (blocks > 0x7fffffff) return fail(fn, "copy too large");
+  SB_LAUNCH("copy", copy_vec16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256),
+            static_cast<hipStream_t>(stream), static_cast<const char*>(src),
+            static_cast<char*>(dst), num_vec);
+  return check_launch(fn);
 }

@@ -106,6 +106,17 @@ def test_invalid_arguments_are_rejected_without_launch():
         assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"2^31" in lib.sb_last_error_string()
 
 
+def test_device_copy_rejects_bad_sizes_and_alignment():
+    lib = _lib.lib()
+    rc = lib.sb_device_copy(4096, 8192, 40, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"multiple of 16" in lib.sb_last_error_string()
+    rc = lib.sb_device_copy(4097, 8192, 32, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"aligned" in lib.sb_last_error_string()
+    rc = lib.sb_device_copy(None, 8192, 32, None)
+    assert rc == _lib.SB_ERR_INVALID_ARGUMENT and b"null" in lib.sb_last_error_string()
+    assert lib.sb_device_copy(None, None, 0, None) == _lib.SB_OK
+
+
 def test_grouped_composite_rejects_bad_segments():
     lib = _lib.lib()
     fake = 4096

@@ -251,3 +251,24 @@ def test_cpu_tensors_rejected():
     with pytest.raises(RuntimeError, match="device tensors"):
         tk.scatter_donor_kv_paged(kv, torch.zeros((2, 1, 4, 8)), torch.tensor([0]),
                                   torch.tensor([0]), torch.tensor([0]))
+
+
+# ---- the flat copy the movers' bandwidth is compared with ----
+
+@pytest.mark.parametrize("nbytes", [16, 4096 + 16, (1 << 20) + 48, 64 << 20])
+def test_device_copy_bytes(dev, nbytes):
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, generator=gen(31)).to(dev)
+    dst = torch.zeros_like(src)
+    from semblend_amd import _lib
+    _lib.device_copy(dst, src)
+    torch.cuda.synchronize()
+    assert torch.equal(dst, src)
+
+
+def test_device_copy_rejects_unaligned(dev):
+    from semblend_amd import _lib
+    a = torch.zeros(64, dtype=torch.uint8, device=dev)
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        _lib.device_copy(a[:40], a[16:56])
+    with pytest.raises(RuntimeError, match="aligned"):
+        _lib.device_copy(a[1:17], a[32:48])
