@@ -63,13 +63,14 @@ KERNELS = ("attn_mfma", "attn_merge", "move_rows", "rope_rows", "rope_index", "f
 
 # HBM bytes per launch on this workload, from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
 # this script, scaled by what the same counters read for the 1 GiB copy of copy_ceiling()
-# (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); kernel changes call for a new measurement.
+# (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); kernel changes call for a new measurement. Attention:
+# the planned launch that the step times.
 MEASURED_TRAFFIC_BYTES = {
-    "attn_mfma": (2 * 72949 + 40897) * 1024,
-    "move_rows": (2 * 391166 + 779861) * 1024,
-    "rope_rows": (2 * 114830 + 229388) * 1024,
+    "attn_mfma": (2 * 92961 + 63581) * 1024,
+    "move_rows": (2 * 391157 + 779861) * 1024,
+    "rope_rows": (2 * 114794 + 229376) * 1024,
 }
-MEASURED_TRAFFIC_SOURCE = ("rocprofv3 FETCH_SIZE / WRITE_SIZE passes at commit 3d8b7a9, "
+MEASURED_TRAFFIC_SOURCE = ("rocprofv3 FETCH_SIZE / WRITE_SIZE passes at commit c40bef3, "
                            "profiles/kv_reuse_7b_16k_hbm_traffic.md")
 
 
