@@ -123,11 +123,15 @@ int sb_masked_qkv_projection(void* out, const void* hidden, const void* weight, 
  * (kv_strides[5] = block, kv, head, pos, dim in elements), skipped when the slot is out of
  * range. A row whose position is outside [0, seq_len) gets a zero Q row and writes no K/V.
  * head_dim must be a multiple of 8 and every row (hidden, W, q_out, cache) 16-byte aligned.
- * With RoPE, `workspace` (16-byte aligned, sb_qkv_projection_paged_workspace_size bytes)
- * holds the per-row cos/sin table; without, it may be NULL.
+ * `workspace` (16-byte aligned, sb_qkv_projection_paged_workspace_size bytes) holds the
+ * per-row cos/sin table with RoPE and, for row counts too small to give every CU a tile,
+ * the fp32 partial products of a split of the hidden dimension (summed in a fixed order by
+ * the epilogue); it may be NULL when that size is 0.
  * No reference counterpart: it fuses masked_qkv_projection (triton_kernels.py:451-522) with
  * the K/V write of partial_prefill (:904-909) into the paged layout, for GQA models. */
-int64_t sb_qkv_projection_paged_workspace_size(int64_t num_rows, int64_t head_dim, int32_t rope);
+int64_t sb_qkv_projection_paged_workspace_size(int64_t num_rows, int64_t num_q_heads,
+                                               int64_t num_kv_heads, int64_t head_dim,
+                                               int64_t hidden_dim, int32_t rope);
 int sb_qkv_projection_paged(void* q_out, const void* hidden, const void* weight,
                             const void* bias, const int32_t* positions, int64_t num_rows,
                             int64_t seq_len, int64_t hidden_dim, int64_t num_q_heads,

@@ -115,7 +115,7 @@ SIZE_QUERIES: dict[str, list] = {
                                         _i64],
     "sb_partial_attention_paged_planned_workspace_size": [_i64, _i64, _i64, _i64, _i32, _i32],
     "sb_masked_qkv_projection_workspace_size": [_i64],
-    "sb_qkv_projection_paged_workspace_size": [_i64, _i64, _i32],
+    "sb_qkv_projection_paged_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i32],
 }
 
 _lib: ctypes.CDLL | None = None

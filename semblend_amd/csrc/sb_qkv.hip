@@ -67,7 +67,10 @@ static_assert(kStages >= 2 && kStages <= 4, "the step waits cover rings of 2 to 
 constexpr int kGroup = SB_QKV_GROUP;  // row tiles per band of the tile order
 constexpr int kXcds = 8;       // MI355X: workgroups go round-robin to 8 XCDs
 
-enum QkvMode : int { QKV_SPLIT = 0, QKV_DENSE = 1 };
+// QKV_PARTIAL: the split form's product for small row counts, the hidden dimension split over
+// grid.y (each slice's fp32 partial product to a workspace; qkv_epilogue_kernel sums the
+// slices in order and runs the split form's epilogue).
+enum QkvMode : int { QKV_SPLIT = 0, QKV_DENSE = 1, QKV_PARTIAL = 2 };
 
 struct QkvArgs {
   const char* hidden;         // [S, hidden] rows
@@ -91,6 +94,9 @@ struct QkvArgs {
   int64_t s_blk, s_kv, s_head, s_pos;
   const int32_t* block_table;
   int64_t block_size, nb_total, nb_per_seq;
+  float* part;                // QKV_PARTIAL: [splits][R][F] fp32 partial products
+  int64_t split_steps;        // QKV_PARTIAL: k-steps per slice of the hidden dimension
+  int64_t splits;             // epilogue: slices to sum (0 or 1: one product)
 };
 
 // 16-byte chunk position of chunk c of tile row r. 256 bytes of banks hold 256 / (2 kTK)
@@ -214,6 +220,13 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
   int64_t rows = a.num_rows;
   if (a.count) rows = min(rows, static_cast<int64_t>(*a.count));
   if (n0 >= rows) return;  // uniform
+  // This workgroup's k-steps: all of them, or (QKV_PARTIAL) slice blockIdx.y.
+  int64_t kbeg = 0, nsteps = a.k_steps;
+  if (MODE == QKV_PARTIAL) {
+    kbeg = static_cast<int64_t>(blockIdx.y) * a.split_steps;
+    nsteps = min(a.split_steps, a.k_steps - kbeg);
+    if (nsteps <= 0) return;  // uniform
+  }
 
   for (int t = tid; t < TN; t += kQThreads) {
     const int64_t n = n0 + t;
@@ -257,7 +270,7 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
     bsrc[q] = a.hidden + brow[q * kLoadRows + tid / kTileChunks] + 16 * chunk;
   // Load q of a step (A loads first, then B), each 16 bytes per lane into its stage.
   auto issue_one = [&](int stage, int64_t kt, int q) {
-    const int64_t ko = kt * (kTK * 2);
+    const int64_t ko = (kbeg + kt) * (kTK * 2);
     if (q < LA)
       qkv_dma(asrc[q] + ko, qkv_lds_addr(As(stage)) + (q * kQThreads + wave * 64) * 16);
     else
@@ -282,7 +295,7 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
   // loads issued right after it refill.
 #pragma unroll
   for (int s0 = 0; s0 < kStages - 1; ++s0)
-    if (s0 < a.k_steps) issue(s0, s0);
+    if (s0 < nsteps) issue(s0, s0);
   // Step kt; REFILL: whether it issues the loads of step kt + kStages - 1 (every step but
   // the last kStages - 1), a compile-time choice so that the loads need no branch.
   auto step = [&](int64_t kt, auto refill_c) {
@@ -290,7 +303,7 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
     const int st = static_cast<int>(kt % kStages);
     // Steps issued after this one: at most kStages - 2, fewer near the end; they may stay
     // in flight while step kt must have landed.
-    const int64_t ahead = a.k_steps - 1 - kt;
+    const int64_t ahead = nsteps - 1 - kt;
     if (kStages >= 4 && ahead >= 2) qkv_wait_vm<2 * (LA + LB)>();
     else if (kStages >= 3 && ahead >= 1) qkv_wait_vm<LA + LB>();
     else qkv_wait_vm<0>();
@@ -355,8 +368,30 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
   };
   {
     int64_t kt = 0;
-    for (; kt + kStages - 1 < a.k_steps; ++kt) step(kt, std::true_type{});
-    for (; kt < a.k_steps; ++kt) step(kt, std::false_type{});
+    for (; kt + kStages - 1 < nsteps; ++kt) step(kt, std::true_type{});
+    for (; kt < nsteps; ++kt) step(kt, std::false_type{});
+  }
+
+  if constexpr (MODE == QKV_PARTIAL) {
+    // The slice's fp32 product: lane (lq, lg) of block (i, j) holds row wn*32*BJ + 32j + lq,
+    // features wm*32*BI + 32i + 8g + 4lg .. +3 in register group g.
+    float* pp = a.part + static_cast<int64_t>(blockIdx.y) * a.num_rows * a.num_features;
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+      const int64_t n = n0 + wn * (32 * BJ) + j * 32 + lq;
+      if (n >= rows) continue;
+#pragma unroll
+      for (int i = 0; i < BI; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t f = m0 + wm * (32 * BI) + i * 32 + 8 * g + 4 * lg;
+          if (f < a.num_features)
+            *reinterpret_cast<float4*>(pp + n * a.num_features + f) =
+                make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                            acc[i][j][4 * g + 3]);
+        }
+    }
+    return;
   }
 
   // Epilogue, phase 1: lane (lq, lg) of block (i, j) holds tile row wn*32*BJ + 32j + lq and,
@@ -509,6 +544,14 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a, const floa
     const float4* src = reinterpret_cast<const float4*>(proj + n * p_s_row + f0);
     const float4 x0 = src[0], x1 = src[1];
     float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    // Slices of a split product, summed in slice order.
+    for (int64_t sl = 1; sl < a.splits; ++sl) {
+      const float4* ps = reinterpret_cast<const float4*>(proj + sl * a.num_rows * p_s_row +
+                                                         n * p_s_row + f0);
+      const float4 y0 = ps[0], y1 = ps[1];
+      v[0] += y0.x; v[1] += y0.y; v[2] += y0.z; v[3] += y0.w;
+      v[4] += y1.x; v[5] += y1.y; v[6] += y1.z; v[7] += y1.w;
+    }
     if (a.bias) {
       const uint16_t* b = reinterpret_cast<const uint16_t*>(a.bias) + f0;
 #pragma unroll
@@ -576,29 +619,62 @@ int qkv_common(const char* fn, QkvArgs* a, const void* hidden, const void* weigh
 
 // Tile shape. 256 features x 64 BJ rows (one workgroup per CU) with BJ in {3, 2} chosen to
 // minimise the work of the busiest CU, rounds x BJ (ties: larger tiles); 128 x 128 (two per
-// CU) when even BJ = 2 leaves more than half the CUs without a tile. (BJ = 4 spilled 5-6
-// VGPRs and never cost less than BJ = 2 in this model: at most a tie.)
+// CU) when the big tiles leave more than half the CUs idle, or leave some idle while the
+// small ones fit one round of two per CU. (BJ = 4 spilled 5-6 VGPRs and never cost less than
+// BJ = 2 in this model: at most a tie.) When even the 128 x 128 tiles number fewer than the
+// CUs (a few hundred rows at the 7B shape), the split form also splits the hidden dimension
+// over grid.y, into slices of at least kMinSplitSteps k-steps (QKV_PARTIAL and the summing
+// epilogue). Qwen2.5-7B shape (3584 -> 4608 features), graph replays on one box, interleaved:
+// slices of at least 12 steps 28-30 us at 64 rows (6 steps: 32 us, 19: 35 us), 30.5 us at 128
+// and 35.5 us at 256 (library 28, 33, 46 us); small tiles from 1024 to 1536 rows 61-72 us
+// against 75-77 us with the 256-feature tiles, which stay faster from 2048 rows (97 against
+// 113 us).
 constexpr int64_t kCus = 256;
-template <int MODE>
-int launch_qkv(const char* fn, const QkvArgs& a, int32_t dtype, hipStream_t st) {
-  const int64_t nft = (a.num_features + 255) / 256;
-  int bj = 0;
-  int64_t best = 0, tiles = 0;
+#ifndef SB_QKV_MIN_SPLIT_STEPS
+#define SB_QKV_MIN_SPLIT_STEPS 12
+#endif
+constexpr int64_t kMinSplitSteps = SB_QKV_MIN_SPLIT_STEPS;
+struct QkvPlan {
+  int bj = 0;               // 3 or 2: 256 x 64 bj tiles; 0: 128 x 128 tiles
+  int64_t tiles = 0;
+  int64_t splits = 1;       // slices of the hidden dimension (> 1: QKV_PARTIAL)
+  int64_t split_steps = 0;  // k-steps per slice
+};
+QkvPlan qkv_plan(int64_t rows, int64_t features, int64_t k_steps, bool allow_split) {
+  QkvPlan pl;
+  const int64_t nft = (features + 255) / 256;
+  int64_t best = 0;
   for (int c = 3; c >= 2; --c) {
-    const int64_t t = nft * ((a.num_rows + 64 * c - 1) / (64 * c));
+    const int64_t t = nft * ((rows + 64 * c - 1) / (64 * c));
     const int64_t cost = ((t + kCus - 1) / kCus) * c;
-    if (bj == 0 || cost < best) {
-      bj = c;
+    if (pl.bj == 0 || cost < best) {
+      pl.bj = c;
       best = cost;
-      tiles = t;
+      pl.tiles = t;
     }
   }
-  if (tiles * 2 < kCus) {
-    bj = 0;  // small tiles
-    tiles = ((a.num_features + 127) / 128) * ((a.num_rows + 127) / 128);
+  const int64_t small = ((features + 127) / 128) * ((rows + 127) / 128);
+  if (pl.tiles * 2 < kCus || (pl.tiles < kCus && small <= 2 * kCus)) {
+    pl.bj = 0;  // small tiles
+    pl.tiles = small;
+    if (allow_split && pl.tiles > 0 && pl.tiles < kCus) {
+      const int64_t s = std::min<int64_t>((2 * kCus) / pl.tiles, k_steps / kMinSplitSteps);
+      if (s > 1) {
+        pl.split_steps = (k_steps + s - 1) / s;
+        pl.splits = (k_steps + pl.split_steps - 1) / pl.split_steps;
+      }
+    }
   }
-  if (tiles > 0x7fffffff) return fail(fn, "grid too large");
-  const dim3 grid(static_cast<unsigned>(tiles));
+  return pl;
+}
+
+template <int MODE>
+int launch_qkv(const char* fn, const QkvArgs& a, int32_t dtype, hipStream_t st,
+               const QkvPlan& pl) {
+  if (pl.tiles > 0x7fffffff || pl.splits > 65535) return fail(fn, "grid too large");
+  const dim3 grid(static_cast<unsigned>(pl.tiles),
+                  static_cast<unsigned>(MODE == QKV_PARTIAL ? pl.splits : 1));
+  const int bj = pl.bj;
 #define SB_QKV_CASE(DT, BI, BJ)                                                              \
   SB_LAUNCH("qkv_mfma", (qkv_mfma_kernel<DT, MODE, BI, BJ>), grid, dim3(kQThreads), st, a)
 #define SB_QKV_DT(DT)                   \
@@ -617,14 +693,43 @@ int launch_qkv(const char* fn, const QkvArgs& a, int32_t dtype, hipStream_t st) 
   return check_launch(fn);
 }
 
+// The summing epilogue of a split product (and the library form's epilogue): one thread per
+// 8 features of a row.
+int launch_qkv_epilogue(const char* fn, const QkvArgs& a, const float* proj, int64_t p_s_row,
+                        int32_t dtype, hipStream_t st) {
+  const int64_t threads = a.num_rows * (a.num_features / 8);
+  if ((threads + 255) / 256 > 0x7fffffff) return fail(fn, "grid too large");
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  if (dtype == SB_DTYPE_BF16)
+    SB_LAUNCH("qkv_epilogue", qkv_epilogue_kernel<SB_DTYPE_BF16>, grid, dim3(256), st, a, proj,
+              p_s_row);
+  else
+    SB_LAUNCH("qkv_epilogue", qkv_epilogue_kernel<SB_DTYPE_F16>, grid, dim3(256), st, a, proj,
+              p_s_row);
+  return check_launch(fn);
+}
+
+// Workspace of the split form: the RoPE table first, then (split product) the slices.
+constexpr int64_t kQkvWsAlign = 256;
+int64_t qkv_table_bytes(int64_t num_rows, int64_t head_dim, bool rope) {
+  const int64_t t = rope ? num_rows * head_dim * static_cast<int64_t>(sizeof(float)) : 0;
+  return (t + kQkvWsAlign - 1) / kQkvWsAlign * kQkvWsAlign;
+}
+
 }  // namespace
 }  // namespace sb
 
 using namespace sb;
 
-extern "C" int64_t sb_qkv_projection_paged_workspace_size(int64_t num_rows, int64_t head_dim,
-                                                         int32_t rope) {
-  return rope ? num_rows * head_dim * static_cast<int64_t>(sizeof(float)) : 0;
+extern "C" int64_t sb_qkv_projection_paged_workspace_size(int64_t num_rows, int64_t num_q_heads,
+                                                         int64_t num_kv_heads, int64_t head_dim,
+                                                         int64_t hidden_dim, int32_t rope) {
+  if (num_rows <= 0 || num_q_heads <= 0 || num_kv_heads < 0 || head_dim <= 0 || hidden_dim <= 0)
+    return 0;
+  const int64_t features = (num_q_heads + 2 * num_kv_heads) * head_dim;
+  const QkvPlan pl = qkv_plan(num_rows, features, hidden_dim / kTK, true);
+  const int64_t part = pl.splits > 1 ? pl.splits * num_rows * features * 4 : 0;
+  return qkv_table_bytes(num_rows, head_dim, rope != 0) + part;
 }
 
 extern "C" int sb_qkv_projection_paged(
@@ -659,11 +764,15 @@ extern "C" int sb_qkv_projection_paged(
   a.kv_features = kvf;
   a.head_dim = static_cast<int>(head_dim);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (inv_freq) {
+  const QkvPlan pl = qkv_plan(num_rows, a.num_features, a.k_steps, true);
+  const int64_t ws_need = sb_qkv_projection_paged_workspace_size(
+      num_rows, num_q_heads, num_kv_heads, head_dim, hidden_dim, inv_freq ? 1 : 0);
+  if (ws_need > 0) {
     if (!workspace || reinterpret_cast<uintptr_t>(workspace) % 16)
-      return fail(fn, "RoPE needs a 16-byte aligned workspace");
-    if (workspace_bytes < sb_qkv_projection_paged_workspace_size(num_rows, head_dim, 1))
-      return fail(fn, "workspace too small");
+      return fail(fn, "RoPE and the split product need a 16-byte aligned workspace");
+    if (workspace_bytes < ws_need) return fail(fn, "workspace too small");
+  }
+  if (inv_freq) {
     float4* table = static_cast<float4*>(workspace);
     const int64_t n = num_rows * (head_dim / 4);
     SB_LAUNCH("qkv_rope_table", qkv_rope_table_kernel,
@@ -684,7 +793,16 @@ extern "C" int sb_qkv_projection_paged(
   a.block_size = block_size;
   a.nb_total = num_blocks_total;
   a.nb_per_seq = num_blocks_per_seq;
-  return launch_qkv<QKV_SPLIT>(fn, a, dtype, st);
+  if (pl.splits > 1) {
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                      qkv_table_bytes(num_rows, head_dim, inv_freq != nullptr));
+    a.split_steps = pl.split_steps;
+    rc = launch_qkv<QKV_PARTIAL>(fn, a, dtype, st, pl);
+    if (rc) return rc;
+    a.splits = pl.splits;
+    return launch_qkv_epilogue(fn, a, a.part, a.num_features, dtype, st);
+  }
+  return launch_qkv<QKV_SPLIT>(fn, a, dtype, st, pl);
 }
 
 extern "C" int sb_qkv_gather_rows(void* xg, const void* hidden, const int32_t* positions,
@@ -763,17 +881,7 @@ extern "C" int sb_qkv_epilogue_paged(
   a.block_size = block_size;
   a.nb_total = num_blocks_total;
   a.nb_per_seq = num_blocks_per_seq;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t threads = num_rows * (a.num_features / 8);
-  if ((threads + 255) / 256 > 0x7fffffff) return fail(fn, "grid too large");
-  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
-  if (dtype == SB_DTYPE_BF16)
-    SB_LAUNCH("qkv_epilogue", qkv_epilogue_kernel<SB_DTYPE_BF16>, grid, dim3(256), st, a, proj,
-              proj_stride);
-  else
-    SB_LAUNCH("qkv_epilogue", qkv_epilogue_kernel<SB_DTYPE_F16>, grid, dim3(256), st, a, proj,
-              proj_stride);
-  return check_launch(fn);
+  return launch_qkv_epilogue(fn, a, proj, proj_stride, dtype, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int64_t sb_masked_qkv_projection_workspace_size(int64_t seq_len) {
@@ -821,5 +929,5 @@ extern "C" int sb_masked_qkv_projection(void* out, const void* hidden, const voi
   a.head_dim = 8;
   a.out = static_cast<char*>(out);
   a.o_s_row = out_stride * 2;
-  return launch_qkv<QKV_DENSE>(fn, a, dtype, st);
+  return launch_qkv<QKV_DENSE>(fn, a, dtype, st, qkv_plan(a.num_rows, a.num_features, a.k_steps, false));
 }

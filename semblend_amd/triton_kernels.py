@@ -262,6 +262,11 @@ def masked_qkv_projection(
 
 
 
+# Row counts up to which qkv_projection_paged(backend="auto") takes the fused kernel (measured
+# at the Qwen2.5-7B shape: faster or level with the library GEMM there, slower above).
+_FUSED_PROJECTION_MAX_ROWS = 512
+
+
 def qkv_projection_paged(
     hidden_states: torch.Tensor,
     qkv_weight: torch.Tensor,
@@ -288,11 +293,13 @@ def qkv_projection_paged(
     ``backend``: "fused" runs one MFMA kernel that gathers the rows, multiplies and writes
     Q and K/V from its epilogue; "library" gathers the rows, multiplies them with the
     library GEMM (hipBLASLt through torch, fp32 output) and runs the same epilogue as a
-    kernel of its own (bias, RoPE, one rounding, Q and the paged K/V write); "auto" is the
-    library form, the faster of the two on MI355X at every row count measured (64 to 4096
-    rows at the Qwen2.5-7B shape, one graph replay: 28.6 against 51.9 us at 64 rows, 96.4
-    against 119.3 us at 2458). The fused form needs no fp32 intermediate of rows x features.
-    Both accumulate in fp32 and round once.
+    kernel of its own (bias, RoPE, one rounding, Q and the paged K/V write); "auto" takes the
+    fused form up to 512 rows (where it splits the hidden dimension when the row tiles are
+    too few for the CUs) and the library form above. Qwen2.5-7B shape, graph replays on one
+    MI355X, fused / library: 29 / 28 us at 64 rows, 30.5 / 33 at 128, 35.5 / 46 at 256, 43 /
+    43 at 512, 52 / 50 at 768, 61 / 58 at 1024, 97 / 88 at 2048, 99 / 100 at 2458, 171 / 164
+    at 4096. The fused form needs no fp32 intermediate of rows x features. Both accumulate in
+    fp32 and round once.
     Fuses the masked projection (semblend_core/triton_kernels.py:451-522) with the K/V write
     of partial_prefill (:904-909), compacted and paged; no reference counterpart.
     """
@@ -329,13 +336,14 @@ def qkv_projection_paged(
         return out
     bias = None if qkv_bias is None else qkv_bias.contiguous()
     inv = inv_freq_table(rope_base, head_dim, dev) if rope_base is not None else None
-    ws_bytes = _lib.size_query("sb_qkv_projection_paged_workspace_size", n, head_dim,
-                               int(inv is not None))
-    ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=dev)
-    if backend in ("library", "auto"):
+    if backend == "auto":
+        backend = "fused" if n <= _FUSED_PROJECTION_MAX_ROWS else "library"
+    if backend == "library":
         # rows outside the hidden states are gathered as zeros; the epilogue zeroes their Q
         # and writes no K/V for them
         xg = torch.empty((n, hidden), dtype=dt, device=dev)
+        ws = torch.empty(max(n * head_dim, 4) if inv is not None else 4, dtype=torch.float32,
+                         device=dev)
         dt_code = _lib.dtype_code(hidden_states)
         with _lib.on_device(dev):
             _lib.call("sb_qkv_gather_rows", xg.data_ptr(), hidden_states.data_ptr(),
@@ -350,6 +358,9 @@ def qkv_projection_paged(
                 num_heads * head_dim, _lib.strides(kv_cache), dt_code, _lib.stream_handle(dev),
             )
         return out
+    ws_bytes = _lib.size_query("sb_qkv_projection_paged_workspace_size", n, num_heads,
+                               num_kv_heads, head_dim, hidden, int(inv is not None))
+    ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=dev)
     with _lib.on_device(dev):
         _lib.call(
             "sb_qkv_projection_paged",

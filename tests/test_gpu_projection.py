@@ -126,6 +126,17 @@ def test_projection_paged_qwen7b_full(dev, backend):
 
 
 @pytest.mark.parametrize("backend", BACKENDS)
+@pytest.mark.parametrize("n_rows", [64, 300])
+def test_projection_paged_qwen7b_few_rows(dev, n_rows, backend):
+    """Few rows at the Qwen2.5-7B shape, RoPE theta 1e6: the fused form splits the hidden
+    dimension (4 slices of 14 k-steps at 64 and at 300 rows) and its epilogue sums the slices;
+    a row without a position gets a zero Q and writes no K/V."""
+    x, w, b, pos, bt, cache = _case(4096, 3584, 28, 4, 128, n_rows, torch.bfloat16, 40)
+    pos = torch.cat([pos, torch.tensor([-1], dtype=torch.int32)])
+    _check_paged(dev, x, w, b, pos, bt, cache, 28, 4, 128, 1e6, backend)
+
+
+@pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("n_rows", [700, 2100])
 def test_projection_paged_llama_shape(dev, n_rows, backend):
     # Llama-3-8B attention: hidden 4096, 32 / 8 heads x 128, no bias, theta 5e5 (700 rows
