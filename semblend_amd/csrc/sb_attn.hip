@@ -1179,10 +1179,12 @@ attn_mfma_kernel(const AttnBatch batch) {
 //   M = max_c m_c,  O = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.
 // One workgroup per (32 rows of a row tile, KV head); 8 threads per row, each owning D / 8
 // output elements, so the partial reads of a row are spread over 8 lanes.
+// Chunks whose partials a merge lane loads in one batch. Six covers the host-planned split of
+// the 7B 16K workload (up to five chunks per row tile): merge 15.3 -> 13.4 us against four
+// (tiles with five chunks then took the two-pass loop); eight gives the same 13.5 us.
 #ifndef SB_MERGE_BATCH_CHUNKS
-#define SB_MERGE_BATCH_CHUNKS 4
+#define SB_MERGE_BATCH_CHUNKS 6
 #endif
-// Chunks whose partials a merge lane loads in one batch.
 constexpr int kMergeBatch = SB_MERGE_BATCH_CHUNKS;
 // One unit: 32 rows of row tile `tile` of KV head `kvh` (mb = (tile * parts + part) * Hkv +
 // kvh). Returns early when the unit has nothing to merge; its one barrier is reached by every
