@@ -133,7 +133,7 @@ constexpr int64_t kGroupedPairAlign = 256;
 
 struct MoveArgs {
   RowSide src, dst;
-  DonorSet donors;         // ROW_DONOR_POS sources only
+  DonorSet donors;         // donor sources (ROW_DONOR_POS, ROW_DONOR_GROUPED) only
   const int32_t* src_pos;  // per-pair source positions (FLAT_POS / PAGED_POS sources)
   const int32_t* dst_pos;  // per-pair destination positions
   const int32_t* repeat;   // ROT_CONST: rotations to apply per pair (nullptr = 1)
