@@ -54,6 +54,10 @@ constexpr int kQThreads = 256;
 #ifndef SB_QKV_FRAG_PIPE
 #define SB_QKV_FRAG_PIPE 1
 #endif
+// Epilogue: blocks of RoPE table entries (4 groups x row blocks) loaded ahead of their use.
+#ifndef SB_QKV_CS_AHEAD
+#define SB_QKV_CS_AHEAD 1
+#endif
 // Substeps over which a step's refill loads are spread (the first ones of the step).
 #ifndef SB_QKV_DMA_SPREAD
 #define SB_QKV_DMA_SPREAD 2
@@ -166,19 +170,45 @@ __device__ __forceinline__ uint32_t qkv_pack2(float lo, float hi) {
   if (DT == SB_DTYPE_BF16) return pack2_bf16(lo, hi);
   return static_cast<uint32_t>(f32_to_f16(lo)) | (static_cast<uint32_t>(f32_to_f16(hi)) << 16);
 }
+// The same rounding without pack2_bf16's NaN canonicalisation (bf16: identical bits for every
+// input but NaN; fp16 has none to drop). For callers that check for NaN separately.
+template <int DT>
+__device__ __forceinline__ uint32_t qkv_pack2_fast(float lo, float hi) {
+  if (DT == SB_DTYPE_BF16) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  return qkv_pack2<DT>(lo, hi);
+}
 
 // cos / sin of every (computed row, rotary pair), correctly rounded to fp32 (fp64 sincos):
-// table[n * D/4 + i/2] = (cos, sin) of pair 2 * (i/2) and of the next pair, angle
-// float(p) * inv_freq[pair]. Rows without a valid position get the identity.
+// entry e of row n = (cos, sin) of pairs 2e and 2e + 1, angle float(p) * inv_freq[pair];
+// rows without a valid position get the identity. Layouts:
+//   row-major (IL false)  table[n * D/4 + e], num_rows rows;
+//   interleaved (IL true) table[((n / 32) * D/4 + e) * 32 + n % 32], rows padded to a
+//   multiple of 32 (identity): the fused kernel's lanes hold 32 consecutive rows, so one
+//   entry of all of them is 512 contiguous bytes.
+template <bool IL>
 __global__ void qkv_rope_table_kernel(const int32_t* positions, int64_t num_rows,
                                       int64_t seq_len, const float* inv_freq, int half_d,
                                       float4* table) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int quads = half_d / 2;
-  if (idx >= num_rows * quads) return;
-  const int64_t n = idx / quads;
-  const int k = static_cast<int>(idx - n * quads);
-  const int p = positions[n];
+  const int64_t table_rows = IL ? (num_rows + 31) / 32 * 32 : num_rows;
+  if (idx >= table_rows * quads) return;
+  int64_t n;
+  int k;
+  if (IL) {
+    const int64_t grp = idx / (32 * quads);
+    const int64_t rem = idx - grp * 32 * quads;
+    k = static_cast<int>(rem / 32);
+    n = grp * 32 + (rem & 31);
+  } else {
+    n = idx / quads;
+    k = static_cast<int>(idx - n * quads);
+  }
+  const int p = n < num_rows ? positions[n] : -1;
   float4 v = make_float4(1.f, 0.f, 1.f, 0.f);
   if (p >= 0 && p < seq_len) {
     sincos_rn(static_cast<float>(p) * inv_freq[2 * k], &v.y, &v.x);
@@ -399,64 +429,135 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
   // rounding happen in registers; the rounded tile goes to LDS as [TN rows][TM features],
   // 8-byte units of row r XOR-swizzled by 2 (r % 16) so that the 32 rows a wave writes at
   // once spread over the banks (and 16-byte pairs of units stay adjacent for phase 2).
-  const int64_t kf0 = a.q_features, vf0 = a.q_features + a.kv_features;
+  // Feature indices fit 32 bits (F = (Hq + 2 Hkv) D): the head arithmetic below is unsigned
+  // 32-bit and hoisted out of the row loops (64-bit divisions by a run-time head_dim expand to
+  // long instruction sequences, and this part runs one wave per SIMD).
+  const uint32_t kf0 = static_cast<uint32_t>(a.q_features);
+  const uint32_t vf0 = static_cast<uint32_t>(a.q_features + a.kv_features);
+  const uint32_t hd = static_cast<uint32_t>(a.head_dim);
   const int quads = a.head_dim / 4;
-  __syncthreads();  // every wave is done with the last stage
+  // Table entry (within a row's D/4) of register group (i, g): Q and K features rotate by
+  // their offset within the head. Whether a group rotates (Q or K, not V or past F) depends
+  // on its 8-feature block only (head_dim and F are multiples of 8), so it is wave-uniform:
+  // computed from scalar values, it makes a scalar branch.
+  int tq[BI][4];
+  bool rot_g[BI][4];
+#pragma unroll
+  for (int i = 0; i < BI; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t fb = static_cast<uint32_t>(m0) + wm * (32 * BI) + i * 32 + 8 * g;
+      const uint32_t f0 = fb + 4 * lg;
+      rot_g[i][g] = fb < vf0;
+      tq[i][g] = fb < vf0 ? static_cast<int>(((f0 < kf0 ? f0 : f0 - kf0) % hd) / 4) : 0;
+    }
+  // This lane's row in the interleaved table (entry e at row_cs[j][32 e]): block j holds 32
+  // consecutive rows from a multiple of 32; groups past the last row are clamped to it (rows
+  // past the count, and rows without a position, are never stored, so whatever they are
+  // rotated by does not matter).
+  const float4* row_cs[BJ];
 #pragma unroll
   for (int j = 0; j < BJ; ++j) {
-    const int tr = wn * (32 * BJ) + j * 32 + lq;
-    const int64_t n = n0 + tr;
-    const bool rot = a.rope_cs && n < rows && bpos[tr] >= 0;
-    const int sw = 2 * (tr & 15);
-    // This row's cos / sin for every group it rotates, fetched together.
-    float4 cs[BI][4];
+    const int64_t grp = min((n0 + wn * (32 * BJ) + j * 32) / 32, (rows - 1) / 32);
+    row_cs[j] = a.rope_cs ? a.rope_cs + grp * quads * 32 + lq : nullptr;
+  }
+  __syncthreads();  // every wave is done with the last stage
+  // Group (i, g) by group: bias, RoPE, rounding. The table entries of block i + 1 are loaded
+  // while block i is processed (one table round trip per block would otherwise serialise the
+  // epilogue). The fast pass packs without NaN canonicalisation and sums every value into a
+  // probe (NaN if any value is NaN, or +inf meets -inf); a wave whose probe is NaN anywhere
+  // runs the pass again with exact NaN bits (it rewrites the same LDS words).
+  auto phase1 = [&](auto exact_c, auto rope_c) {
+    constexpr bool EXACT = decltype(exact_c)::value;
+    constexpr bool ROPE = decltype(rope_c)::value;
+    float probe = 0.f;
+    constexpr int kAhead = SB_QKV_CS_AHEAD;  // blocks of table entries in flight
+    float4 cs[kAhead + 1][4][BJ];
+    auto load_cs = [&](int i, float4 (&dst)[4][BJ]) {
 #pragma unroll
-    for (int i = 0; i < BI; ++i)
+      for (int g = 0; g < 4; ++g)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t f0 = m0 + wm * (32 * BI) + i * 32 + 8 * g + 4 * lg;
-        cs[i][g] = make_float4(1.f, 0.f, 1.f, 0.f);
-        if (rot && f0 < vf0) {
-          const int64_t rf = f0 - (f0 < kf0 ? 0 : kf0);
-          cs[i][g] = a.rope_cs[n * quads + (rf % a.head_dim) / 4];
-        }
-      }
+        for (int j = 0; j < BJ; ++j) dst[g][j] = row_cs[j][32 * tq[i][g]];
+    };
+    if (ROPE) {
+#pragma unroll
+      for (int i = 0; i < kAhead && i < BI; ++i) load_cs(i, cs[i % (kAhead + 1)]);
+    }
 #pragma unroll
     for (int i = 0; i < BI; ++i) {
+      if (ROPE && i + kAhead < BI) load_cs(i + kAhead, cs[(i + kAhead) % (kAhead + 1)]);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int fl = wm * (32 * BI) + i * 32 + 8 * g + 4 * lg;  // tile feature
         const float4 b = *reinterpret_cast<const float4*>(&bias_s[fl]);
-        float v0 = acc[i][j][4 * g] + b.x, v1 = acc[i][j][4 * g + 1] + b.y;
-        float v2 = acc[i][j][4 * g + 2] + b.z, v3 = acc[i][j][4 * g + 3] + b.w;
-        if (rot) {  // the identity (1, 0) for features that are not rotated
-          const float4 c = cs[i][g];
-          float ev = v0, od = v1;
-          v0 = ev * c.x - od * c.y;
-          v1 = ev * c.y + od * c.x;
-          ev = v2;
-          od = v3;
-          v2 = ev * c.z - od * c.w;
-          v3 = ev * c.w + od * c.z;
+        float v[BJ][4];
+#pragma unroll
+        for (int j = 0; j < BJ; ++j) {
+          v[j][0] = acc[i][j][4 * g] + b.x;
+          v[j][1] = acc[i][j][4 * g + 1] + b.y;
+          v[j][2] = acc[i][j][4 * g + 2] + b.z;
+          v[j][3] = acc[i][j][4 * g + 3] + b.w;
         }
-        uint2 w;
-        w.x = qkv_pack2<DT>(v0, v1);
-        w.y = qkv_pack2<DT>(v2, v3);
-        *reinterpret_cast<uint2*>(smem + tr * TM + 4 * ((fl / 4) ^ sw)) = w;
+        if (ROPE && rot_g[i][g]) {
+#pragma unroll
+          for (int j = 0; j < BJ; ++j) {
+            const float4 c = cs[i % (kAhead + 1)][g][j];
+            float ev = v[j][0], od = v[j][1];
+            v[j][0] = ev * c.x - od * c.y;
+            v[j][1] = ev * c.y + od * c.x;
+            ev = v[j][2];
+            od = v[j][3];
+            v[j][2] = ev * c.z - od * c.w;
+            v[j][3] = ev * c.w + od * c.z;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < BJ; ++j) {
+          const int tr = wn * (32 * BJ) + j * 32 + lq;
+          uint2 w;
+          if (EXACT) {
+            w.x = qkv_pack2<DT>(v[j][0], v[j][1]);
+            w.y = qkv_pack2<DT>(v[j][2], v[j][3]);
+          } else {
+            w.x = qkv_pack2_fast<DT>(v[j][0], v[j][1]);
+            w.y = qkv_pack2_fast<DT>(v[j][2], v[j][3]);
+            probe += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+          }
+          *reinterpret_cast<uint2*>(smem + tr * TM + 4 * ((fl / 4) ^ (2 * (tr & 15)))) = w;
+        }
       }
     }
-  }
+    return probe;
+  };
+  auto run_phase1 = [&](auto exact_c) {
+    if (a.rope_cs) return phase1(exact_c, std::true_type{});
+    return phase1(exact_c, std::false_type{});
+  };
+  const float probe = run_phase1(std::false_type{});
+  if (DT == SB_DTYPE_BF16 && __builtin_amdgcn_ballot_w64(probe != probe) != 0)
+    run_phase1(std::true_type{});
   __syncthreads();
 
   // Phase 2: 16-byte chunks (8 features) of each tile row to their destination, consecutive
   // threads along a row: Q / dense rows and K / V head rows are contiguous, so the stores
   // coalesce. Chunks never straddle a head (head_dim % 8 == 0).
+  // Each thread keeps one chunk column c (kQThreads is a multiple of CPR), so its feature
+  // range, destination (Q / dense, K or V) and head offset are fixed for all its rows.
   constexpr int CPR = TM / 8;  // chunks per tile row
-  for (int k = tid; k < TN * CPR; k += kQThreads) {
-    const int tr = k / CPR, c = k % CPR;
+  static_assert(kQThreads % CPR == 0, "a thread keeps one chunk column");
+  const int c = tid % CPR;
+  const uint32_t f0 = static_cast<uint32_t>(m0) + 8 * c;
+  if (f0 >= static_cast<uint32_t>(a.num_features)) return;
+  int64_t kv_off = 0;  // K / V: plane + head + in-head byte offset of this chunk
+  if (MODE != QKV_DENSE && f0 >= kf0) {
+    const bool is_v = f0 >= vf0;
+    const uint32_t rf = f0 - (is_v ? vf0 : kf0);
+    const uint32_t h = rf / hd;
+    kv_off = (is_v ? a.s_kv : 0) + static_cast<int64_t>(h) * a.s_head + 2 * (rf - h * hd);
+  }
+  for (int tr = tid / CPR; tr < TN; tr += kQThreads / CPR) {
     const int64_t n = n0 + tr;
-    const int64_t f0 = m0 + 8 * c;
-    if (n >= rows || f0 >= a.num_features) continue;
+    if (n >= rows) break;  // rows ascend with tr
     const int p = bpos[tr];
     uint4 w = *reinterpret_cast<const uint4*>(smem + tr * TM + 4 * ((2 * c) ^ (2 * (tr & 15))));
     if (MODE == QKV_DENSE) {
@@ -466,12 +567,7 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
       *reinterpret_cast<uint4*>(a.out + n * a.o_s_row + 2 * f0) = w;
     } else {
       const int64_t slot = kvofs[tr];
-      if (slot < 0) continue;
-      const bool is_v = f0 >= vf0;
-      const int64_t rf = f0 - (is_v ? vf0 : kf0);
-      const int64_t h = rf / a.head_dim;
-      *reinterpret_cast<uint4*>(a.kv + slot + (is_v ? a.s_kv : 0) + h * a.s_head +
-                                2 * (rf - h * a.head_dim)) = w;
+      if (slot >= 0) *reinterpret_cast<uint4*>(a.kv + slot + kv_off) = w;
     }
   }
 }
@@ -479,7 +575,7 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
 // Row gather for a library GEMM, plus the RoPE table in the same launch: threads
 // [0, R * hidden / 8) copy 16-byte chunks of hidden row positions[n] to xg[n] (rows without
 // a valid position are zero); the next R * D / 4 threads fill table entries as
-// qkv_rope_table_kernel does.
+// the row-major qkv_rope_table_kernel does.
 __global__ __launch_bounds__(256) void qkv_gather_kernel(char* xg, const char* hidden,
                                                          int64_t h_s_row, int64_t hidden_dim,
                                                          const int32_t* positions,
@@ -522,22 +618,29 @@ __global__ __launch_bounds__(256) void qkv_gather_kernel(char* xg, const char* h
 template <int DT>
 __global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a, const float* proj,
                                                            int64_t p_s_row) {
-  const int64_t cpr = a.num_features / 8;  // 8-feature chunks per row
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= a.num_rows * cpr) return;
-  const int64_t n = idx / cpr;
-  const int64_t f0 = (idx - n * cpr) * 8;
+  // Index arithmetic in unsigned 32 bits (the host bounds R * F / 8 below 2^31; features,
+  // positions and block sizes fit): 64-bit divisions by run-time values expand to long call
+  // sequences.
+  const uint32_t cpr = static_cast<uint32_t>(a.num_features / 8);  // 8-feature chunks per row
+  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+  if (idx >= static_cast<uint64_t>(a.num_rows) * cpr) return;
+  const uint32_t n32 = idx / cpr;
+  const int64_t n = n32;
+  const uint32_t f0 = (idx - n32 * cpr) * 8;
   const int p = a.positions[n];
   const bool valid = p >= 0 && p < a.seq_len;
-  const int64_t kf0 = a.q_features, vf0 = a.q_features + a.kv_features;
+  const uint32_t kf0 = static_cast<uint32_t>(a.q_features);
+  const uint32_t vf0 = static_cast<uint32_t>(a.q_features + a.kv_features);
+  const uint32_t hd = static_cast<uint32_t>(a.head_dim);
   int64_t slot = -1;
   if (f0 >= kf0) {
     if (!valid) return;
-    const int64_t lb = p / a.block_size;
+    const uint32_t bs = static_cast<uint32_t>(a.block_size);
+    const uint32_t lb = static_cast<uint32_t>(p) / bs;
     if (lb >= a.nb_per_seq) return;
     const int64_t pb = a.block_table[lb];
     if (pb < 0 || pb >= a.nb_total) return;
-    slot = pb * a.s_blk + (p - lb * a.block_size) * a.s_pos;
+    slot = pb * a.s_blk + static_cast<int64_t>(static_cast<uint32_t>(p) - lb * bs) * a.s_pos;
   }
   uint4 w = make_uint4(0u, 0u, 0u, 0u);
   if (valid) {
@@ -558,8 +661,8 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a, const floa
       for (int e = 0; e < 8; ++e) v[e] += qkv_elem<DT>(b[e]);
     }
     if (a.rope_cs && f0 < vf0) {
-      const int64_t rf = f0 - (f0 < kf0 ? 0 : kf0);
-      const int64_t d0 = rf % a.head_dim;  // multiple of 8: two table entries
+      const uint32_t rf = f0 - (f0 < kf0 ? 0 : kf0);
+      const uint32_t d0 = rf % hd;  // multiple of 8: two table entries
       const int quads = a.head_dim / 4;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -582,10 +685,10 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(QkvArgs a, const floa
     *reinterpret_cast<uint4*>(a.out + n * a.o_s_row + 2 * f0) = w;
   } else {
     const bool is_v = f0 >= vf0;
-    const int64_t rf = f0 - (is_v ? vf0 : kf0);
-    const int64_t h = rf / a.head_dim;
-    *reinterpret_cast<uint4*>(a.kv + slot + (is_v ? a.s_kv : 0) + h * a.s_head +
-                              2 * (rf - h * a.head_dim)) = w;
+    const uint32_t rf = f0 - (is_v ? vf0 : kf0);
+    const uint32_t h = rf / hd;
+    *reinterpret_cast<uint4*>(a.kv + slot + (is_v ? a.s_kv : 0) +
+                              static_cast<int64_t>(h) * a.s_head + 2 * (rf - h * hd)) = w;
   }
 }
 
@@ -698,7 +801,7 @@ int launch_qkv(const char* fn, const QkvArgs& a, int32_t dtype, hipStream_t st,
 int launch_qkv_epilogue(const char* fn, const QkvArgs& a, const float* proj, int64_t p_s_row,
                         int32_t dtype, hipStream_t st) {
   const int64_t threads = a.num_rows * (a.num_features / 8);
-  if ((threads + 255) / 256 > 0x7fffffff) return fail(fn, "grid too large");
+  if (threads + 255 >= (int64_t{1} << 31)) return fail(fn, "grid too large");  // 32-bit indices
   const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
   if (dtype == SB_DTYPE_BF16)
     SB_LAUNCH("qkv_epilogue", qkv_epilogue_kernel<SB_DTYPE_BF16>, grid, dim3(256), st, a, proj,
@@ -712,7 +815,9 @@ int launch_qkv_epilogue(const char* fn, const QkvArgs& a, const float* proj, int
 // Workspace of the split form: the RoPE table first, then (split product) the slices.
 constexpr int64_t kQkvWsAlign = 256;
 int64_t qkv_table_bytes(int64_t num_rows, int64_t head_dim, bool rope) {
-  const int64_t t = rope ? num_rows * head_dim * static_cast<int64_t>(sizeof(float)) : 0;
+  // Rows padded to a multiple of 32 (the interleaved layout; the row-major one fits too).
+  const int64_t rows = (num_rows + 31) / 32 * 32;
+  const int64_t t = rope ? rows * head_dim * static_cast<int64_t>(sizeof(float)) : 0;
   return (t + kQkvWsAlign - 1) / kQkvWsAlign * kQkvWsAlign;
 }
 
@@ -773,11 +878,17 @@ extern "C" int sb_qkv_projection_paged(
     if (workspace_bytes < ws_need) return fail(fn, "workspace too small");
   }
   if (inv_freq) {
+    // The fused kernel reads the interleaved layout, the split product's epilogue kernel the
+    // row-major one.
     float4* table = static_cast<float4*>(workspace);
-    const int64_t n = num_rows * (head_dim / 4);
-    SB_LAUNCH("qkv_rope_table", qkv_rope_table_kernel,
-              dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), st, positions, num_rows,
-              seq_len, inv_freq, static_cast<int>(head_dim / 2), table);
+    const int64_t n = (num_rows + 31) / 32 * 32 * (head_dim / 4);
+    const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+    if (pl.splits > 1)
+      SB_LAUNCH("qkv_rope_table", qkv_rope_table_kernel<false>, grid, dim3(256), st, positions,
+                num_rows, seq_len, inv_freq, static_cast<int>(head_dim / 2), table);
+    else
+      SB_LAUNCH("qkv_rope_table", qkv_rope_table_kernel<true>, grid, dim3(256), st, positions,
+                num_rows, seq_len, inv_freq, static_cast<int>(head_dim / 2), table);
     rc = check_launch(fn);
     if (rc) return rc;
     a.rope_cs = table;

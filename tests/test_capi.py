@@ -316,16 +316,16 @@ def test_attention_plan_edge_cases():
 
 
 def test_projection_workspace_covers_the_split_product():
-    """The fused projection's workspace: the RoPE table (rows x head_dim fp32, rounded up to
-    256 bytes), plus, when the row count leaves CUs without a 128 x 128 tile, the fp32 slices
-    of the split hidden dimension (Qwen2.5-7B: 4 slices of 14 k-steps at 64 and 300 rows,
-    none at 2458)."""
+    """The fused projection's workspace: the RoPE table (rows padded to a multiple of 32, x
+    head_dim fp32, rounded up to 256 bytes), plus, when the row count leaves CUs without a
+    128 x 128 tile, the fp32 slices of the split hidden dimension (Qwen2.5-7B: 4 slices of
+    14 k-steps at 64 and 300 rows, none at 2458)."""
     lib = _lib.lib()
     f = (28 + 2 * 4) * 128
     size = lib.sb_qkv_projection_paged_workspace_size
     assert size(64, 28, 4, 128, 3584, 1) == 64 * 128 * 4 + 4 * 64 * f * 4
     assert size(64, 28, 4, 128, 3584, 0) == 4 * 64 * f * 4
-    assert size(300, 28, 4, 128, 3584, 1) == 300 * 128 * 4 + 4 * 300 * f * 4
-    assert size(2458, 28, 4, 128, 3584, 1) == 2458 * 128 * 4
+    assert size(300, 28, 4, 128, 3584, 1) == 320 * 128 * 4 + 4 * 300 * f * 4
+    assert size(2458, 28, 4, 128, 3584, 1) == 2464 * 128 * 4
     assert size(2458, 28, 4, 128, 3584, 0) == 0
     assert size(0, 28, 4, 128, 3584, 1) == 0
