@@ -530,7 +530,7 @@ __global__ __launch_bounds__(kQThreads, BI * BJ > 4 ? 1 : 2) void qkv_mfma_kerne
     return probe;
   };
   auto run_phase1 = [&](auto exact_c) {
-    if (a.rope_cs) return phase1(exact_c, std::true_type{});
+    if (MODE != QKV_DENSE && a.rope_cs) return phase1(exact_c, std::true_type{});
     return phase1(exact_c, std::false_type{});
   };
   const float probe = run_phase1(std::false_type{});

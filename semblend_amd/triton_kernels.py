@@ -262,9 +262,9 @@ def masked_qkv_projection(
 
 
 
-# Row counts up to which qkv_projection_paged(backend="auto") takes the fused kernel (measured
-# at the Qwen2.5-7B shape: faster or level with the library GEMM there, slower above).
-_FUSED_PROJECTION_MAX_ROWS = 512
+# Row counts in which qkv_projection_paged(backend="auto") takes the library GEMM (measured at
+# the Qwen2.5-7B shape: the fused kernel is faster or level below and above this range).
+_LIBRARY_PROJECTION_ROWS = (513, 1024)
 
 
 def qkv_projection_paged(
@@ -294,11 +294,11 @@ def qkv_projection_paged(
     Q and K/V from its epilogue; "library" gathers the rows, multiplies them with the
     library GEMM (hipBLASLt through torch, fp32 output) and runs the same epilogue as a
     kernel of its own (bias, RoPE, one rounding, Q and the paged K/V write); "auto" takes the
-    fused form up to 512 rows (where it splits the hidden dimension when the row tiles are
-    too few for the CUs) and the library form above. Qwen2.5-7B shape, graph replays on one
-    MI355X, fused / library: 29 / 28 us at 64 rows, 30.5 / 33 at 128, 35.5 / 46 at 256, 43 /
-    43 at 512, 52 / 50 at 768, 61 / 58 at 1024, 97 / 88 at 2048, 99 / 100 at 2458, 171 / 164
-    at 4096. The fused form needs no fp32 intermediate of rows x features. Both accumulate in
+    library form from 513 to 1024 rows and the fused form otherwise (which splits the hidden
+    dimension when its row tiles are too few for the CUs). Qwen2.5-7B shape, graph replays on
+    one MI355X, fused / library: 28.5 / 28 us at 64 rows, 36.5 / 46 at 256, 42.5 / 43.5 at
+    512, 52 / 48 at 768, 57 / 56.5 at 1024, 83 / 86.5 at 2048, 89 / 98 at 2458, 158 / 165 at
+    4096. The fused form needs no fp32 intermediate of rows x features. Both accumulate in
     fp32 and round once.
     Fuses the masked projection (semblend_core/triton_kernels.py:451-522) with the K/V write
     of partial_prefill (:904-909), compacted and paged; no reference counterpart.
@@ -337,7 +337,8 @@ def qkv_projection_paged(
     bias = None if qkv_bias is None else qkv_bias.contiguous()
     inv = inv_freq_table(rope_base, head_dim, dev) if rope_base is not None else None
     if backend == "auto":
-        backend = "fused" if n <= _FUSED_PROJECTION_MAX_ROWS else "library"
+        lo, hi = _LIBRARY_PROJECTION_ROWS
+        backend = "library" if lo <= n <= hi else "fused"
     if backend == "library":
         # rows outside the hidden states are gathered as zeros; the epilogue zeroes their Q
         # and writes no K/V for them

@@ -28,10 +28,25 @@ def _absdot(x, w):
 def _assert_proj_close(got, want, absdot, what=""):
     got, want = got.cpu(), want.cpu()
     assert got.shape == want.shape and got.dtype == want.dtype
+    # Non-finite outputs (from non-finite inputs): the oracle's infinity bit for bit, and NaN
+    # where it has NaN. NaN bits are not compared with the oracle: torch's CPU rounding writes
+    # 0xFFFF from its vectorised path and 0x7FC0 from its scalar one. The library writes 0x7FC0
+    # in bf16 from every path (fp16 keeps the NaN's sign).
+    nonfinite = ~torch.isfinite(want.float())
+    if nonfinite.any():
+        w_nan = torch.isnan(want.float())
+        w_inf = nonfinite & ~w_nan
+        n_diff = int((got[w_inf].view(torch.int16) != want[w_inf].view(torch.int16)).sum())
+        g_nan = got[w_nan]
+        n_diff += int((~torch.isnan(g_nan.float())).sum())
+        if got.dtype == torch.bfloat16:
+            n_diff += int((g_nan.view(torch.int16) != 0x7FC0).sum())
+        assert n_diff == 0, f"{what}: {n_diff} non-finite outputs differ"
     diff = (got.float() - want.float()).abs()
     mag = torch.maximum(got.float().abs(), want.float().abs())
     allowed = _ulp16(mag, got.dtype) + ACC_TOL * absdot
-    bad = diff > allowed
+    bad = (diff > allowed) & ~nonfinite
+    bad |= ~torch.isfinite(got.float()) & ~nonfinite
     n_bad = int(bad.sum())
     if n_bad:
         i = bad.nonzero()[0].tolist()
@@ -107,6 +122,22 @@ def test_projection_paged_qwen05b_shape(dev, dtype, rope_base, backend):
     x, w, b, pos, bt, cache = _case(300, 896, 14, 2, 64, 77, dtype, 10)
     pos = torch.cat([pos, torch.tensor([-1, 300], dtype=torch.int32)])  # zero Q, no K/V
     _check_paged(dev, x, w, b, pos, bt, cache, 14, 2, 64, rope_base, backend)
+
+
+@pytest.mark.parametrize("backend", BACKENDS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_projection_paged_nonfinite_rows(dev, dtype, backend):
+    """Hidden rows holding a NaN, an infinity, or both infinities: every output of such a row
+    is non-finite and must match the oracle's (the same infinity, or NaN: in bf16 the
+    library's one NaN 0x7FC0); the other rows keep the usual bar. In the fused kernel the row
+    tiles that hold these rows take the exact second packing pass."""
+    x, w, b, pos, bt, cache = _case(300, 896, 14, 2, 64, 77, dtype, 50)
+    x[pos[3], 5] = float("nan")
+    x[pos[10], 7] = float("inf")
+    x[pos[20], 0] = float("-inf")
+    x[pos[20], 1] = float("inf")
+    x[pos[40], 9] = float("-inf")
+    _check_paged(dev, x, w, b, pos, bt, cache, 14, 2, 64, 1e6, backend)
 
 
 @pytest.mark.parametrize("backend", BACKENDS)
