@@ -894,10 +894,15 @@ attn_mfma_kernel(const AttnBatch batch) {
       if (it + 2 < ntiles) load_k(slot2, par);
       if (it + 1 < ntiles) load_v(slot1, par ^ 1);
     }
-    // Offsets of tile it+3: kTileKeys / kWaves entries from each wave.
+    // Offsets of tile it+3: kTileKeys / kWaves entries from each wave, or (one-wave form) all
+    // of them from one of waves 0-3 in turn. Waves w and w + 4 share a SIMD, and the older
+    // one (w) wins the issue ties and then waits at the tile barrier for the other, so extra
+    // work belongs on waves 0-3 (7B 16K: 271.3 -> 268.7 us against rotating over all eight;
+    // moving the tile loads there as well was slower, 273.8 us).
 #if SB_ATTN_FILL_ONE_WAVE
     static_assert(kTileKeys == 64, "one entry per lane");
-    if (it + 3 < ntiles && wave == (it & (kWaves - 1))) fill_offsets(slot, t0 + 3 * kTileKeys, lane);
+    if (it + 3 < ntiles && wave == (it & (kWaves / 2 - 1)))
+      fill_offsets(slot, t0 + 3 * kTileKeys, lane);
 #else
     if (it + 3 < ntiles && lane < kTileKeys / kWaves)
       fill_offsets(slot, t0 + 3 * kTileKeys, wave * (kTileKeys / kWaves) + lane);
