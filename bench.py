@@ -66,11 +66,11 @@ KERNELS = ("attn_mfma", "attn_merge", "move_rows", "rope_rows", "rope_index", "f
 # (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0); kernel changes call for a new measurement. Attention:
 # the planned launch that the step times.
 MEASURED_TRAFFIC_BYTES = {
-    "attn_mfma": (2 * 92927 + 63581) * 1024,
-    "move_rows": (2 * 391149 + 779859) * 1024,
+    "attn_mfma": (2 * 92677 + 63581) * 1024,
+    "move_rows": (2 * 391155 + 779861) * 1024,
     "rope_rows": (2 * 114793 + 229376) * 1024,
 }
-MEASURED_TRAFFIC_SOURCE = ("rocprofv3 FETCH_SIZE / WRITE_SIZE passes at commit c422a9a, "
+MEASURED_TRAFFIC_SOURCE = ("rocprofv3 FETCH_SIZE / WRITE_SIZE passes at commit 0817005, "
                            "profiles/kv_reuse_7b_16k_hbm_traffic.md")
 
 
