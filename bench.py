@@ -743,6 +743,16 @@ def projection_section(dev: torch.device, inp, steps: int) -> dict:
                                        HKV, D, qkv_bias=b, rope_base=ROPE_BASE)
 
     ms_layer = timed(layer, False)
+    # the same layer with the request's attention plan, made once (as for every layer of it)
+    layer_plan = tk.plan_partial_attention_paged(inp["pos_cpu"], HQ, HKV, D, BS,
+                                                 inp["block_table"].shape[0], torch.bfloat16,
+                                                 dev)
+
+    def layer_planned():
+        tk.partial_prefill_layer_paged(x, w, wo, pos, inp["attn_kv"], inp["block_table"], HQ,
+                                       HKV, D, qkv_bias=b, rope_base=ROPE_BASE, plan=layer_plan)
+
+    ms_layer_planned = timed(layer_planned, False)
     return {
         "rows": rows, "hidden": hidden, "features": feats, "flops": flops,
         "fused": {"ms": round(ms_fused, 4), "tflops": round(flops / (ms_fused * 1e-3) / 1e12, 1)},
@@ -757,8 +767,10 @@ def projection_section(dev: torch.device, inp, steps: int) -> dict:
                                "tflops": round(flops / (ms_lib * 1e-3) / 1e12, 1),
                                "what": "x[pos] @ W^T + b via torch (hipBLASLt), no RoPE, no K/V write"},
         "layer": {"ms": round(ms_layer, 4),
+                  "planned_ms": round(ms_layer_planned, 4),
                   "what": "partial_prefill_layer_paged: projection + K/V write + RoPE, paged "
-                          "GQA attention, output projection (3584 x 3584) of the 2458 rows"},
+                          "GQA attention, output projection (3584 x 3584) of the 2458 rows; "
+                          "planned_ms with the request's attention plan"},
     }
 
 

@@ -670,6 +670,7 @@ def partial_prefill_layer_paged(
     output_bias: torch.Tensor | None = None,
     rope_base: float | None = None,
     scale: float | None = None,
+    plan: PagedAttentionPlan | None = None,
 ) -> PagedLayerResult:
     """One attention layer of partial prefill, on the paged cache of that layer.
 
@@ -681,14 +682,16 @@ def partial_prefill_layer_paged(
     slots already hold the scattered, RoPE-corrected donor K/V; (2) GQA attention of those
     rows over the cache (``partial_prefill_attention_paged``); (3) the output projection of
     the attention rows (torch's GEMM, fp32 accumulation, rounded to the input dtype). A model
-    runs this once per layer with that layer's weights and cache.
+    runs this once per layer with that layer's weights and cache; ``plan`` (from
+    :func:`plan_partial_attention_paged` for these positions, made once per request) serves
+    every layer's attention.
     """
     dev = _lib.require_device(hidden_states, qkv_weight, output_projection, kv_cache)
     q = qkv_projection_paged(hidden_states, qkv_weight, compute_positions, kv_cache,
                              block_table, num_heads, num_kv_heads, head_dim, qkv_bias=qkv_bias,
                              rope_base=rope_base)
     pos = _lib.as_index(compute_positions, dev)
-    attn = partial_prefill_attention_paged(q, kv_cache, block_table, pos, scale=scale)
+    attn = partial_prefill_attention_paged(q, kv_cache, block_table, pos, scale=scale, plan=plan)
     flat = attn.reshape(attn.shape[0], num_heads * head_dim)
     out = torch.nn.functional.linear(flat, output_projection, output_bias)
     return PagedLayerResult(output=out, query=q, attention=attn)

@@ -235,7 +235,7 @@ def test_partial_prefill_layers_paged(dev):
     shape, bias, RoPE theta 1e6), each stage against the oracle: the projection to its bar,
     the attention over the oracle-written cache to the attention bar (2e-2), and the output
     projection within 2e-2 * sum_k |Wo[j, k]| + 1 ulp (the attention bar carried through the
-    linear map)."""
+    linear map). The second layer runs its attention with the request's host plan."""
     hq, hkv, d, hidden, seq = 14, 2, 64, 896, 400
     x = randn((seq, hidden), torch.bfloat16, 60)
     pos = torch.randperm(seq, generator=gen(61))[:90].sort().values.to(torch.int32)
@@ -251,9 +251,11 @@ def test_partial_prefill_layers_paged(dev):
         bo = randn((hidden,), torch.bfloat16, s0 + 3)
         cache = randn((nbs + 3, 2, hkv, 16, d), torch.bfloat16, s0 + 4)  # donor K/V stand-in
         kv_dev = cache.to(dev)
+        plan = (tk.plan_partial_attention_paged(pos, hq, hkv, d, 16, bt.shape[0],
+                                                torch.bfloat16, dev) if layer == 1 else None)
         res = tk.partial_prefill_layer_paged(
             x.to(dev), w.to(dev), wo.to(dev), pos.to(dev), kv_dev, bt.to(dev), hq, hkv, d,
-            qkv_bias=b.to(dev), output_bias=bo.to(dev), rope_base=1e6)
+            qkv_bias=b.to(dev), output_bias=bo.to(dev), rope_base=1e6, plan=plan)
         want_kv = cache.clone()
         want_q = ref.qkv_project_paged(x, w, pos, want_kv, bt, hq, hkv, d, qkv_bias=b,
                                        rope_base=1e6)
